@@ -1,0 +1,137 @@
+/* libqwen_gpu.so: MI355X (gfx950) implementation of the routed-MoE subset of
+ * the reference's GPU C ABI.  Names, argument lists, return conventions and
+ * semantics follow /root/reference/qwen/gpu.h, so the reference's ctypes
+ * caller (test_gpu.py:12-36) and host engine (qwen.c) bind unchanged.
+ *
+ * Conventions (gpu.h:4-10, gpu.cu:38-46,181-189):
+ *  - device arrays are token-major; the caller owns every device buffer;
+ *  - int returns are runtime error codes (hipError_t here, cudaError_t in the
+ *    reference), 0 = success, text from qg_error(); argument errors return
+ *    the "invalid value" code;
+ *  - operator wrappers are asynchronous on the calling thread's stream and
+ *    return the launch status; qg_write/qg_read are synchronous;
+ *  - between qg_graph_begin and qg_graph_end the calling thread's launches
+ *    are captured (per-thread capture stream, gpu.cu:10,21-34).
+ * Entry points whose reference signature carries no width (gather, scatter,
+ * reduce, mtp_moe, shared_add) use the hidden/FFN widths set by
+ * qg_moe_configure (default 2560/640, the reference's hard-coded shapes,
+ * gpu.cu:508-553). */
+#ifndef NEBULA_QWEN_GPU_H
+#define NEBULA_QWEN_GPU_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime (gpu.h:11-21,24,30-36; gpu.cu:13-85,114-120) ---- */
+void *qg_alloc(size_t bytes);                                   /* gpu.h:11, NULL on failure */
+void qg_free(void *p);                                          /* gpu.h:12 */
+int qg_write(void *dst, const void *src, size_t bytes);         /* gpu.h:13, synchronous H2D */
+int qg_read(void *dst, const void *src, size_t bytes);          /* gpu.h:14, synchronous D2H */
+int qg_copy(void *dst, const void *src, size_t bytes);          /* gpu.h:15, async D2D */
+int qg_zero(void *dst, size_t bytes);                           /* gpu.h:16, async fill */
+int qg_sync(void);                                              /* gpu.h:17 */
+int qg_graph_begin(void **graph);                               /* gpu.h:18 */
+int qg_graph_end(void *graph);                                  /* gpu.h:19 */
+int qg_graph_launch(void *graph);                               /* gpu.h:20 */
+void qg_graph_destroy(void *graph);                             /* gpu.h:21 */
+int qg_memory(size_t *free_bytes, size_t *total_bytes);         /* gpu.h:24 */
+const char *qg_error(int error);                                /* gpu.h:30 */
+int qg_tensor_bytes(int type, const uint64_t dims[4], uint64_t *bytes); /* gpu.h:31 */
+void *qg_upload_create(size_t expert_bytes);                    /* gpu.h:32 */
+void qg_upload_destroy(void *uploader);                         /* gpu.h:33 */
+int qg_upload_expert(void *uploader, void *dst, const void *gate, size_t gate_bytes,
+                     const void *up, size_t up_bytes, const void *down, size_t down_bytes); /* gpu.h:34-35 */
+double qg_upload_seconds(void *uploader);                       /* gpu.h:36 */
+
+/* ---- operators on the MoE path (gpu.h:37-43,62-78) ---- */
+/* out[t,r] = sum_c deq(W)[r,c] x[t,c]; types 0,1,30,2,6,7,8,12,13,14,20;
+ * tokens 1..8192; the reference's fixed summation order (gpu.cu:154-189,
+ * cpu.c:119-148), so results equal cpu.c's qc_matmul bit for bit. */
+int qg_matmul(float *out, const void *w, int type, int rows, int cols, const float *x, int tokens); /* gpu.h:37-38 */
+int qg_gather(float *out, const void *w, int type, int cols, int row);          /* gpu.h:39 */
+int qg_norm(float *out, const float *x, const float *weight, int width,
+            int groups, int tokens, int weight_groups, int l2, float eps);      /* gpu.h:40-41 */
+int qg_unary(float *out, const float *x, int count, int op, float scale);      /* gpu.h:42 */
+int qg_binary(float *out, const float *a, const float *b, int count, int op);  /* gpu.h:43 */
+int qg_route(int *ids, float *weights, const float *logits, int tokens);        /* gpu.h:62 */
+typedef struct {
+    uint64_t token_layers, missing_selections, skipped_selections, avoided_token_handoffs;
+    double skipped_mass;
+} qg_prune_stats;                                                               /* gpu.h:63-66 */
+int qg_prune_routes(int *ids, float *weights, const unsigned char *resident,
+                    int tokens, double threshold, qg_prune_stats *stats);       /* gpu.h:67-68 */
+int qg_moe_map(int *map, const int *ids, int tokens);                          /* gpu.h:69 */
+int qg_moe_gather(float *out, const float *x, const int *token_map, int selected_tokens);   /* gpu.h:70 */
+int qg_moe_scatter(float *slots, const float *expert, const float *weights, const int *ids,
+                   const int *token_map, int expert_id, int selected_tokens);  /* gpu.h:71-72 */
+int qg_moe_reduce(float *out, const float *slots, int tokens);                 /* gpu.h:73 */
+int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const float *weights,
+               const void *gate, int gate_type, const void *up, int up_type,
+               const void *down, int down_type, int tokens);                    /* gpu.h:74-76 */
+int qg_dequant(float *out, const void *packed, int type, int rows, int cols);  /* gpu.h:77 */
+int qg_shared_add(float *out, const float *shared, const float *gate, int tokens); /* gpu.h:78 */
+
+/* ---- additions (no reference counterpart; the reference hard-codes the
+ * shapes and drives the layer from the host, qwen.c:633-735) ---- */
+
+/* Hidden width D and expert FFN width F used by the width-less entry points
+ * above.  D multiple of 256, F multiple of 32, D <= 8192, F <= 4096. */
+int qg_moe_configure(int width, int ff);
+
+/* Dispatch of routing ids into per-expert contiguous row lists (CSR), the
+ * device-side histogram/prefix-sum/permutation replacing qg_moe_map's
+ * [512, tokens] map and the host count loop of qwen.c:650-655.  offsets[513];
+ * entries offsets[e]..offsets[e+1]-1 list (ascending token) the selections of
+ * expert e: row_token = t, row_slot = t*10+k.  Ids in [-513,-2] (pruned) are
+ * skipped; any other id outside [0,512) makes *status nonzero. */
+int qg_moe_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int tokens);
+
+/* One routed-MoE layer, device-driven (no host read of routing ids), so it
+ * can be captured into a graph: router -> top-10 -> [coverage/prune] ->
+ * dispatch -> gate/up + SwiGLU -> down + router-rank combine -> shared expert.
+ * Replaces moe()/grouped_moe()/shared_direct() of qwen.c:633-735 for one
+ * layer.  Arithmetic: router logits in the reference's fixed order (ids
+ * bit-exact); expert products in fp32 from exactly dequantised weights. */
+typedef struct {
+    int width, ff;                              /* D, F */
+    const float *router;                        /* F32 [512, D] (ffn_gate_inp) */
+    const void *gate, *up, *down;               /* [512][F][row(D)], [512][F][row(D)], [512][D][row(F)] */
+    int gate_type, up_type, down_type;
+    const void *sh_gate, *sh_up, *sh_down;      /* shared expert or NULL (ffn_*_shexp) */
+    int sh_gate_type, sh_up_type, sh_down_type;
+    const float *sh_gate_inp;                   /* F32 [1, D] (ffn_gate_inp_shexp) */
+    const unsigned char *resident;              /* 512-byte device mask or NULL */
+    double threshold;                           /* omitted-mass threshold (0.10, config.py:9) */
+} qg_moe_layer;
+
+/* Device workspace bytes for qg_moe_forward at up to `tokens` tokens. */
+size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
+
+/* out [tokens, D]; ids/weights [tokens, 10] (after pruning); flags [tokens]
+ * or NULL: 0 all selections resident, 1 pruned (omitted mass < threshold),
+ * 2 handoff (coverage below 1-threshold), 3 invalid router distribution;
+ * stats may be NULL.  With flags==2 the token's output row is not computed
+ * here (it belongs to the host handoff, qwen.c:658-678) and is written as 0.
+ * tokens 1..17. */
+int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
+                   const float *x, int tokens, const qg_moe_layer *layer, void *workspace, size_t workspace_bytes);
+
+/* Timing helpers for the benchmark (events on the calling thread's stream). */
+void *qg_event_create(void);
+void qg_event_destroy(void *event);
+int qg_event_record(void *event);
+int qg_event_elapsed(float *ms, void *begin, void *end);
+int qg_device_info(char *name, size_t name_len, int *cus, int *clock_khz, int *mem_clock_khz, int *bus_bits);
+
+/* Synthetic inputs generated on the device (benchmark/test support; not a
+ * reference interface).  Value (r,c) of tensor `stream` under `seed` is
+ * sigma*N(0,1) from a counter-based hash; encoded to type 0/12/20.  The
+ * bytes equal the CPU generator's in oracle/nb_synth.c. */
+int qg_synth_matrix(void *out, int type, uint64_t seed, uint64_t stream, int rows, int cols, float sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,111 @@
+/* Host C driver of stacked routed-MoE layers (declarations and contract in
+ * include/nebula_moe.h).  Calls only the qg_* C ABI of libqwen_gpu.so. */
+#include "nebula_moe.h"
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { NM_MAX_TOKENS = 17, NM_TOP = 10 };
+
+static _Thread_local char nm_error[256];
+static int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(nm_error, sizeof nm_error, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+const char *nm_last_error(void) { return nm_error; }
+
+struct nm_stack {
+    int n_layers, max_tokens, width, record;
+    qg_moe_layer *layers;
+    float *h, *xn, *out, *w;
+    int *ids;
+    void *ws;
+    size_t ws_bytes;
+    float *rec_x, *rec_out, *rec_w;
+    int *rec_ids;
+    void *graphs[NM_MAX_TOKENS + 1];
+};
+
+void nm_stack_destroy(nm_stack *s) {
+    if (!s) return;
+    for (int i = 0; i <= NM_MAX_TOKENS; i++) if (s->graphs[i]) qg_graph_destroy(s->graphs[i]);
+    qg_free(s->h); qg_free(s->xn); qg_free(s->out); qg_free(s->w); qg_free(s->ids); qg_free(s->ws);
+    qg_free(s->rec_x); qg_free(s->rec_out); qg_free(s->rec_w); qg_free(s->rec_ids);
+    free(s->layers);
+    free(s);
+}
+
+nm_stack *nm_stack_create(const qg_moe_layer *layers, int n_layers, int max_tokens, int record) {
+    if (!layers || n_layers < 1 || max_tokens < 1 || max_tokens > NM_MAX_TOKENS) { fail("invalid stack arguments"); return NULL; }
+    const int D = layers[0].width;
+    for (int l = 1; l < n_layers; l++)
+        if (layers[l].width != D || layers[l].ff != layers[0].ff) { fail("layer %d shape differs from layer 0", l); return NULL; }
+    nm_stack *s = calloc(1, sizeof *s);
+    if (!s) { fail("host allocation"); return NULL; }
+    s->n_layers = n_layers; s->max_tokens = max_tokens; s->width = D; s->record = record;
+    s->layers = malloc(sizeof(qg_moe_layer) * (size_t)n_layers);
+    s->ws_bytes = qg_moe_workspace_bytes(D, layers[0].ff, max_tokens);
+    const size_t act = (size_t)max_tokens * D * sizeof(float), sel = (size_t)max_tokens * NM_TOP * 4;
+    if (!s->layers || !s->ws_bytes) { fail("invalid layer shape"); nm_stack_destroy(s); return NULL; }
+    memcpy(s->layers, layers, sizeof(qg_moe_layer) * (size_t)n_layers);
+    s->h = qg_alloc(act); s->xn = qg_alloc(act); s->out = qg_alloc(act);
+    s->w = qg_alloc(sel); s->ids = qg_alloc(sel); s->ws = qg_alloc(s->ws_bytes);
+    if (!s->h || !s->xn || !s->out || !s->w || !s->ids || !s->ws) { fail("device allocation"); nm_stack_destroy(s); return NULL; }
+    if (record) {
+        s->rec_x = qg_alloc(act * n_layers); s->rec_out = qg_alloc(act * n_layers);
+        s->rec_w = qg_alloc(sel * n_layers); s->rec_ids = qg_alloc(sel * n_layers);
+        if (!s->rec_x || !s->rec_out || !s->rec_w || !s->rec_ids) { fail("device allocation (record)"); nm_stack_destroy(s); return NULL; }
+    }
+    if (qg_zero(s->h, act) || qg_sync()) { fail("initialise hidden state"); nm_stack_destroy(s); return NULL; }
+    return s;
+}
+
+float *nm_stack_hidden(nm_stack *s) { return s ? s->h : NULL; }
+
+#define GPU(call) do { int rc_ = (call); if (rc_) return fail("%s: %s", #call, qg_error(rc_)); } while (0)
+
+static int run_layers(nm_stack *s, int nt) {
+    const int D = s->width;
+    const size_t act = (size_t)nt * D * sizeof(float), sel = (size_t)nt * NM_TOP * 4;
+    const size_t act_stride = (size_t)s->max_tokens * D * sizeof(float), sel_stride = (size_t)s->max_tokens * NM_TOP * 4;
+    for (int l = 0; l < s->n_layers; l++) {
+        GPU(qg_norm(s->xn, s->h, NULL, D, 1, nt, 0, 0, 1e-6f));
+        GPU(qg_moe_forward(s->out, s->ids, s->w, NULL, NULL, s->xn, nt, &s->layers[l], s->ws, s->ws_bytes));
+        if (s->record) {
+            GPU(qg_copy((char *)s->rec_x + act_stride * l, s->xn, act));
+            GPU(qg_copy((char *)s->rec_out + act_stride * l, s->out, act));
+            GPU(qg_copy((char *)s->rec_ids + sel_stride * l, s->ids, sel));
+            GPU(qg_copy((char *)s->rec_w + sel_stride * l, s->w, sel));
+        }
+        GPU(qg_binary(s->h, s->h, s->out, nt * D, 0));
+    }
+    return 0;
+}
+
+int nm_stack_forward(nm_stack *s, int nt, int use_graph) {
+    if (!s || nt < 1 || nt > s->max_tokens) return fail("invalid token count");
+    if (!use_graph) return run_layers(s, nt);
+    void **g = &s->graphs[nt];
+    if (!*g) {
+        GPU(qg_graph_begin(g));
+        if (run_layers(s, nt)) { qg_graph_destroy(*g); *g = NULL; return -1; }
+        int end = qg_graph_end(*g);
+        if (end) { qg_graph_destroy(*g); *g = NULL; return fail("capture MoE stack: %s", qg_error(end)); }
+    }
+    GPU(qg_graph_launch(*g));
+    return 0;
+}
+
+int nm_stack_record(nm_stack *s, int layer, const float **x, const int **ids, const float **weights, const float **out) {
+    if (!s || !s->record || layer < 0 || layer >= s->n_layers) return fail("no record for this layer");
+    const size_t a = (size_t)s->max_tokens * s->width, b = (size_t)s->max_tokens * NM_TOP;
+    if (x) *x = s->rec_x + a * layer;
+    if (out) *out = s->rec_out + a * layer;
+    if (ids) *ids = s->rec_ids + b * layer;
+    if (weights) *weights = s->rec_w + b * layer;
+    return 0;
+}

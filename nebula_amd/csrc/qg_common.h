@@ -1,0 +1,129 @@
+// Device-side helpers shared by the HIP translation units of libqwen_gpu.so.
+// CDNA4 (gfx950) only: 64-lane wavefronts, DPP/ds_swizzle cross-lane ops.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#define QG_DEV static __device__ __forceinline__
+
+enum { QG_EXPERTS = 512, QG_TOP = 10, QG_MAX_DECODE = 17, QG_MAX_TOKENS = 8192 };
+
+// GGML type ids on the path (cpu.c:17-30): 0 F32, 12 Q4_K, 20 IQ4_NL; the
+// generic path also handles 1 F16, 30 BF16, 2 Q4_0, 6 Q5_0, 7 Q4_1, 8 Q8_0,
+// 13 Q5_K, 14 Q6_K.
+enum { QT_F32 = 0, QT_F16 = 1, QT_Q4_0 = 2, QT_Q5_0 = 6, QT_Q4_1 = 7, QT_Q8_0 = 8,
+       QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_BF16 = 30 };
+
+static inline size_t qg_row_bytes_host(int type, int cols) {  // cpu.c:17-30 / gpu.cu:105-113
+    if (cols < 1) return 0;
+    switch (type) {
+    case QT_F32: return (size_t)cols * 4;
+    case QT_F16: case QT_BF16: return (size_t)cols * 2;
+    case QT_Q4_0: case QT_IQ4_NL: return cols % 32 ? 0 : (size_t)cols / 32 * 18;
+    case QT_Q5_0: return cols % 32 ? 0 : (size_t)cols / 32 * 22;
+    case QT_Q4_1: return cols % 32 ? 0 : (size_t)cols / 32 * 24;
+    case QT_Q8_0: return cols % 32 ? 0 : (size_t)cols / 32 * 34;
+    case QT_Q4_K: return cols % 256 ? 0 : (size_t)cols / 256 * 144;
+    case QT_Q5_K: return cols % 256 ? 0 : (size_t)cols / 256 * 176;
+    case QT_Q6_K: return cols % 256 ? 0 : (size_t)cols / 256 * 210;
+    default: return 0;
+    }
+}
+
+// fp16 bits -> float, exact for every encoding (cpu.c:31-42 semantics).
+QG_DEV float qg_half(const uint8_t *p) {
+    uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+QG_DEV float qg_half_u16(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+__constant__ static const int8_t qg_iq4nl_lut[16] = {-127,-104,-83,-65,-49,-35,-22,-10,1,13,25,38,53,69,89,113};
+
+// One dequantised weight, element i of a row (cpu.c:43-67, gpu.cu:121-153).
+// Q4_K/Q5_K use fma(d*s, q, -(dmin*m)) as cpu.c:66 does.
+QG_DEV float qg_weight_at(const uint8_t *row, int type, int i) {
+    if (type == QT_F32) return ((const float *)row)[i];
+    if (type == QT_F16) return qg_half(row + 2 * i);
+    if (type == QT_BF16) return __uint_as_float((uint32_t)((const uint16_t *)row)[i] << 16);
+    if (type == QT_Q8_0) { const uint8_t *p = row + (size_t)(i / 32) * 34; return qg_half(p) * (float)(int8_t)p[2 + i % 32]; }
+    if (type == QT_Q4_0 || type == QT_IQ4_NL || type == QT_Q5_0 || type == QT_Q4_1) {
+        int bytes = type == QT_Q4_1 ? 24 : type == QT_Q5_0 ? 22 : 18, j = i % 32, off = type == QT_Q4_1 ? 8 : type == QT_Q5_0 ? 6 : 2;
+        const uint8_t *p = row + (size_t)(i / 32) * bytes;
+        int q = (p[off + j % 16] >> ((j / 16) * 4)) & 15;
+        if (type == QT_Q5_0 || type == QT_Q4_1) {
+            const uint8_t *hp = p + (type == QT_Q4_1 ? 4 : 2);
+            uint32_t high = (uint32_t)hp[0] | ((uint32_t)hp[1] << 8) | ((uint32_t)hp[2] << 16) | ((uint32_t)hp[3] << 24);
+            q |= ((high >> j) & 1) << 4;
+        }
+        if (type == QT_IQ4_NL) return qg_half(p) * (float)qg_iq4nl_lut[q];
+        return type == QT_Q4_1 ? __builtin_fmaf(qg_half(p), (float)q, qg_half(p + 2))
+                               : qg_half(p) * (float)(q - (type == QT_Q4_0 ? 8 : type == QT_Q5_0 ? 16 : 0));
+    }
+    int k = i % 256, g = k / 32, l = k % 32;
+    const uint8_t *p = row + (size_t)(i / 256) * (type == QT_Q4_K ? 144 : type == QT_Q5_K ? 176 : 210);
+    if (type == QT_Q6_K) {
+        int h = k / 128, s = (k % 128) / 32;
+        int lo = (p[h * 64 + (s % 2) * 32 + l] >> ((s / 2) * 4)) & 15, hi = (p[128 + h * 32 + l] >> (s * 2)) & 3;
+        return qg_half(p + 208) * (float)(int8_t)p[192 + h * 8 + s * 2 + l / 16] * (float)((lo | (hi << 4)) - 32);
+    }
+    const uint8_t *sc = p + 4;
+    int s = g < 4 ? (sc[g] & 63) : ((sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4));
+    int m = g < 4 ? (sc[g + 4] & 63) : ((sc[g + 4] >> 4) | ((sc[g] >> 6) << 4));
+    int q = (p[(type == QT_Q4_K ? 16 : 48) + (g / 2) * 32 + l] >> ((g % 2) * 4)) & 15;
+    if (type == QT_Q5_K) q |= ((p[16 + l] >> g) & 1) << 4;
+    return __builtin_fmaf(qg_half(p) * (float)s, (float)q, -(qg_half(p + 2) * (float)m));
+}
+
+// exp(x) evaluated in double and rounded once to float.  Cody-Waite
+// reduction by ln 2 (fdlibm's hi/lo split) and a degree-17 Taylor polynomial
+// on |r| <= ln2/2, Horner with fused multiply-adds, exact 2^k scaling.  The
+// same statement runs on the host in the test oracle, so routing weights are
+// bit-identical on both sides.
+QG_DEV double qg_exp_d(double x) {
+    if (x != x) return x;
+    if (x > 709.782712893384) return __builtin_inf();
+    if (x < -745.1332191019412) return 0.0;
+    const double ln2_hi = 6.93147180369123816490e-01, ln2_lo = 1.90821492927058770002e-10;
+    double kd = __builtin_rint(x * 1.44269504088896338700e+00);
+    double r = __builtin_fma(-kd, ln2_hi, x);
+    r = __builtin_fma(-kd, ln2_lo, r);
+    const double c[18] = {
+        1.0, 1.0, 1.0/2.0, 1.0/6.0, 1.0/24.0, 1.0/120.0, 1.0/720.0, 1.0/5040.0, 1.0/40320.0,
+        1.0/362880.0, 1.0/3628800.0, 1.0/39916800.0, 1.0/479001600.0, 1.0/6227020800.0,
+        1.0/87178291200.0, 1.0/1307674368000.0, 1.0/20922789888000.0, 1.0/355687428096000.0};
+    double p = c[17];
+#pragma unroll
+    for (int n = 16; n >= 0; n--) p = __builtin_fma(p, r, c[n]);
+    int k = (int)kd;
+    if (k > 1023) { k -= 1023; p *= 8.98846567431157953865e+307; }
+    if (k < -1022) { k += 1022; p *= 2.22507385850720138309e-308; }
+    return p * __longlong_as_double((long long)((uint64_t)(k + 1023) << 52));
+}
+QG_DEV float qg_expf(float x) { return (float)qg_exp_d((double)x); }
+QG_DEV float qg_sig(float a) { return 1.0f / (1.0f + qg_expf(-a)); }
+// SwiGLU as cpu.c:216 writes it: (g*(1/(1+exp(-g))))*u.
+QG_DEV float qg_swiglu(float g, float u) { return (g * (1.0f / (1.0f + qg_expf(-g)))) * u; }
+
+// ---- cross-lane helpers (wave64) ----
+// Pairwise tree over 32-lane halves with strides 16,8,4,2,1: lane 0 (and 32)
+// ends with ((a0+a16)+(a8+a24))+... exactly as cpu.c's reduction
+// (cpu_portable.h:333, gpu.cu:89-92).
+QG_DEV float qg_tree32(float v) {
+    v += __shfl_down(v, 16, 32);
+    v += __shfl_down(v, 8, 32);
+    v += __shfl_down(v, 4, 32);
+    v += __shfl_down(v, 2, 32);
+    v += __shfl_down(v, 1, 32);
+    return v;
+}
+// Sum over `width` consecutive lanes (power of two <= 64); result in every lane.
+template <int WIDTH>
+QG_DEV float qg_sum_lanes(float v) {
+#pragma unroll
+    for (int d = WIDTH / 2; d >= 1; d /= 2) v += __shfl_xor(v, d, WIDTH);
+    return v;
+}
+
+// 16 bytes from global memory with one 128-bit load (address 4-byte aligned).
+QG_DEV uint4 qg_ld16(const uint8_t *p) { return *(const uint4 *)p; }

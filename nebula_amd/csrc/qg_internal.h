@@ -1,0 +1,16 @@
+// Internal declarations shared by the libqwen_gpu.so translation units.
+#pragma once
+#include "qg_common.h"
+#include "../../include/qwen_gpu.h"
+
+// The calling thread's launch stream (null stream, or the capture stream).
+hipStream_t qg_stream(void);
+
+// Shapes used by the entry points that take no width (gather, scatter,
+// reduce, mtp_moe, shared_add); set by qg_moe_configure.
+int qg_cfg_width(void);
+int qg_cfg_ff(void);
+
+// Launchers shared between the drop-in entry points and the fused layer.
+int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt,
+                           const uint8_t *w_extra_row, hipStream_t s);

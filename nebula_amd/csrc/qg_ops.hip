@@ -1,0 +1,371 @@
+// Drop-in operators of the reference's GPU C ABI on the routed-MoE path
+// (gpu.h:37-43,62-78).  Each entry point keeps the reference's argument
+// list, validation and semantics (gpu.cu lines cited per function); the
+// kernels are written for CDNA4 wave64.
+#include "qg_internal.h"
+
+static int g_width = 2560, g_ff = 640;  // gpu.cu:508-553 hard-code these
+int qg_cfg_width(void) { return g_width; }
+int qg_cfg_ff(void) { return g_ff; }
+
+namespace {
+
+// ------------------------------------------------------------------------
+// qg_matmul: out[t,r] = sum_c deq(W)[r,c] x[t,c] in the reference's order.
+// Each 32-lane half of a wave owns one row; lane j owns partial sum j
+// (k = j mod 32, ascending k, fused multiply-add), then the stride
+// 16/8/4/2/1 tree.  This is the order of cpu.c:122-139 and gpu.cu:154-180,
+// so every result equals cpu.c's qc_matmul bit for bit.  A block is one
+// wave (two rows) so that even the 512-row router fills all CUs.  TT tokens
+// share each weight value.
+// ------------------------------------------------------------------------
+template <int TT>
+struct Acc { float v[TT]; };
+
+template <int TT>
+QG_DEV void acc_step(Acc<TT> &a, float w, const float *x, size_t cols, int k, int n) {
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+        if (t < n) a.v[t] = __builtin_fmaf(w, x[(size_t)t * cols + k], a.v[t]);
+}
+
+template <int TYPE, int TT>
+__global__ __launch_bounds__(64) void mm_exact_kernel(float *__restrict__ out, const uint8_t *__restrict__ w, int type,
+                                                      int rows, int cols, const float *__restrict__ x, int nt,
+                                                      size_t stride, const uint8_t *extra_row) {
+    const int half = threadIdx.x >> 5, j = threadIdx.x & 31;
+    const int row = blockIdx.x * 2 + half;
+    const int t0 = blockIdx.y * TT, n = min(nt - t0, TT);
+    if (row >= rows) return;  // whole 32-lane half leaves; shuffles stay within halves
+    const uint8_t *wr = (extra_row && row == rows - 1) ? extra_row : w + (size_t)row * stride;
+    const float *xb = x + (size_t)t0 * cols;
+    Acc<TT> a;
+#pragma unroll
+    for (int t = 0; t < TT; t++) a.v[t] = 0.0f;
+    if (TYPE == QT_F32) {
+        const float *wf = (const float *)wr;
+        for (int k = 0; k < cols; k += 32) acc_step<TT>(a, wf[k + j], xb, cols, k + j, n);
+    } else if (TYPE == QT_Q4_K) {
+        for (int sb = 0; sb < cols / 256; sb++) {
+            const uint8_t *p = wr + (size_t)sb * 144;
+            const float d = qg_half(p), dmin = qg_half(p + 2);
+            const uint8_t *sc = p + 4;
+#pragma unroll
+            for (int gp = 0; gp < 4; gp++) {
+                const int byte = p[16 + gp * 32 + j];
+#pragma unroll
+                for (int hi = 0; hi < 2; hi++) {
+                    const int g = gp * 2 + hi;
+                    const int s = g < 4 ? (sc[g] & 63) : ((sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4));
+                    const int m = g < 4 ? (sc[g + 4] & 63) : ((sc[g + 4] >> 4) | ((sc[g] >> 6) << 4));
+                    const float wv = __builtin_fmaf(d * (float)s, (float)((byte >> (hi * 4)) & 15), -(dmin * (float)m));
+                    acc_step<TT>(a, wv, xb, cols, sb * 256 + g * 32 + j, n);
+                }
+            }
+        }
+    } else if (TYPE == QT_IQ4_NL) {
+        for (int b = 0; b < cols / 32; b++) {
+            const uint8_t *p = wr + (size_t)b * 18;
+            const int q = (p[2 + (j & 15)] >> ((j >> 4) * 4)) & 15;
+            acc_step<TT>(a, qg_half(p) * (float)qg_iq4nl_lut[q], xb, cols, b * 32 + j, n);
+        }
+    } else {
+        // generic formats; F32/F16/BF16 rows may end in a partial 32-column step
+        // (lanes past the end add nothing, as gpu.cu:159's k<cols loop)
+        for (int k = 0; k < cols; k += 32)
+            if (k + j < cols) acc_step<TT>(a, qg_weight_at(wr, type, k + j), xb, cols, k + j, n);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        if (t < n) {
+            const float s = qg_tree32(a.v[t]);
+            if (j == 0) out[(size_t)(t0 + t) * rows + row] = s;
+        }
+    }
+}
+
+template <int TYPE>
+void launch_mm_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt, size_t stride,
+                     const uint8_t *extra, hipStream_t s) {
+    dim3 grid((rows + 1) / 2, 1);
+    if (nt == 1) { mm_exact_kernel<TYPE, 1><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra); return; }
+    if (nt <= 4) { mm_exact_kernel<TYPE, 4><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra); return; }
+    grid.y = (nt + 15) / 16;
+    mm_exact_kernel<TYPE, 16><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra);
+}
+
+// ------------------------------------------------------------------------
+// Elementwise and row operators.
+// ------------------------------------------------------------------------
+__global__ void gather_kernel(float *o, const uint8_t *w, int type, int n, size_t stride, int row) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = qg_weight_at(w + (size_t)row * stride, type, i);
+}
+__global__ void dequant_kernel(float *o, const uint8_t *w, int type, int rows, int cols, size_t stride) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (size_t)rows * cols) o[i] = qg_weight_at(w + (i / cols) * stride, type, (int)(i % cols));
+}
+
+// RMS/L2 norm of gpu.cu:204-214: one block per (group, token).
+__global__ __launch_bounds__(256) void norm_kernel(float *o, const float *x, const float *w, int width, int groups, int wg, int l2, float eps) {
+    __shared__ float partial[4];
+    const int g = blockIdx.x, base = g * width;
+    float ss = 0;
+    for (int i = threadIdx.x; i < width; i += 256) ss = __builtin_fmaf(x[base + i], x[base + i], ss);
+    ss = qg_sum_lanes<64>(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float scale = 1.0f / __builtin_sqrtf(ss / (l2 ? 1.0f : (float)width) + eps);
+    for (int i = threadIdx.x; i < width; i += 256)
+        o[base + i] = x[base + i] * scale * (w ? w[(wg ? g % groups : 0) * width + i] : 1.0f);
+}
+
+// gpu.cu:215-220: a = x*scale; op0 a*sig(a), op1 sig(a), else a.
+__global__ void unary_kernel(float *o, const float *x, int n, int op, float s) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { float a = x[i] * s; o[i] = op == 0 ? a * qg_sig(a) : op == 1 ? qg_sig(a) : a; }
+}
+// gpu.cu:221-226: op0 add, otherwise multiply.
+__global__ void binary_kernel(float *o, const float *a, const float *b, int n, int op) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = op == 0 ? a[i] + b[i] : a[i] * b[i];
+}
+
+// ------------------------------------------------------------------------
+// Routing (gpu.cu:456-465).  One wave per token; lane l holds logits
+// l, l+64, ..., l+448.  Ten rounds of wave argmax with the lowest index
+// among equal maxima (the reference's strict-greater scan from index 0),
+// numerators exp(s - max) summed in rank order, then divided by the sum.
+// ------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void route_kernel(int *ids, float *weights, const float *logits, int nt, int ld) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *s = logits + (size_t)t * ld;
+    float v[8];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
+    if (__any(bad)) {
+        if (lane < QG_TOP) { ids[t * QG_TOP + lane] = -1; weights[t * QG_TOP + lane] = 0.0f; }
+        return;
+    }
+    float largest = v[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) largest = fmaxf(largest, v[i]);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) largest = fmaxf(largest, __shfl_xor(largest, d));
+    float num[QG_TOP], total = 0.0f;
+    int best_id[QG_TOP];
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) {
+        float bv = v[0];
+        int bi = 0;
+#pragma unroll
+        for (int i = 1; i < 8; i++) if (v[i] > bv) { bv = v[i]; bi = i; }
+        int bidx = lane + 64 * bi;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            const float ov = __shfl_xor(bv, d);
+            const int oi = __shfl_xor(bidx, d);
+            if (ov > bv || (ov == bv && oi < bidx)) { bv = ov; bidx = oi; }
+        }
+        best_id[k] = bidx;
+        num[k] = qg_expf(bv - largest);
+        total += num[k];
+        if ((bidx & 63) == lane) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) if (i == (bidx >> 6)) v[i] = -__builtin_inff();
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++)
+        if (lane == k) { ids[t * QG_TOP + k] = best_id[k]; weights[t * QG_TOP + k] = num[k] / total; }
+}
+
+// Pruning (gpu.cu:467-483), one thread per token, device atomics for the
+// counters exactly as the reference (skipped_mass is an order-dependent
+// double atomic there too).
+__global__ void prune_kernel(int *ids, float *w, const uint8_t *resident, int nt, double thr, qg_prune_stats *st) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nt) return;
+    int missing = 0;
+    double mass = 0;
+    for (int k = 0; k < QG_TOP; k++) {
+        const int e = ids[t * QG_TOP + k];
+        if (e < 0 || e >= QG_EXPERTS) return;
+        if (!resident[e]) { missing++; mass += (double)w[t * QG_TOP + k]; }
+    }
+    atomicAdd((unsigned long long *)&st->token_layers, 1ULL);
+    atomicAdd((unsigned long long *)&st->missing_selections, (unsigned long long)missing);
+    if (missing && thr > 0 && mass < thr) {
+        for (int k = 0; k < QG_TOP; k++) {
+            const int e = ids[t * QG_TOP + k];
+            if (!resident[e]) { ids[t * QG_TOP + k] = -e - 2; w[t * QG_TOP + k] = 0.0f; }
+        }
+        atomicAdd((unsigned long long *)&st->skipped_selections, (unsigned long long)missing);
+        atomicAdd((unsigned long long *)&st->avoided_token_handoffs, 1ULL);
+        atomicAdd(&st->skipped_mass, mass);
+    }
+}
+
+// Token map (gpu.cu:489-500): row e lists ascending tokens that selected e.
+// One wave per expert; ordered compaction by ballot + popcount.
+__global__ __launch_bounds__(64) void moe_map_kernel(int *map, const int *ids, int nt) {
+    const int e = blockIdx.x, lane = threadIdx.x;
+    int carry = 0;
+    for (int base = 0; base < nt; base += 64) {
+        const int t = base + lane;
+        bool sel = false;
+        if (t < nt) {
+#pragma unroll
+            for (int k = 0; k < QG_TOP; k++) sel |= ids[t * QG_TOP + k] == e;
+        }
+        const unsigned long long mask = __ballot(sel);
+        if (sel) map[(size_t)e * nt + carry + __popcll(mask & ((1ULL << lane) - 1ULL))] = t;
+        carry += __popcll(mask);
+    }
+}
+
+// gpu.cu:506-512, width from qg_moe_configure.
+__global__ void moe_gather_kernel(float *out, const float *x, const int *map, int width) {
+    const int r = blockIdx.x, t = map[r];
+    for (int d = threadIdx.x; d < width; d += blockDim.x) out[(size_t)r * width + d] = x[(size_t)t * width + d];
+}
+// gpu.cu:513-517: rank r -> token map[r] (or r), slot = last k with
+// ids[t,k]==expert, slots[t,slot,:] = y[r,:]*w[t,slot].
+__global__ void moe_scatter_kernel(float *slots, const float *y, const float *w, const int *ids, const int *map, int expert, int width) {
+    const int r = blockIdx.x, t = map ? map[r] : r;
+    int slot = -1;
+    for (int k = 0; k < QG_TOP; k++) if (ids[t * QG_TOP + k] == expert) slot = k;
+    if (slot < 0) return;
+    const float wk = w[t * QG_TOP + slot];
+    for (int d = threadIdx.x; d < width; d += blockDim.x)
+        slots[((size_t)t * QG_TOP + slot) * width + d] = y[(size_t)r * width + d] * wk;
+}
+// gpu.cu:521-527: out = sum of the 10 slots from 0 in router-rank order.
+__global__ void moe_reduce_kernel(float *out, const float *slots, int nt, int width) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)nt * width) return;
+    const size_t t = i / width, d = i % width;
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) sum += slots[(t * QG_TOP + k) * width + d];
+    out[i] = sum;
+}
+// gpu.cu:552-553: out += shared*sig(gate[t]) (contracted to one fma, as nvcc does).
+__global__ void shared_add_kernel(float *o, const float *x, const float *g, int nt, int width) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (size_t)nt * width) o[i] = __builtin_fmaf(x[i], qg_sig(g[i / width]), o[i]);
+}
+
+unsigned blocks_for(size_t n, unsigned threads) { return (unsigned)((n + threads - 1) / threads); }
+
+}  // namespace
+
+int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt,
+                           const uint8_t *extra, hipStream_t s) {
+    const size_t stride = qg_row_bytes_host(type, cols);
+    switch (type) {
+    case QT_F32: launch_mm_exact<QT_F32>(out, w, type, rows, cols, x, nt, stride, extra, s); break;
+    case QT_Q4_K: launch_mm_exact<QT_Q4_K>(out, w, type, rows, cols, x, nt, stride, extra, s); break;
+    case QT_IQ4_NL: launch_mm_exact<QT_IQ4_NL>(out, w, type, rows, cols, x, nt, stride, extra, s); break;
+    default: launch_mm_exact<-1>(out, w, type, rows, cols, x, nt, stride, extra, s); break;
+    }
+    return hipGetLastError();
+}
+
+extern "C" {
+
+int qg_moe_configure(int width, int ff) {
+    if (width < 256 || width > 8192 || width % 256 || ff < 32 || ff > 4096 || ff % 32) return hipErrorInvalidValue;
+    g_width = width;
+    g_ff = ff;
+    return hipSuccess;
+}
+
+// gpu.cu:181-189: same validation (tokens 1..8192, block-multiple columns).
+int qg_matmul(float *o, const void *w, int type, int rows, int cols, const float *x, int nt) {
+    const size_t stride = qg_row_bytes_host(type, cols);
+    if (!stride || rows < 1 || cols < 1 || nt < 1 || nt > QG_MAX_TOKENS || !o || !w || !x) return hipErrorInvalidValue;
+    if (cols % 32) {  // only F32/F16/BF16 rows can have a partial last step
+        launch_mm_exact<-1>(o, (const uint8_t *)w, type, rows, cols, x, nt, stride, nullptr, qg_stream());
+        return hipGetLastError();
+    }
+    return qg_launch_matmul_exact(o, (const uint8_t *)w, type, rows, cols, x, nt, nullptr, qg_stream());
+}
+
+int qg_gather(float *o, const void *w, int type, int cols, int row) {  // gpu.cu:193-196
+    const size_t stride = qg_row_bytes_host(type, cols);
+    if (!stride || row < 0) return hipErrorInvalidValue;
+    gather_kernel<<<blocks_for(cols, 256), 256, 0, qg_stream()>>>(o, (const uint8_t *)w, type, cols, stride, row);
+    return hipGetLastError();
+}
+
+int qg_dequant(float *o, const void *w, int type, int rows, int cols) {  // gpu.cu:200-203
+    const size_t stride = qg_row_bytes_host(type, cols);
+    if (!stride || rows < 1) return hipErrorInvalidValue;
+    dequant_kernel<<<blocks_for((size_t)rows * cols, 256), 256, 0, qg_stream()>>>(o, (const uint8_t *)w, type, rows, cols, stride);
+    return hipGetLastError();
+}
+
+int qg_norm(float *o, const float *x, const float *w, int width, int groups, int nt, int wg, int l2, float eps) {  // gpu.cu:212-214
+    if (width < 1 || groups < 1 || nt < 1) return hipErrorInvalidValue;
+    norm_kernel<<<groups * nt, 256, 0, qg_stream()>>>(o, x, w, width, groups, wg, l2, eps);
+    return hipGetLastError();
+}
+
+int qg_unary(float *o, const float *x, int n, int op, float s) {  // gpu.cu:219-220
+    if (n < 1) return hipSuccess;
+    unary_kernel<<<blocks_for(n, 256), 256, 0, qg_stream()>>>(o, x, n, op, s);
+    return hipGetLastError();
+}
+
+int qg_binary(float *o, const float *a, const float *b, int n, int op) {  // gpu.cu:225-226
+    if (n < 1) return hipSuccess;
+    binary_kernel<<<blocks_for(n, 256), 256, 0, qg_stream()>>>(o, a, b, n, op);
+    return hipGetLastError();
+}
+
+int qg_route(int *ids, float *w, const float *logits, int nt) {  // gpu.cu:466
+    if (nt < 1 || nt > QG_MAX_TOKENS || !ids || !w || !logits) return hipErrorInvalidValue;
+    route_kernel<<<nt, 64, 0, qg_stream()>>>(ids, w, logits, nt, QG_EXPERTS);
+    return hipGetLastError();
+}
+
+int qg_prune_routes(int *ids, float *w, const unsigned char *resident, int nt, double thr, qg_prune_stats *st) {  // gpu.cu:484-488
+    if (nt < 1 || nt > QG_MAX_TOKENS || thr < 0 || thr > 0.1 || !__builtin_isfinite(thr)) return hipErrorInvalidValue;
+    prune_kernel<<<blocks_for(nt, 128), 128, 0, qg_stream()>>>(ids, w, resident, nt, thr, st);
+    return hipGetLastError();
+}
+
+int qg_moe_map(int *map, const int *ids, int nt) {  // gpu.cu:501-505
+    if (nt < 1 || nt > QG_MAX_TOKENS) return hipErrorInvalidValue;
+    moe_map_kernel<<<QG_EXPERTS, 64, 0, qg_stream()>>>(map, ids, nt);
+    return hipGetLastError();
+}
+
+int qg_moe_gather(float *o, const float *x, const int *map, int selected) {  // gpu.cu:509-512
+    if (selected < 1) return selected ? hipErrorInvalidValue : hipSuccess;
+    moe_gather_kernel<<<selected, 256, 0, qg_stream()>>>(o, x, map, g_width);
+    return hipGetLastError();
+}
+
+int qg_moe_scatter(float *o, const float *y, const float *w, const int *ids, const int *map, int expert, int selected) {  // gpu.cu:518-520
+    if (selected < 1) return selected ? hipErrorInvalidValue : hipSuccess;
+    moe_scatter_kernel<<<selected, 256, 0, qg_stream()>>>(o, y, w, ids, map, expert, g_width);
+    return hipGetLastError();
+}
+
+int qg_moe_reduce(float *out, const float *slots, int nt) {  // gpu.cu:525-527
+    if (nt < 1) return hipErrorInvalidValue;
+    moe_reduce_kernel<<<blocks_for((size_t)nt * g_width, 256), 256, 0, qg_stream()>>>(out, slots, nt, g_width);
+    return hipGetLastError();
+}
+
+int qg_shared_add(float *o, const float *x, const float *g, int nt) {  // gpu.cu:553
+    if (nt < 1) return hipErrorInvalidValue;
+    shared_add_kernel<<<blocks_for((size_t)nt * g_width, 256), 256, 0, qg_stream()>>>(o, x, g, nt, g_width);
+    return hipGetLastError();
+}
+
+}  // extern "C"

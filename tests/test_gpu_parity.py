@@ -1,0 +1,418 @@
+"""GPU parity tests through libqwen_gpu.so's C ABI against the CPU oracle.
+
+Bars: routing ids, weights, coverage flags, dispatch permutations and the
+drop-in qg_matmul are bit-exact; fp32 layer outputs are within max-abs 1e-3
+and rel-L2 1e-4 of the oracle (the tolerance stated for this path).
+Inputs are seeded; weights are generated on the device and, independently,
+on the host by the oracle's generator (their bytes are checked equal).
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from nebula_amd import qg, synth
+from nebula_amd.qg import Device, call
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 1e-3, 1e-4
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def assert_close(got, want, what=""):
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    diff = g - w
+    maxabs = float(np.abs(diff).max()) if diff.size else 0.0
+    rel = float(np.linalg.norm(diff) / max(np.linalg.norm(w), 1e-30))
+    assert maxabs <= MAX_ABS and rel <= REL_L2, f"{what}: max-abs {maxabs:.3g} rel-L2 {rel:.3g}"
+    return maxabs, rel
+
+
+def legal_blocks(rng, typ, rows, cols):
+    from test_oracle_cpu import legal_blocks as lb
+    return np.ascontiguousarray(lb(rng, typ, rows, cols))
+
+
+# ---------------- generator ----------------
+
+@pytest.mark.parametrize("typ,rows,cols", [(0, 3, 2048), (12, 5, 2048), (20, 7, 512), (12, 4, 512)])
+def test_device_generator_matches_host(qgl, typ, rows, cols):
+    say(f"synth type={typ} {rows}x{cols}")
+    strm = synth.stream(synth.GATE, 37)
+    dev = Device(nbytes=rows * qg.row_bytes(typ, cols))
+    qg.call("synth_matrix", dev.p, typ, 1234, strm, rows, cols, qg.F(0.02))
+    np.testing.assert_array_equal(dev.get(), O.fill_matrix(typ, 1234, strm, rows, cols))
+
+
+# ---------------- drop-in operators ----------------
+
+def test_matmul_bitexact_all_formats(qgl):
+    """qg_matmul == the oracle (== cpu.c qc_matmul) bit for bit, every format,
+    the batch tails of qwen/test_gpu.py:157."""
+    rng = np.random.default_rng(812603)
+    for typ in (0, 1, 30, 2, 6, 7, 8, 12, 13, 14, 20):
+        for cols in ((512, 2048) if typ in (12, 13, 14) else (320, 640)):
+            rows = 13
+            w = legal_blocks(rng, typ, rows, cols)
+            dw = Device(w)
+            for nt in (1, 4, 16, 17, 33, 512):
+                say(f"matmul type={typ} cols={cols} nt={nt}")
+                x = rng.normal(0, .2, (nt, cols)).astype(np.float32)
+                dx, out = Device(x), Device(shape=(nt, rows), dtype=np.float32)
+                call("matmul", out.p, dw.p, typ, rows, cols, dx.p, nt)
+                np.testing.assert_array_equal(out.get().view('u4'), O.matmul(w, typ, rows, cols, x).view('u4'),
+                                              err_msg=f"type {typ} cols {cols} nt {nt}")
+
+
+def test_matmul_router_shape_and_errors(qgl):
+    rng = np.random.default_rng(1)
+    w = rng.normal(0, .02, (512, 2048)).astype(np.float32)
+    x = rng.normal(0, 1, (2048, 2048)).astype(np.float32)
+    dw, dx, out = Device(w), Device(x), Device(shape=(2048, 512), dtype=np.float32)
+    say("matmul router 512x2048 nt=2048")
+    call("matmul", out.p, dw.p, 0, 512, 2048, dx.p, 2048)
+    got = out.get()
+    for t in (0, 1, 777, 2047):
+        np.testing.assert_array_equal(got[t].view('u4'), O.matmul(w, 0, 512, 2048, x[t:t + 1])[0].view('u4'))
+    # odd F32 width (partial last lane step), as the reference's k<cols loop allows
+    w2 = rng.normal(0, .1, (5, 100)).astype(np.float32)
+    x2 = rng.normal(0, 1, (3, 100)).astype(np.float32)
+    o2, dw2, dx2 = Device(shape=(3, 5), dtype=np.float32), Device(w2), Device(x2)
+    call("matmul", o2.p, dw2.p, 0, 5, 100, dx2.p, 3)
+    np.testing.assert_allclose(o2.get(), x2.astype(np.float64) @ w2.T.astype(np.float64), rtol=1e-5, atol=1e-5)
+    assert qgl.qg_matmul(out.p, dw.p, 12, 512, 100, dx.p, 1) != 0  # Q4_K needs 256-multiples
+    assert qgl.qg_matmul(out.p, dw.p, 0, 512, 2048, dx.p, 8193) != 0
+
+
+def test_route_matches_oracle_and_kat(qgl):
+    rng = np.random.default_rng(812603)
+    logits = (rng.normal(size=(300, 512))).astype(np.float32)
+    logits[0] = 0
+    logits[1, 100:120] = logits[1, 5]  # ties
+    dl = Device(logits)
+    ids, w = Device(shape=(300, 10), dtype=np.int32), Device(shape=(300, 10), dtype=np.float32)
+    say("route 300 tokens")
+    call("route", ids.p, w.p, dl.p, 300)
+    oi, ow = O.route(logits)
+    np.testing.assert_array_equal(ids.get(), oi)
+    np.testing.assert_array_equal(w.get().view('u4'), ow.view('u4'))
+    np.testing.assert_array_equal(ids.get()[:, :10], np.argsort(-logits, axis=1, kind='stable')[:, :10])
+    logits[5, 7] = np.nan
+    logits[6, 511] = -np.inf
+    dl.set(logits)
+    call("route", ids.p, w.p, dl.p, 300)
+    np.testing.assert_array_equal(ids.get()[[5, 6]], -1)
+    np.testing.assert_array_equal(w.get()[[5, 6]], 0)
+
+
+def test_prune_known_answer_gpu(qgl):
+    """qwen/test_gpu.py:84-95 on the device."""
+    ids = np.tile(np.arange(10, dtype=np.int32), (5, 1))
+    weights = np.full((5, 10), .1, np.float32)
+    resident = np.zeros(512, np.uint8)
+    resident[:8] = 1
+    weights[0, 8:] = .04; weights[1, 8:] = .05; weights[2, 8:] = .06; weights[3, 8:] = 0; weights[4, 8:] = [.01, .10]
+    di, dw, dr, dc = Device(ids), Device(weights), Device(resident), Device(nbytes=C.sizeof(qg.PruneStats))
+    say("prune KAT")
+    call("prune_routes", di.p, dw.p, dr.p, 5, .10, dc.p)
+    actual = di.get()
+    assert np.all(actual[[0, 3], 8:] <= -2)
+    np.testing.assert_array_equal(actual[[1, 2, 4]], ids[[1, 2, 4]])
+    np.testing.assert_array_equal(dw.get()[:, :8], weights[:, :8])
+    st = qg.PruneStats.from_buffer_copy(dc.get())
+    assert (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs) == (5, 10, 4, 2)
+    oi, ow, ost = O.prune(ids, weights, resident)
+    np.testing.assert_array_equal(actual, oi)
+    np.testing.assert_array_equal(dw.get(), ow)
+    assert st.skipped_mass == ost.skipped_mass
+    assert qgl.qg_prune_routes(di.p, dw.p, dr.p, 5, .2, dc.p) != 0
+
+
+def test_moe_map_and_dispatch(qgl):
+    """qwen/test_gpu.py:352-359 at nt 511/513/1025/2048 and the CSR dispatch."""
+    rng = np.random.default_rng(812603)
+    for nt in (1, 17, 511, 513, 1025, 2048):
+        say(f"map/dispatch nt={nt}")
+        ids = np.stack([rng.choice(512, 10, replace=False) for _ in range(nt)]).astype(np.int32)
+        dids = Device(ids)
+        mapping = Device(shape=(512, nt), dtype=np.int32)
+        call("moe_map", mapping.p, dids.p, nt)
+        om, counts = O.moe_map(ids)
+        got = mapping.get()
+        for e in range(512):
+            np.testing.assert_array_equal(got[e, :counts[e]], om[e, :counts[e]])
+        off, tok, slot, status = (Device(shape=(513,), dtype=np.int32), Device(shape=(nt * 10,), dtype=np.int32),
+                                  Device(shape=(nt * 10,), dtype=np.int32), Device(shape=(1,), dtype=np.int32))
+        call("moe_dispatch", off.p, tok.p, slot.p, status.p, dids.p, nt)
+        ooff, otok, oslot = O.dispatch(ids)
+        assert status.get()[0] == 0
+        np.testing.assert_array_equal(off.get(), ooff)
+        np.testing.assert_array_equal(tok.get()[:len(otok)], otok)
+        np.testing.assert_array_equal(slot.get()[:len(oslot)], oslot)
+    bad = ids.copy()
+    bad[3, 4] = 700
+    dids = Device(bad)
+    call("moe_dispatch", off.p, tok.p, slot.p, status.p, dids.p, nt)
+    assert status.get()[0] != 0
+
+
+def test_gather_scatter_reduce_order_independent(qgl):
+    """qwen/test_gpu.py:361-384: warm/cold expert order must not change the
+    router-rank summation."""
+    rng = np.random.default_rng(812603)
+    call("moe_configure", 2560, 640)
+    nt = 4
+    ids = np.stack([rng.choice(27, 10, replace=False) for _ in range(nt)]).astype(np.int32)
+    weights = np.exp((rng.normal(size=(nt, 10)) * .2).astype(np.float32))
+    weights /= weights.sum(1, keepdims=True)
+    values = (rng.normal(size=(27, nt, 2560)) * 6).astype(np.float32)
+    dids, dw = Device(ids), Device(weights.astype(np.float32))
+    mapping = Device(shape=(512, nt), dtype=np.int32)
+    call("moe_map", mapping.p, dids.p, nt)
+    slots = Device(shape=(nt, 10, 2560), dtype=np.float32)
+    out = Device(shape=(nt, 2560), dtype=np.float32)
+    expected = np.zeros((nt, 2560), np.float32)
+    for k in range(10):
+        expected += values[ids[:, k], np.arange(nt)] * weights[:, k, None]
+    results = []
+    for order in (np.unique(ids), rng.permutation(np.unique(ids))):
+        call("zero", slots.p, slots.nbytes)
+        for expert in order:
+            selected = (ids == expert).any(1)
+            dx = Device(values[expert])
+            compact = Device(shape=values[expert].shape, dtype=np.float32)
+            token_map = mapping.p + int(expert) * nt * 4
+            call("moe_gather", compact.p, dx.p, token_map, int(selected.sum()))
+            np.testing.assert_array_equal(compact.get()[:selected.sum()], values[expert, selected])
+            call("moe_scatter", slots.p, compact.p, dw.p, dids.p, token_map, int(expert), int(selected.sum()))
+        call("moe_reduce", out.p, slots.p, nt)
+        results.append(out.get())
+    np.testing.assert_array_equal(results[0], results[1])
+    np.testing.assert_allclose(results[0], expected, atol=2e-5, rtol=2e-5)
+
+
+def _mtp_oracle(x, ids, weights, gate, up, down, D, Fd, dt):
+    """slots/mid of gpu.cu:528-543 from the oracle's fixed-order products."""
+    nt = x.shape[0]
+    gb, ub, db = Fd * O.row_bytes(12, D), Fd * O.row_bytes(12, D), D * O.row_bytes(dt, Fd)
+    slots = np.full((nt, 10, D), np.nan, np.float32)
+    mid = np.full((nt, 10, Fd), np.nan, np.float32)
+    for t in range(nt):
+        for k in range(10):
+            e = int(ids[t, k])
+            if not 0 <= e < 512:
+                continue
+            g = O.matmul(gate[e * gb:(e + 1) * gb], 12, Fd, D, x[t:t + 1])[0]
+            u = O.matmul(up[e * ub:(e + 1) * ub], 12, Fd, D, x[t:t + 1])[0]
+            ex = np.array([O.lib().nbo_expf(float(-v)) for v in g], np.float32)
+            m = (g * (np.float32(1) / (np.float32(1) + ex))) * u
+            mid[t, k] = m
+            slots[t, k] = O.matmul(down[e * db:(e + 1) * db], dt, D, Fd, m[None])[0] * weights[t, k]
+    return slots, mid
+
+
+@pytest.mark.parametrize("D,Fd", [(2560, 640), (2048, 512)])
+def test_mtp_moe(qgl, D, Fd):
+    """qwen/test_gpu.py:164-187: seventeen rows, Q4_K gate/up, IQ4_NL down,
+    repeated ids across tokens, 18 rows rejected.  The 2560/640 shape runs the
+    fixed-order generic kernels (bit-exact); 2048/512 the fast kernels."""
+    rng = np.random.default_rng(812603)
+    call("moe_configure", D, Fd)
+    nexp = 3
+    gate = legal_blocks(rng, 12, nexp * Fd, D).reshape(-1)
+    up = legal_blocks(rng, 12, nexp * Fd, D).reshape(-1)
+    down = legal_blocks(rng, 20, nexp * D, Fd).reshape(-1)
+    for arr in (gate, up):
+        v = arr.reshape(-1, 144)
+        v[:, :2] = np.array([.0002], 'f2').view('u1')
+        v[:, 2:4] = np.array([.0001], 'f2').view('u1')
+    down.reshape(-1, 18)[:, :2] = np.array([.0002], 'f2').view('u1')
+    nt = 17
+    x = (rng.normal(size=(nt, D)) * .2).astype(np.float32)
+    ids = rng.integers(0, nexp, (nt, 10)).astype(np.int32)
+    ids[2, 3] = -1
+    scales = rng.uniform(.01, .2, (nt, 10)).astype(np.float32)
+    dx, di, dw = Device(x), Device(ids), Device(scales)
+    mid = Device(shape=(nt, 10, Fd), dtype=np.float32)
+    slots = Device(shape=(nt, 10, D), dtype=np.float32)
+    dg, du, dd = Device(gate), Device(up), Device(down)
+    say(f"mtp_moe D={D} F={Fd}")
+    call("mtp_moe", slots.p, mid.p, dx.p, di.p, dw.p, dg.p, 12, du.p, 12, dd.p, 20, nt)
+    want_slots, want_mid = _mtp_oracle(x, ids, scales, gate, up, down, D, Fd, 20)
+    got_slots, got_mid = slots.get(), mid.get()
+    assert np.all(np.isnan(got_slots[2, 3])) and np.all(np.isnan(got_mid[2, 3]))
+    ok = ~np.isnan(want_slots[..., 0])
+    if D == 2560:
+        np.testing.assert_array_equal(got_mid[ok].view('u4'), want_mid[ok].view('u4'))
+        np.testing.assert_array_equal(got_slots[ok].view('u4'), want_slots[ok].view('u4'))
+    else:
+        np.testing.assert_allclose(got_mid[ok], want_mid[ok], atol=2e-5, rtol=5e-5)
+        np.testing.assert_allclose(got_slots[ok], want_slots[ok], atol=2e-5, rtol=5e-5)
+    assert qgl.qg_mtp_moe(slots.p, mid.p, dx.p, di.p, dw.p, dg.p, 12, du.p, 12, dd.p, 20, 18) != 0
+    call("moe_configure", 2560, 640)
+
+
+# ---------------- the fused device-driven layer ----------------
+
+CFG0 = synth.LayerSpec(seed=100, gate_type=12, up_type=12, down_type=12)
+CFG1 = synth.LayerSpec(seed=200, gate_type=12, up_type=12, down_type=20, shared=True, sh_types=(12, 12, 12))
+
+
+@pytest.fixture(scope="module")
+def layer0(qgl):
+    say("building config-0 layer on device")
+    L = synth.build_layer(CFG0)
+    H = O.HostLayer(CFG0.seed, gt=12, ut=12, dt=12)
+    return L, H
+
+
+@pytest.fixture(scope="module")
+def layer1(qgl):
+    say("building config-1 layer on device")
+    L = synth.build_layer(CFG1)
+    H = O.HostLayer(CFG1.seed, gt=12, ut=12, dt=20, shared=True, sh_types=(12, 12, 12))
+    return L, H
+
+
+def _check_layer(L, H, x, what, resident=None):
+    nt = x.shape[0]
+    fw = synth.Forward(2048, 512, nt)
+    fw.x.set(np.concatenate([x, np.zeros((fw.tokens - nt, 2048), np.float32)]) if nt < fw.tokens else x)
+    say(f"forward {what} nt={nt}")
+    fw.run(L, nt)
+    qg.call("sync")
+    out, ids, w, logits, flags, st = H.forward(x, resident)
+    gi, gw = fw.ids.get()[:nt], fw.w.get()[:nt]
+    np.testing.assert_array_equal(gi, ids, err_msg=f"{what}: routing ids")
+    np.testing.assert_array_equal(gw.view('u4'), w.view('u4'), err_msg=f"{what}: routing weights")
+    gf = fw.flags.get()[:nt]
+    np.testing.assert_array_equal(gf, flags, err_msg=f"{what}: flags")
+    keep = gf < 2
+    maxabs, rel = assert_close(fw.out.get()[:nt][keep], out[keep], what)
+    assert np.all(fw.out.get()[:nt][~keep] == 0)
+    say(f"  {what}: unique experts {len(np.unique(ids[ids >= 0]))}, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
+    return fw, st
+
+
+def test_layer_config0_batch1(layer0):
+    L, H = layer0
+    for seed in (1, 2, 3):
+        _check_layer(L, H, synth.inputs(seed, 1, 2048), f"config0 seed{seed}")
+
+
+@pytest.mark.parametrize("nt", [4, 8, 17])
+def test_layer_config1_verify_batches(layer1, nt):
+    L, H = layer1
+    _check_layer(L, H, synth.inputs(50 + nt, nt, 2048, correlated=True), f"config1 B={nt}")
+
+
+def test_layer_config0_multitoken_no_shared(layer0):
+    L, H = layer0
+    _check_layer(L, H, synth.inputs(9, 5, 2048), "config0 B=5")
+
+
+def test_layer_partial_residency_flags(layer1):
+    """Config 4: 128 resident experts chosen by routed-weight mass over 4096
+    synthetic tokens; flags and pruning exact, unflagged rows in tolerance."""
+    L, H = layer1
+    xs = synth.inputs(4242, 4096, 2048, correlated=False)
+    dx = Device(xs)
+    logits = Device(shape=(4096, 512), dtype=np.float32)
+    ids, w = Device(shape=(4096, 10), dtype=np.int32), Device(shape=(4096, 10), dtype=np.float32)
+    call("matmul", logits.p, L.bufs["router"].p, 0, 512, 2048, dx.p, 4096)
+    call("route", ids.p, w.p, logits.p, 4096)
+    score = np.zeros(512)
+    np.add.at(score, ids.get().ravel(), w.get().ravel().astype(np.float64))
+    order = np.lexsort((np.arange(512), -score))
+    resident = np.zeros(512, np.uint8)
+    resident[order[:128]] = 1
+    desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    rdev = Device(resident)
+    desc.resident, desc.threshold = rdev.p, 0.10
+    saved = L.desc
+    L.desc = desc
+    try:
+        x = synth.inputs(77, 17, 2048, correlated=True)
+        fw, st = _check_layer(L, H, x, "config4 B=17", resident=resident)
+        gst = qg.PruneStats.from_buffer_copy(fw.stats.get())
+        assert (gst.token_layers, gst.missing_selections, gst.skipped_selections, gst.avoided_token_handoffs) == \
+               (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs)
+        assert gst.skipped_mass == st.skipped_mass
+    finally:
+        L.desc = saved
+
+
+def test_layer_graph_replay(layer1):
+    """The fused layer captured into a graph and replayed, with eager work in
+    between, equals the eager result every time."""
+    L, H = layer1
+    nt = 8
+    fw = synth.Forward(2048, 512, nt)
+    fw.x.set(synth.inputs(5, nt, 2048, correlated=True))
+    fw.run(L, nt)
+    eager = fw.out.get()
+    g = C.c_void_p()
+    say("graph capture of the fused layer")
+    call("graph_begin", C.byref(g))
+    fw.run(L, nt)
+    call("graph_end", g)
+    for rep in range(3):
+        call("zero", fw.out.p, fw.out.nbytes)
+        call("sync")
+        call("graph_launch", g)
+        call("sync")
+        np.testing.assert_array_equal(fw.out.get().view('u4'), eager.view('u4'), err_msg=f"replay {rep}")
+    qg.lib().qg_graph_destroy(g)
+
+
+def test_stack_per_layer_routing(qgl):
+    """Config 2 in miniature: 3 seeded layers, h <- h + MoE(RMSNorm(h)),
+    graph-captured; per layer, routing from the recorded input is bit-exact
+    and the layer output is within tolerance."""
+    specs = [synth.LayerSpec(seed=300 + l) for l in range(3)]
+    layers = [synth.build_layer(s) for s in specs]
+    hosts = [O.HostLayer(s.seed) for s in specs]
+    arr = (qg.MoeLayer * 3)(*[l.desc for l in layers])
+    h = qg.host()
+    stack = h.nm_stack_create(arr, 3, 1, 1)
+    assert stack, h.nm_last_error()
+    try:
+        x0 = synth.inputs(31, 1, 2048)
+        call("write", h.nm_stack_hidden(stack), x0.ctypes.data, x0.nbytes)
+        say("stack forward (graph)")
+        assert h.nm_stack_forward(stack, 1, 1) == 0, h.nm_last_error()
+        call("sync")
+        hfin = np.empty((1, 2048), np.float32)
+        call("read", hfin.ctypes.data, h.nm_stack_hidden(stack), hfin.nbytes)
+        hcur = x0.copy()
+        for l in range(3):
+            px, pids, pw, pout = C.c_void_p(), C.c_void_p(), C.c_void_p(), C.c_void_p()
+            assert h.nm_stack_record(stack, l, C.byref(px), C.byref(pids), C.byref(pw), C.byref(pout)) == 0
+            xl = np.empty((1, 2048), np.float32); ol = np.empty((1, 2048), np.float32)
+            il = np.empty((1, 10), np.int32); wl = np.empty((1, 10), np.float32)
+            for arr_, p in ((xl, px), (ol, pout), (il, pids), (wl, pw)):
+                call("read", arr_.ctypes.data, p.value, arr_.nbytes)
+            out, ids, w, _, _, _ = hosts[l].forward(xl)
+            np.testing.assert_array_equal(il, ids, err_msg=f"layer {l} ids")
+            np.testing.assert_array_equal(wl.view('u4'), w.view('u4'), err_msg=f"layer {l} weights")
+            assert_close(ol, out, f"stack layer {l}")
+            hcur = (hcur + ol).astype(np.float32)
+        np.testing.assert_array_equal(hfin, hcur)
+    finally:
+        h.nm_stack_destroy(stack)
+
+
+def test_forward_rejects_bad_arguments(layer0):
+    L, _ = layer0
+    fw = synth.Forward(2048, 512, 17)
+    lib = qg.lib()
+    assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 18, C.byref(L.desc), fw.ws.p, fw.ws_bytes) != 0
+    assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 1, C.byref(L.desc), fw.ws.p, 16) != 0
+    assert lib.qg_moe_workspace_bytes(2048, 512, 18) == 0
