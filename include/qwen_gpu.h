@@ -118,6 +118,13 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
 int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                    const float *x, int tokens, const qg_moe_layer *layer, void *workspace, size_t workspace_bytes);
 
+/* Benchmark support: record events[i] (qg_event_create handles) on the
+ * launch stream at the phase boundaries of this thread's qg_moe_forward
+ * calls: 0 start, 1 after the router, 2 after routing/dispatch, 3 after
+ * gate/up, 4 after down, 5 after the combine (phases fused into one kernel
+ * record adjacent events back to back).  n = 0 disables. */
+int qg_moe_phase_events(void **events, int n);
+
 /* Timing helpers for the benchmark (events on the calling thread's stream). */
 void *qg_event_create(void);
 void qg_event_destroy(void *event);

@@ -125,5 +125,82 @@ QG_DEV float qg_sum_lanes(float v) {
     return v;
 }
 
+// DPP-based wave reductions (VALU cross-lane moves instead of LDS-crossbar
+// shuffles).  quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and
+// row_mirror leave every lane of a 16-lane row with the row's result; the
+// four rows are then combined from lanes 0/16/32/48 via readlane.
+#define QG_DPP_F(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false))
+QG_DEV float qg_row_max(float v) {
+    v = fmaxf(v, QG_DPP_F(v, 0xB1));
+    v = fmaxf(v, QG_DPP_F(v, 0x4E));
+    v = fmaxf(v, QG_DPP_F(v, 0x141));
+    v = fmaxf(v, QG_DPP_F(v, 0x140));
+    return v;
+}
+QG_DEV float qg_wave_max(float v) {
+    v = qg_row_max(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+// Sum over each 16-lane row (every lane gets its row's sum).
+QG_DEV float qg_row_sum(float v) {
+    v += QG_DPP_F(v, 0xB1);
+    v += QG_DPP_F(v, 0x4E);
+    v += QG_DPP_F(v, 0x141);
+    v += QG_DPP_F(v, 0x140);
+    return v;
+}
+// Sum over groups of 8 lanes (every lane gets its group's sum).
+QG_DEV float qg_oct_sum(float v) {
+    v += QG_DPP_F(v, 0xB1);
+    v += QG_DPP_F(v, 0x4E);
+    v += QG_DPP_F(v, 0x141);
+    return v;
+}
+
+// Routing of one token by one wave (gpu.cu:456-465): ids/w receive the 10
+// winners in rank order (any non-finite logit -> ids -1, weights 0).
+// Lane l holds logits l, l+64, ..., l+448.  Each of the 10 rounds takes the
+// wave maximum (DPP), then the lowest index holding it from per-slot ballots
+// (scalar work: the first slot i with a match, its lowest lane), which is the
+// winner of the reference's strict-greater scan from index 0.
+QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane) {
+    float v[8];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
+    if (__any(bad)) {
+        if (lane < QG_TOP) { ids[lane] = -1; w[lane] = 0.0f; }
+        return;
+    }
+    float num[QG_TOP], total = 0.0f, largest = 0.0f;
+    int best_id[QG_TOP];
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) {
+        float lm = v[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) lm = fmaxf(lm, v[i]);
+        const float m = qg_wave_max(lm);
+        if (k == 0) largest = m;
+        int bidx = -1;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const unsigned long long b = __ballot(v[i] == m);
+            if (bidx < 0 && b) bidx = 64 * i + __builtin_ctzll(b);
+        }
+        best_id[k] = bidx;
+        num[k] = qg_expf(m - largest);
+        total += num[k];
+#pragma unroll
+        for (int i = 0; i < 8; i++) if (bidx == lane + 64 * i) v[i] = -__builtin_inff();
+    }
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++)
+        if (lane == k) { ids[k] = best_id[k]; w[k] = num[k] / total; }
+}
+
 // 16 bytes from global memory with one 128-bit load (address 4-byte aligned).
 QG_DEV uint4 qg_ld16(const uint8_t *p) { return *(const uint4 *)p; }

@@ -24,18 +24,18 @@ namespace {
 constexpr int MAXB = QG_MAX_DECODE;       // 17 tokens (anchor + 16 drafts, qwen.h:10)
 constexpr int MAXS = MAXB * QG_TOP;       // 170 routed selections
 constexpr int ROWS_DOWN = 32;             // output rows per down block
+constexpr int RD_THREADS = 1024;          // route/dispatch block
 
 struct Disp {
     int n_active, n_entries, status, has_shared;
-    int act_expert[QG_EXPERTS];
-    int act_off[QG_EXPERTS + 1];
+    int4 act[QG_EXPERTS];                 // active expert a: (expert id, first entry, entries, 0)
     int ent_token[MAXS];
     int ent_slot[MAXS];
     int slot_ent[MAXS];
     int tok_flag[MAXB];
 };
 
-struct WsLayout { size_t logits, disp, mid, slots, arrive, total; };
+struct WsLayout { size_t logits, disp, mid, slots, total; };
 WsLayout ws_layout(int D, int F) {
     WsLayout L;
     size_t off = 0;
@@ -44,56 +44,24 @@ WsLayout ws_layout(int D, int F) {
     L.disp = take(sizeof(Disp));
     L.mid = take((size_t)(MAXS + MAXB) * F * 4);
     L.slots = take((size_t)(MAXS + MAXB) * D * 4);
-    L.arrive = take((size_t)(D / 2 + 1) * 4);
     L.total = off;
     return L;
 }
 
-// ---------------- routing of one token by one wave (gpu.cu:456-465) ----------------
-QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane) {
-    float v[8];
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
-    if (__any(bad)) {
-        if (lane < QG_TOP) { s_ids[t * QG_TOP + lane] = -1; s_w[t * QG_TOP + lane] = 0.0f; }
-        return;
-    }
-    float largest = v[0];
-#pragma unroll
-    for (int i = 1; i < 8; i++) largest = fmaxf(largest, v[i]);
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) largest = fmaxf(largest, __shfl_xor(largest, d));
-    float num[QG_TOP], total = 0.0f;
-    int best_id[QG_TOP];
-#pragma unroll
-    for (int k = 0; k < QG_TOP; k++) {
-        float bv = v[0];
-        int bi = 0;
-#pragma unroll
-        for (int i = 1; i < 8; i++) if (v[i] > bv) { bv = v[i]; bi = i; }
-        int bidx = lane + 64 * bi;
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            const float ov = __shfl_xor(bv, d);
-            const int oi = __shfl_xor(bidx, d);
-            if (ov > bv || (ov == bv && oi < bidx)) { bv = ov; bidx = oi; }
-        }
-        best_id[k] = bidx;
-        num[k] = qg_expf(bv - largest);
-        total += num[k];
-        if ((bidx & 63) == lane) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) if (i == (bidx >> 6)) v[i] = -__builtin_inff();
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < QG_TOP; k++)
-        if (lane == k) { s_ids[t * QG_TOP + k] = best_id[k]; s_w[t * QG_TOP + k] = num[k] / total; }
+// Optional per-phase timing (benchmark support): events recorded on the
+// launch stream after each kernel of qg_moe_forward.
+thread_local void *tl_phase_ev[8] = {nullptr};
+thread_local int tl_phase_n = 0;
+void phase_mark(int i, hipStream_t s) {
+    if (i < tl_phase_n && tl_phase_ev[i]) (void)hipEventRecord((hipEvent_t)tl_phase_ev[i], s);
 }
 
-// Inclusive scan of one int per thread over a 256-thread block.
-QG_DEV int block_scan256(int v, int *s_tmp) {
+QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane) {
+    qg_route_wave(s_ids + t * QG_TOP, s_w + t * QG_TOP, s, lane);
+}
+
+// Inclusive scan of one int per thread over a RD_THREADS-thread block.
+QG_DEV int block_scan(int v, int *s_tmp) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -108,57 +76,68 @@ QG_DEV int block_scan256(int v, int *s_tmp) {
     return v + base;
 }
 
-// Build the CSR dispatch from ids in LDS.  eligible(t) excludes tokens whose
-// flag is 2 (handoff) or 3 (invalid); ids outside [0,512) never dispatch.
-// Entries of each expert are in ascending (token, rank) order.
-QG_DEV void build_dispatch(const int *s_ids, const int *s_flag, int nt, Disp *ds, int *s_tmp) {
-    const int tid = threadIdx.x, n = nt * QG_TOP;
-    for (int i = tid; i < MAXS; i += 256) ds->slot_ent[i] = -1;
-    const int e0 = 2 * tid, e1 = 2 * tid + 1;
-    int c0 = 0, c1 = 0;
-    for (int i = 0; i < n; i++) {
-        const int id = s_ids[i];
-        if ((id >> 1) == tid && id >= 0 && s_flag[i / QG_TOP] < 2) { c0 += id == e0; c1 += id == e1; }
-    }
-    const int local = (((c0 > 0) + (c1 > 0)) << 16) | (c0 + c1);
-    const int incl = block_scan256(local, s_tmp);
-    const int excl = incl - local;
-    int act = excl >> 16, off = excl & 0xffff;
-    __syncthreads();  // slot_ent initialisation above is complete
-    for (int h = 0; h < 2; h++) {
-        const int e = h ? e1 : e0, c = h ? c1 : c0;
-        if (!c) continue;
-        ds->act_expert[act] = e;
-        ds->act_off[act] = off;
-        int i = off;
-        for (int t = 0; t < nt; t++) {
-            if (s_flag[t] >= 2) continue;
-            for (int k = 0; k < QG_TOP; k++)
-                if (s_ids[t * QG_TOP + k] == e) { ds->ent_token[i] = t; ds->ent_slot[i] = t * QG_TOP + k; ds->slot_ent[t * QG_TOP + k] = i; i++; }
+// CSR dispatch of the ids in LDS, every step parallel (RD_THREADS threads):
+// selection i is eligible if 0<=id<512 and its token's flag is 0 or 1; its
+// rank within its expert is the number of earlier eligible selections of the
+// same expert, so entries of an expert come in ascending (token, rank) order.
+QG_DEV void build_dispatch(const int *s_ids, const int *s_flag, int nt, Disp *ds, int *s_cnt, int *s_rank, int *s_tmp) {
+    const int tid = threadIdx.x, n = nt * QG_TOP, lane = tid & 63;
+    if (tid < QG_EXPERTS) s_cnt[tid] = 0;
+    __syncthreads();
+    // One wave ranks 64 selections at a time: the lanes holding the same
+    // expert are found with nine ballots (one per id bit); a selection's rank
+    // is the count from earlier chunks plus its same-expert lanes below it.
+    if (tid < 64) {
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int i = c0 + lane;
+            int e = 0;
+            bool el = false;
+            if (i < n) { e = s_ids[i]; el = e >= 0 && e < QG_EXPERTS && s_flag[i / QG_TOP] < 2; }
+            unsigned long long peers = __ballot(el);
+#pragma unroll
+            for (int b = 0; b < 9; b++) {
+                const bool bit = (e >> b) & 1;
+                const unsigned long long bal = __ballot(el && bit);
+                peers &= bit ? bal : ~bal;
+            }
+            const int base = el ? s_cnt[e] : 0;
+            if (i < n) s_rank[i] = el ? base + __popcll(peers & ((1ULL << lane) - 1ULL)) : -1;
+            if (el && lane == 63 - __builtin_clzll(peers)) s_cnt[e] = base + __popcll(peers);
         }
-        act++;
-        off += c;
     }
-    if (tid == 255) {
-        ds->n_active = incl >> 16;
-        ds->n_entries = incl & 0xffff;
-        ds->act_off[incl >> 16] = incl & 0xffff;
+    __syncthreads();
+    const int c = tid < QG_EXPERTS ? s_cnt[tid] : 0;
+    const int local = ((c > 0) << 16) | c;
+    const int incl = block_scan(local, s_tmp);
+    const int excl = incl - local;
+    if (c) {
+        ds->act[excl >> 16] = make_int4(tid, excl & 0xffff, c, 0);
+        s_cnt[tid] = excl & 0xffff;  // becomes the expert's first entry
+    }
+    if (tid == RD_THREADS - 1) { ds->n_active = incl >> 16; ds->n_entries = incl & 0xffff; }
+    __syncthreads();
+    if (tid < MAXS) {
+        int ent = -1;
+        if (tid < n && s_rank[tid] >= 0) {
+            ent = s_cnt[s_ids[tid]] + s_rank[tid];
+            ds->ent_token[ent] = tid / QG_TOP;
+            ds->ent_slot[ent] = tid;
+        }
+        ds->slot_ent[tid] = ent;
     }
 }
 
 // ---------------- kernel 2: route + coverage + dispatch (one block) ----------------
-__global__ __launch_bounds__(256) void route_dispatch_kernel(int *ids_out, float *w_out, uint8_t *flags_out,
-                                                             qg_prune_stats *stats, const float *logits, int ld, int nt,
-                                                             const uint8_t *resident, double thr, Disp *ds,
-                                                             int *arrive, int n_arrive, int has_shared) {
-    __shared__ int s_ids[MAXS];
+__global__ __launch_bounds__(RD_THREADS) void route_dispatch_kernel(int *ids_out, float *w_out, uint8_t *flags_out,
+                                                                    qg_prune_stats *stats, const float *logits, int ld, int nt,
+                                                                    const uint8_t *resident, double thr, Disp *ds, int has_shared) {
+    __shared__ int s_ids[MAXS], s_rank[MAXS], s_cnt[QG_EXPERTS];
     __shared__ float s_w[MAXS];
     __shared__ int s_flag[MAXB], s_missing[MAXB];
     __shared__ double s_mass[MAXB];
-    __shared__ int s_tmp[4];
+    __shared__ int s_tmp[RD_THREADS / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < n_arrive; i += 256) arrive[i] = 0;
-    for (int t = wave; t < nt; t += 4) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane);
+    for (int t = wave; t < nt; t += RD_THREADS / 64) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane);
     __syncthreads();
     // Coverage (gpu.cu:470-478): mass of non-resident selections in rank order.
     if (tid < nt) {
@@ -180,58 +159,60 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(int *ids_out, float
         s_missing[t] = missing;
         s_mass[t] = mass;
         ds->tok_flag[t] = flag;
+        if (flags_out) flags_out[t] = (uint8_t)flag;
     }
     __syncthreads();
     // Counters in token order (deterministic, unlike the reference's atomics).
-    if (tid == 0 && resident && stats) {
+    if (tid == 0) {
+        int bad = 0;
         for (int t = 0; t < nt; t++) {
-            if (s_flag[t] == 3) continue;
-            stats->token_layers += 1;
-            stats->missing_selections += (uint64_t)s_missing[t];
-            if (s_flag[t] == 1) {
-                stats->skipped_selections += (uint64_t)s_missing[t];
-                stats->avoided_token_handoffs += 1;
-                stats->skipped_mass += s_mass[t];
+            if (s_flag[t] == 3) { bad = 1; continue; }
+            if (resident && stats) {
+                stats->token_layers += 1;
+                stats->missing_selections += (uint64_t)s_missing[t];
+                if (s_flag[t] == 1) {
+                    stats->skipped_selections += (uint64_t)s_missing[t];
+                    stats->avoided_token_handoffs += 1;
+                    stats->skipped_mass += s_mass[t];
+                }
             }
         }
+        ds->status = bad;
+        ds->has_shared = has_shared;
     }
-    for (int i = tid; i < nt * QG_TOP; i += 256) { ids_out[i] = s_ids[i]; w_out[i] = s_w[i]; }
-    if (flags_out && tid < nt) flags_out[tid] = (uint8_t)s_flag[tid];
-    if (tid == 0) { ds->status = 0; ds->has_shared = has_shared; }
-    for (int t = 0; t < nt; t++) if (s_flag[t] == 3 && tid == 0) ds->status = 1;
-    build_dispatch(s_ids, s_flag, nt, ds, s_tmp);
+    for (int i = tid; i < nt * QG_TOP; i += RD_THREADS) { ids_out[i] = s_ids[i]; w_out[i] = s_w[i]; }
+    build_dispatch(s_ids, s_flag, nt, ds, s_cnt, s_rank, s_tmp);
 }
 
 // ---------------- dispatch from given ids (qg_mtp_moe front end) ----------------
 // Every selection with 0<=id<512 dispatches (duplicates included, as the
 // reference computes each (token, rank) independently); invalid slots get
 // NaN in mid and slots (gpu.cu:531,539).
-__global__ __launch_bounds__(256) void dispatch_ids_kernel(const int *ids, int nt, Disp *ds, float *mid_slot, float *slots_out,
-                                                           int D, int F) {
-    __shared__ int s_ids[MAXS];
+__global__ __launch_bounds__(RD_THREADS) void dispatch_ids_kernel(const int *ids, int nt, Disp *ds, float *mid_slot,
+                                                                  float *slots_out, int D, int F) {
+    __shared__ int s_ids[MAXS], s_rank[MAXS], s_cnt[QG_EXPERTS];
     __shared__ int s_flag[MAXB];
-    __shared__ int s_tmp[4];
+    __shared__ int s_tmp[RD_THREADS / 64];
     const int tid = threadIdx.x;
-    for (int i = tid; i < nt * QG_TOP; i += 256) s_ids[i] = ids[i];
+    if (tid < nt * QG_TOP) s_ids[tid] = ids[tid];
     if (tid < MAXB) s_flag[tid] = 0;
     if (tid == 0) { ds->status = 0; ds->has_shared = 0; }
+    if (tid < nt) ds->tok_flag[tid] = 0;
     __syncthreads();
-    // duplicates: the CSR keeps ascending (token, rank); a duplicate id within
-    // a token yields two entries of that expert, both computed.
-    build_dispatch(s_ids, s_flag, nt, ds, s_tmp);
+    build_dispatch(s_ids, s_flag, nt, ds, s_cnt, s_rank, s_tmp);
     const float nan = __builtin_nanf("");
     for (int s = 0; s < nt * QG_TOP; s++) {
         const int e = s_ids[s];
         if (e >= 0 && e < QG_EXPERTS) continue;
-        for (int r = tid; r < F; r += 256) mid_slot[(size_t)s * F + r] = nan;
-        for (int d = tid; d < D; d += 256) slots_out[(size_t)s * D + d] = nan;
+        for (int r = tid; r < F; r += RD_THREADS) mid_slot[(size_t)s * F + r] = nan;
+        for (int d = tid; d < D; d += RD_THREADS) slots_out[(size_t)s * D + d] = nan;
     }
 }
 
 // ---------------- Q4_K chunk arithmetic ----------------
 // Chunk q (0..7) of a superblock: qs bytes 16q..16q+15 hold elements
 // l = 16(q&1)+0..15 of group ga = 2(q>>1) (low nibbles) and gb = ga+1 (high
-// nibbles) (cpu.c:56-64 layout).  Scales decoded four bytes at a time.
+// nibbles) (layout of cpu.c:56-64).  Scales decoded four bytes at a time.
 struct Q4kScale { float dsa, dma, dsb, dmb; };
 QG_DEV Q4kScale q4k_scale(uint4 hd, int q) {
     const float d = qg_half_u16(hd.x & 0xffffu), dmin = qg_half_u16(hd.x >> 16);
@@ -276,31 +257,30 @@ QG_DEV void q4k_load_slice(Q4kSlice &s, const float *xrow, int koff, bool valid)
     s.sb = sb;
 }
 
-template <int TC>
-QG_DEV void q4k_chunk_dot(float (&part)[TC], uint4 qv, const Q4kScale &sc, const Q4kSlice (&xs)[TC]) {
-    float qa[16], qb[16];
+// Nibbles of a chunk as floats: qa = group ga (low nibbles), qb = group gb.
+struct Q4kVals { float qa[16], qb[16]; };
+QG_DEV void q4k_unpack(Q4kVals &v, uint4 qv) {
     const uint32_t w4[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t lo = w4[i] & 0x0F0F0F0Fu, hi = (w4[i] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            qa[4 * i + b] = (float)((lo >> (8 * b)) & 0xffu);
-            qb[4 * i + b] = (float)((hi >> (8 * b)) & 0xffu);
+            v.qa[4 * i + b] = (float)((lo >> (8 * b)) & 0xffu);
+            v.qb[4 * i + b] = (float)((hi >> (8 * b)) & 0xffu);
         }
     }
+}
+// d*s_a*sum(q x) - dmin*m_a*sum(x) + (same for gb), added to p.
+QG_DEV float q4k_dot(float p, const Q4kVals &v, const Q4kScale &sc, const Q4kSlice &x) {
+    float sa = 0.0f, sb = 0.0f;
 #pragma unroll
-    for (int t = 0; t < TC; t++) {
-        float sa = 0.0f, sb = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) { sa = __builtin_fmaf(qa[i], xs[t].a[i], sa); sb = __builtin_fmaf(qb[i], xs[t].b[i], sb); }
-        float p = part[t];
-        p = __builtin_fmaf(sc.dsa, sa, p);
-        p = __builtin_fmaf(-sc.dma, xs[t].sa, p);
-        p = __builtin_fmaf(sc.dsb, sb, p);
-        p = __builtin_fmaf(-sc.dmb, xs[t].sb, p);
-        part[t] = p;
-    }
+    for (int i = 0; i < 16; i++) { sa = __builtin_fmaf(v.qa[i], x.a[i], sa); sb = __builtin_fmaf(v.qb[i], x.b[i], sb); }
+    p = __builtin_fmaf(sc.dsa, sa, p);
+    p = __builtin_fmaf(-sc.dma, x.sa, p);
+    p = __builtin_fmaf(sc.dsb, sb, p);
+    p = __builtin_fmaf(-sc.dmb, x.sb, p);
+    return p;
 }
 
 // koff of chunk `ch` (16-byte qs chunk index along a row of Q4_K superblocks)
@@ -315,6 +295,34 @@ QG_DEV float group_sum(float v) {
     return v;
 }
 
+// Eight per-lane partial sums -> the full wave sum of value r(lane) in every
+// lane, r = 4*bit5 + 2*bit4 + bit3 of the lane id.  A transposed butterfly:
+// 10 shuffles instead of 48.
+QG_DEV float reduce8(float (&v)[8], int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const bool up = lane & 32;
+        const float send = up ? v[i] : v[i + 4], keep = up ? v[i + 4] : v[i];
+        v[i] = keep + __shfl_xor(send, 32);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const bool up = lane & 16;
+        const float send = up ? v[i] : v[i + 2], keep = up ? v[i + 2] : v[i];
+        v[i] = keep + __shfl_xor(send, 16);
+    }
+    {
+        const bool up = lane & 8;
+        const float send = up ? v[0] : v[1], keep = up ? v[1] : v[0];
+        v[0] = keep + __shfl_xor(send, 8);
+    }
+    float r = v[0];
+    r += __shfl_xor(r, 4);
+    r += __shfl_xor(r, 2);
+    r += __shfl_xor(r, 1);
+    return r;
+}
+
 // ---------------- kernel 3: gate/up + SwiGLU (Q4_K, D = 2048*CPL) ----------------
 struct GateUpArgs {
     const float *x;
@@ -326,9 +334,12 @@ struct GateUpArgs {
     float *mid_slot;  // slot layout [(t*10+k)][F] or null
 };
 
+// Block = 4 waves x 4 (gate row, up row) pairs = 16 rows of the expert.
+// All 16 row loads are issued before any arithmetic and stay in registers
+// while the expert's tokens are processed TC at a time.
 template <int TC, int CPL>
 __global__ __launch_bounds__(256) void gateup_q4k_kernel(GateUpArgs A) {
-    constexpr int RPW = 2;  // row pairs (gate row + up row) per wave
+    constexpr int RPW = 4;
     const int a = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool shared = A.sh_gate && a == A.maxa;
     int n, ent0 = 0;
@@ -336,64 +347,64 @@ __global__ __launch_bounds__(256) void gateup_q4k_kernel(GateUpArgs A) {
     if (shared) { n = A.nt; G = A.sh_gate; U = A.sh_up; }
     else {
         if (a >= A.ds->n_active) return;
-        const int e = A.ds->act_expert[a];
-        ent0 = A.ds->act_off[a];
-        n = A.ds->act_off[a + 1] - ent0;
-        G = A.gate + (size_t)e * A.F * A.rb;
-        U = A.up + (size_t)e * A.F * A.rb;
+        const int4 info = A.ds->act[a];
+        ent0 = info.y;
+        n = info.z;
+        G = A.gate + (size_t)info.x * A.F * A.rb;
+        U = A.up + (size_t)info.x * A.F * A.rb;
     }
     const int row0 = (blockIdx.y * 4 + wave) * RPW;
-    if (row0 >= A.F) return;
-    int koff[CPL];
-    size_t qoff[CPL], hoff[CPL];
-    int qsel[CPL];
+    uint4 qg[RPW][CPL], hg[RPW][CPL], qu[RPW][CPL], hu[RPW][CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const int ch = lane + 64 * c;
-        koff[c] = q4k_koff(ch); qoff[c] = q4k_qoff(ch); hoff[c] = q4k_hoff(ch); qsel[c] = ch & 7;
+    for (int r = 0; r < RPW; r++) {
+        const size_t rowoff = (size_t)(row0 + r) * A.rb;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const int ch = lane + 64 * c;
+            qg[r][c] = qg_ld16(G + rowoff + q4k_qoff(ch)); hg[r][c] = qg_ld16(G + rowoff + q4k_hoff(ch));
+            qu[r][c] = qg_ld16(U + rowoff + q4k_qoff(ch)); hu[r][c] = qg_ld16(U + rowoff + q4k_hoff(ch));
+        }
     }
     for (int t0 = 0; t0 < n; t0 += TC) {
-        Q4kSlice xs[CPL][TC];
-        int tok[TC];
+        Q4kSlice xs[TC][CPL];
 #pragma unroll
         for (int i = 0; i < TC; i++) {
             const bool valid = t0 + i < n;
-            tok[i] = valid ? (shared ? t0 + i : A.ds->ent_token[ent0 + t0 + i]) : 0;
+            const int tok = !valid ? 0 : shared ? t0 + i : A.nt == 1 ? 0 : A.ds->ent_token[ent0 + t0 + i];
 #pragma unroll
-            for (int c = 0; c < CPL; c++) q4k_load_slice(xs[c][i], A.x + (size_t)tok[i] * A.D, koff[c], valid);
+            for (int c = 0; c < CPL; c++) q4k_load_slice(xs[i][c], A.x + (size_t)tok * A.D, q4k_koff(lane + 64 * c), valid);
         }
-        uint4 qg[RPW][CPL], hg[RPW][CPL], qu[RPW][CPL], hu[RPW][CPL];
+        float v[TC][2 * RPW];
+#pragma unroll
+        for (int i = 0; i < TC; i++)
+#pragma unroll
+            for (int r = 0; r < 2 * RPW; r++) v[i][r] = 0.0f;
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const size_t rowoff = (size_t)(row0 + r) * A.rb;
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
-                qg[r][c] = qg_ld16(G + rowoff + qoff[c]); hg[r][c] = qg_ld16(G + rowoff + hoff[c]);
-                qu[r][c] = qg_ld16(U + rowoff + qoff[c]); hu[r][c] = qg_ld16(U + rowoff + hoff[c]);
+                const int q = (lane + 64 * c) & 7;
+                Q4kVals vals;
+                q4k_unpack(vals, qg[r][c]);
+                const Q4kScale sg = q4k_scale(hg[r][c], q);
+#pragma unroll
+                for (int i = 0; i < TC; i++) v[i][r] = q4k_dot(v[i][r], vals, sg, xs[i][c]);
+                q4k_unpack(vals, qu[r][c]);
+                const Q4kScale su = q4k_scale(hu[r][c], q);
+#pragma unroll
+                for (int i = 0; i < TC; i++) v[i][RPW + r] = q4k_dot(v[i][RPW + r], vals, su, xs[i][c]);
             }
         }
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            float pg[TC], pu[TC];
-#pragma unroll
-            for (int i = 0; i < TC; i++) { pg[i] = 0.0f; pu[i] = 0.0f; }
-#pragma unroll
-            for (int c = 0; c < CPL; c++) {
-                q4k_chunk_dot<TC>(pg, qg[r][c], q4k_scale(hg[r][c], qsel[c]), xs[c]);
-                q4k_chunk_dot<TC>(pu, qu[r][c], q4k_scale(hu[r][c], qsel[c]), xs[c]);
-            }
-            float gsel = 0.0f, usel = 0.0f;
-#pragma unroll
-            for (int i = 0; i < TC; i++) {
-                const float g = group_sum<64>(pg[i]), u = group_sum<64>(pu[i]);
-                if (lane == i) { gsel = g; usel = u; }
-            }
-            if (lane < TC && t0 + lane < n) {
-                const int row = row0 + r;
-                const float m = qg_swiglu(gsel, usel);
-                if (shared) A.mid[(size_t)(MAXS + t0 + lane) * A.F + row] = m;
+        for (int i = 0; i < TC; i++) {
+            const float s = reduce8(v[i], lane);          // gate (bit5=0) or up (bit5=1) row (lane>>3)&3
+            const float u = __shfl_xor(s, 32);
+            if ((lane & 39) == 0 && t0 + i < n) {
+                const int row = row0 + ((lane >> 3) & 3);
+                const float m = qg_swiglu(s, u);
+                if (shared) A.mid[(size_t)(MAXS + t0 + i) * A.F + row] = m;
                 else {
-                    const int ent = ent0 + t0 + lane;
+                    const int ent = ent0 + t0 + i;
                     A.mid[(size_t)ent * A.F + row] = m;
                     if (A.mid_slot) A.mid_slot[(size_t)A.ds->ent_slot[ent] * A.F + row] = m;
                 }
@@ -402,7 +413,7 @@ __global__ __launch_bounds__(256) void gateup_q4k_kernel(GateUpArgs A) {
     }
 }
 
-// ---------------- kernel 4: down + weighted slots + rank-order combine ----------------
+// ---------------- kernel 4: down -> weighted slot rows ----------------
 struct DownArgs {
     int nt, D, F, maxa;
     const uint8_t *down, *sh_down;
@@ -412,16 +423,12 @@ struct DownArgs {
     const float *route_w;      // [nt][10] after pruning
     float *slots;              // workspace [MAXS+MAXB][D] (entry-indexed)
     float *slots_out;          // slot mode: caller's [(t*10+k)][D], or null
-    int *arrive;               // per row block arrival counters (fused mode)
-    const float *sh_logit;     // logits + 512, stride ld
-    int ld;
-    float *out;                // [nt][D] (fused mode)
 };
 
 // IQ4_NL: 8 lanes per 512-column row, a lane owns a pair of 18-byte blocks
 // (64 columns).  The table is shifted by +128 to unsigned bytes so v_perm can
-// look it up and cvt_f32_ubyte can convert; the shift is removed with the
-// block's x sum.
+// look it up and cvt_f32_ubyte convert; the shift is removed with the block's
+// x sum.
 QG_DEV uint32_t iq4_lookup(uint32_t idx) {
     // lut + 128 = {1,24,45,63, 79,93,106,118, 129,141,153,166, 181,197,217,241}
     const uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
@@ -433,13 +440,7 @@ QG_DEV uint32_t iq4_lookup(uint32_t idx) {
 
 struct Iq4Slice { float v[64]; float s0, s1; };
 
-QG_DEV void iq4_load_slice(Iq4Slice &s, const float *xrow, int koff, bool valid) {
-    if (!valid) {
-#pragma unroll
-        for (int i = 0; i < 64; i++) s.v[i] = 0.0f;
-        s.s0 = s.s1 = 0.0f;
-        return;
-    }
+QG_DEV void iq4_load_slice(Iq4Slice &s, const float *xrow, int koff) {
     const float4 *p = (const float4 *)(xrow + koff);
 #pragma unroll
     for (int i = 0; i < 16; i++) { const float4 f = p[i]; s.v[4*i] = f.x; s.v[4*i+1] = f.y; s.v[4*i+2] = f.z; s.v[4*i+3] = f.w; }
@@ -459,16 +460,15 @@ QG_DEV Iq4Raw iq4_load(const uint8_t *p) {
     for (int i = 0; i < 9; i++) r.w[i] = q[i];
     return r;
 }
-
-template <int TC>
-QG_DEV void iq4_pair_dot(float (&part)[TC], const Iq4Raw &r, const Iq4Slice (&xs)[TC]) {
-    const float d0 = qg_half_u16(r.w[0] & 0xffffu), d1 = qg_half_u16(r.w[4] >> 16);
+struct Iq4Vals { float val[64]; float d0, d1; };
+QG_DEV void iq4_unpack(Iq4Vals &v, const Iq4Raw &r) {
+    v.d0 = qg_half_u16(r.w[0] & 0xffffu);
+    v.d1 = qg_half_u16(r.w[4] >> 16);
     uint32_t qs[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) qs[i] = __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
 #pragma unroll
     for (int i = 0; i < 4; i++) qs[4 + i] = r.w[5 + i];
-    float val[64];
 #pragma unroll
     for (int blk = 0; blk < 2; blk++) {
 #pragma unroll
@@ -477,142 +477,326 @@ QG_DEV void iq4_pair_dot(float (&part)[TC], const Iq4Raw &r, const Iq4Slice (&xs
             const uint32_t lo = iq4_lookup(w & 0x0F0F0F0Fu), hi = iq4_lookup((w >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                val[blk * 32 + 4 * i + b] = (float)((lo >> (8 * b)) & 0xffu);
-                val[blk * 32 + 16 + 4 * i + b] = (float)((hi >> (8 * b)) & 0xffu);
+                v.val[blk * 32 + 4 * i + b] = (float)((lo >> (8 * b)) & 0xffu);
+                v.val[blk * 32 + 16 + 4 * i + b] = (float)((hi >> (8 * b)) & 0xffu);
             }
         }
     }
+}
+QG_DEV float iq4_dot(const Iq4Vals &v, const Iq4Slice &x) {
+    float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-    for (int t = 0; t < TC; t++) {
-        float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) { s0 = __builtin_fmaf(val[i], xs[t].v[i], s0); s1 = __builtin_fmaf(val[32 + i], xs[t].v[32 + i], s1); }
-        s0 = __builtin_fmaf(-128.0f, xs[t].s0, s0);
-        s1 = __builtin_fmaf(-128.0f, xs[t].s1, s1);
-        part[t] = __builtin_fmaf(d0, s0, __builtin_fmaf(d1, s1, part[t]));
-    }
+    for (int i = 0; i < 32; i++) { s0 = __builtin_fmaf(v.val[i], x.v[i], s0); s1 = __builtin_fmaf(v.val[32 + i], x.v[32 + i], s1); }
+    s0 = __builtin_fmaf(-128.0f, x.s0, s0);
+    s1 = __builtin_fmaf(-128.0f, x.s1, s1);
+    return __builtin_fmaf(v.d0, s0, v.d1 * s1);
 }
 
-// Rows [rowbase, rowbase+32) of one expert (or the shared expert).  FMT is the
-// row format: 20 (IQ4_NL, 8 lanes/row) or 12 (Q4_K, 16 lanes/row).
-template <int FMT, int TC>
+QG_DEV void down_store(const DownArgs &A, bool shared, int mrow, int row, float y) {
+    if (shared) { A.slots[(size_t)mrow * A.D + row] = y; return; }
+    const int slot = A.ds->ent_slot[mrow];
+    const float v = y * A.route_w[slot];
+    if (A.slots_out) A.slots_out[(size_t)slot * A.D + row] = v;
+    else A.slots[(size_t)mrow * A.D + row] = v;
+}
+
+// Rows [rowbase, rowbase+32) of one expert (or the shared expert) for all of
+// its tokens.  Weights are loaded and unpacked once, then reused per token.
+template <int FMT>
 QG_DEV void down_rows(const DownArgs &A, const uint8_t *W, size_t rb, int n, int ent0, bool shared, int rowbase) {
-    constexpr int LPR = FMT == QT_IQ4_NL ? 8 : 16, RPW = 64 / LPR, PASSES = ROWS_DOWN / (4 * RPW);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane % LPR, rsub = lane / LPR;
-    for (int t0 = 0; t0 < n; t0 += TC) {
-        int mrow[TC];
-        bool valid[TC];
-#pragma unroll
-        for (int i = 0; i < TC; i++) {
-            valid[i] = t0 + i < n;
-            mrow[i] = valid[i] ? (shared ? MAXS + t0 + i : ent0 + t0 + i) : 0;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (FMT == QT_IQ4_NL) {
+        const int c = lane & 7, row = rowbase + wave * 8 + (lane >> 3);
+        Iq4Vals vals;
+        iq4_unpack(vals, iq4_load(W + (size_t)row * rb + 36 * c));
+        for (int t = 0; t < n; t++) {
+            const int mrow = shared ? MAXS + t : ent0 + t;
+            Iq4Slice xs;
+            iq4_load_slice(xs, A.mid + (size_t)mrow * A.F, 64 * c);
+            const float y = group_sum<8>(iq4_dot(vals, xs));
+            if (c == 0) down_store(A, shared, mrow, row, y);
         }
-        if (FMT == QT_IQ4_NL) {
-            Iq4Slice xs[TC];
-#pragma unroll
-            for (int i = 0; i < TC; i++) iq4_load_slice(xs[i], A.mid + (size_t)mrow[i] * A.F, 64 * c, valid[i]);
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ps++) {
-                const int row = rowbase + (ps * 4 + wave) * RPW + rsub;
-                const Iq4Raw raw = iq4_load(W + (size_t)row * rb + 36 * c);
-                float part[TC];
-#pragma unroll
-                for (int i = 0; i < TC; i++) part[i] = 0.0f;
-                iq4_pair_dot<TC>(part, raw, xs);
-#pragma unroll
-                for (int i = 0; i < TC; i++) {
-                    const float y = group_sum<LPR>(part[i]);
-                    if (c == i && valid[i]) {
-                        if (shared) A.slots[(size_t)mrow[i] * A.D + row] = y;
-                        else {
-                            const int slot = A.ds->ent_slot[mrow[i]];
-                            const float v = y * A.route_w[slot];
-                            if (A.slots_out) A.slots_out[(size_t)slot * A.D + row] = v;
-                            else A.slots[(size_t)mrow[i] * A.D + row] = v;
-                        }
-                    }
-                }
-            }
-        } else {
-            Q4kSlice xs[1][TC];
-            const int koff = q4k_koff(c);
-#pragma unroll
-            for (int i = 0; i < TC; i++) q4k_load_slice(xs[0][i], A.mid + (size_t)mrow[i] * A.F, koff, valid[i]);
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ps++) {
-                const int row = rowbase + (ps * 4 + wave) * RPW + rsub;
-                const uint8_t *rp = W + (size_t)row * rb;
-                const uint4 qv = qg_ld16(rp + q4k_qoff(c)), hd = qg_ld16(rp + q4k_hoff(c));
-                float part[TC];
-#pragma unroll
-                for (int i = 0; i < TC; i++) part[i] = 0.0f;
-                q4k_chunk_dot<TC>(part, qv, q4k_scale(hd, c & 7), xs[0]);
-#pragma unroll
-                for (int i = 0; i < TC; i++) {
-                    const float y = group_sum<LPR>(part[i]);
-                    if (c == i && valid[i]) {
-                        if (shared) A.slots[(size_t)mrow[i] * A.D + row] = y;
-                        else {
-                            const int slot = A.ds->ent_slot[mrow[i]];
-                            const float v = y * A.route_w[slot];
-                            if (A.slots_out) A.slots_out[(size_t)slot * A.D + row] = v;
-                            else A.slots[(size_t)mrow[i] * A.D + row] = v;
-                        }
-                    }
-                }
-            }
+    } else {
+        const int c = lane & 15;
+        const int rowA = rowbase + wave * 8 + (lane >> 4), rowB = rowA + 4;
+        const uint8_t *pa = W + (size_t)rowA * rb, *pb = W + (size_t)rowB * rb;
+        const uint4 qa = qg_ld16(pa + q4k_qoff(c)), ha = qg_ld16(pa + q4k_hoff(c));
+        const uint4 qb = qg_ld16(pb + q4k_qoff(c)), hb = qg_ld16(pb + q4k_hoff(c));
+        Q4kVals va, vb;
+        q4k_unpack(va, qa);
+        q4k_unpack(vb, qb);
+        const Q4kScale sa = q4k_scale(ha, c & 7), sb = q4k_scale(hb, c & 7);
+        for (int t = 0; t < n; t++) {
+            const int mrow = shared ? MAXS + t : ent0 + t;
+            Q4kSlice xs;
+            q4k_load_slice(xs, A.mid + (size_t)mrow * A.F, q4k_koff(c), true);
+            const float ya = group_sum<16>(q4k_dot(0.0f, va, sa, xs));
+            const float yb = group_sum<16>(q4k_dot(0.0f, vb, sb, xs));
+            if (c == 0) { down_store(A, shared, mrow, rowA, ya); down_store(A, shared, mrow, rowB, yb); }
         }
     }
 }
 
-// Sum the 10 weighted slots of each token in router-rank order from 0.0f
-// (gpu.cu:521-527, cpu.c:227-230; pruned ranks add +0), then add the
-// sigmoid-gated shared expert with one fma (gpu.cu:552).  Tokens flagged
-// handoff/invalid get a zero row.
-QG_DEV void combine_rows(const DownArgs &A, int rowbase) {
-    const int has_shared = A.ds->has_shared;
-    for (int idx = threadIdx.x; idx < A.nt * ROWS_DOWN; idx += 256) {
-        const int t = idx / ROWS_DOWN, d = rowbase + idx % ROWS_DOWN;
-        float acc = 0.0f;
-        const int flag = A.ds->tok_flag[t];
-        if (flag < 2) {
-#pragma unroll
-            for (int k = 0; k < QG_TOP; k++) {
-                const int se = A.ds->slot_ent[t * QG_TOP + k];
-                acc += se >= 0 ? A.slots[(size_t)se * A.D + d] : 0.0f;
-            }
-            if (has_shared)
-                acc = __builtin_fmaf(A.slots[(size_t)(MAXS + t) * A.D + d],
-                                     qg_sig(A.sh_logit[(size_t)t * A.ld]), acc);
-        }
-        A.out[(size_t)t * A.D + d] = acc;
-    }
-}
-
-template <int FR, int FS, int TC>
+template <int FR, int FS>
 __global__ __launch_bounds__(256) void down_kernel(DownArgs A) {
     const int a = blockIdx.x, rowbase = blockIdx.y * ROWS_DOWN;
-    const bool shared = A.sh_down && a == A.maxa;
-    if (shared) down_rows<FS, TC>(A, A.sh_down, A.sh_rb, A.nt, 0, true, rowbase);
-    else {
-        if (a >= A.ds->n_active) return;
-        const int e = A.ds->act_expert[a], ent0 = A.ds->act_off[a], n = A.ds->act_off[a + 1] - ent0;
-        down_rows<FR, TC>(A, A.down + (size_t)e * A.D * A.rb, A.rb, n, ent0, false, rowbase);
+    if (A.sh_down && a == A.maxa) { down_rows<FS>(A, A.sh_down, A.sh_rb, A.nt, 0, true, rowbase); return; }
+    if (a >= A.ds->n_active) return;
+    const int4 info = A.ds->act[a];
+    down_rows<FR>(A, A.down + (size_t)info.x * A.D * A.rb, A.rb, info.z, info.y, false, rowbase);
+}
+
+// ---------------- kernel 5: router-rank combine + shared expert ----------------
+// out[t,d] = sum over k=0..9 of the weighted slots from 0.0f in router-rank
+// order (gpu.cu:521-527, cpu.c:227-230; pruned ranks add +0), then the
+// sigmoid-gated shared expert added with one fma (gpu.cu:552).  Tokens
+// flagged handoff/invalid get a zero row.
+__global__ __launch_bounds__(256) void combine_kernel(float *out, const float *slots, const Disp *ds, const float *sh_logit,
+                                                      int ld, int nt, int D) {
+    const int i = blockIdx.x * 256 + threadIdx.x, q = D / 4;
+    if (i >= nt * q) return;
+    const int t = i / q, d4 = (i % q) * 4;
+    int se[QG_TOP];
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) se[k] = ds->slot_ent[t * QG_TOP + k];  // issued together
+    const int flag = ds->tok_flag[t], has_shared = ds->has_shared;
+    const float g = has_shared ? qg_sig(sh_logit[(size_t)t * ld]) : 0.0f;
+    float4 v[QG_TOP];
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++)
+        v[k] = *(const float4 *)(slots + (size_t)(se[k] >= 0 ? se[k] : 0) * D + d4);
+    const float4 s = *(const float4 *)(slots + (size_t)(MAXS + t) * D + d4);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (flag < 2) {
+#pragma unroll
+        for (int k = 0; k < QG_TOP; k++) {
+            const bool ok = se[k] >= 0;
+            acc.x += ok ? v[k].x : 0.0f; acc.y += ok ? v[k].y : 0.0f; acc.z += ok ? v[k].z : 0.0f; acc.w += ok ? v[k].w : 0.0f;
+        }
+        if (has_shared) {
+            acc.x = __builtin_fmaf(s.x, g, acc.x); acc.y = __builtin_fmaf(s.y, g, acc.y);
+            acc.z = __builtin_fmaf(s.z, g, acc.z); acc.w = __builtin_fmaf(s.w, g, acc.w);
+        }
     }
-    if (!A.out) return;
-    // Last block of this row block combines (release/acquire at agent scope).
-    __shared__ int s_last;
-    __threadfence();
+    *(float4 *)(out + (size_t)t * D + d4) = acc;
+}
+
+// ---------------- small-batch path (1..4 tokens): 3 kernels per layer ----------------
+// router -> gate/up (every block re-derives the routing from the logits, so
+// no dispatch kernel or host round trip is needed) -> down + combine (each
+// block owns 8 output rows for every selected expert, so the router-rank sum
+// is formed in LDS without a separate combine pass).
+constexpr int SMALL_B = 4;
+constexpr int SMALL_S = SMALL_B * QG_TOP;
+
+struct SmallArgs {
+    const float *x;
+    int nt, D, F;
+    const float *logits; int ld;            // router output, row stride 512 or 513
+    const uint8_t *resident; double thr;
+    const uint8_t *gate, *up, *sh_gate, *sh_up;
+    size_t rb;
+    float *mid;                             // [MAXS+MAXB][F]: slot-indexed rows, shared at MAXS+t
+    int *ids_out; float *w_out; uint8_t *flags_out; qg_prune_stats *stats;
+    int *tok_flag;                          // [MAXB] for the down kernel
+};
+
+// Routing of all tokens (wave w routes token w) plus coverage/pruning
+// (gpu.cu:470-478) into LDS.  Called by every thread of the block.
+QG_DEV void small_route(const SmallArgs &A, int *s_ids, float *s_w, int *s_flag, int *s_missing, double *s_mass) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (wave < A.nt) qg_route_wave(s_ids + wave * QG_TOP, s_w + wave * QG_TOP, A.logits + (size_t)wave * A.ld, lane);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int expected = A.ds->n_active + (A.sh_down ? 1 : 0);
-        s_last = atomicAdd(&A.arrive[blockIdx.y], 1) == expected - 1;
+    if (tid < A.nt) {
+        const int t = tid;
+        int missing = 0, bad = 0;
+        double mass = 0;
+        for (int k = 0; k < QG_TOP; k++) {
+            const int e = s_ids[t * QG_TOP + k];
+            if (e < 0 || e >= QG_EXPERTS) { bad = 1; break; }
+            if (A.resident && !A.resident[e]) { missing++; mass += (double)s_w[t * QG_TOP + k]; }
+        }
+        const int flag = bad ? 3 : !missing ? 0 : (A.thr > 0 && mass < A.thr) ? 1 : 2;
+        if (flag == 1)
+            for (int k = 0; k < QG_TOP; k++) {
+                const int e = s_ids[t * QG_TOP + k];
+                if (!A.resident[e]) { s_ids[t * QG_TOP + k] = -e - 2; s_w[t * QG_TOP + k] = 0.0f; }
+            }
+        s_flag[t] = flag;
+        s_missing[t] = missing;
+        s_mass[t] = mass;
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    combine_rows(A, rowbase);
-    if (threadIdx.x == 0) A.arrive[blockIdx.y] = 0;
+}
+
+// Block (a, rows): a < nt*10 is selection (t,k) = (a/10, a%10); it computes
+// the expert only if this is the expert's first eligible selection, for every
+// token that chose it (at most one selection per token).  a == nt*10 is the
+// shared expert.  mid rows are slot-indexed: row t*10+k for every selection.
+__global__ __launch_bounds__(256) void gateup_small_kernel(SmallArgs A) {
+    constexpr int RPW = 4;
+    __shared__ int s_ids[SMALL_S], s_flag[SMALL_B], s_missing[SMALL_B];
+    __shared__ float s_w[SMALL_S];
+    __shared__ double s_mass[SMALL_B];
+    const int a = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool shared = A.sh_gate && a == A.nt * QG_TOP;
+    int tok[SMALL_B], slot[SMALL_B], n = 0;
+    const uint8_t *G, *U;
+    if (shared) {
+        n = A.nt;
+        for (int i = 0; i < SMALL_B; i++) { tok[i] = i < A.nt ? i : 0; slot[i] = MAXS + i; }
+        G = A.sh_gate; U = A.sh_up;
+    } else {
+        small_route(A, s_ids, s_w, s_flag, s_missing, s_mass);
+        if (a == 0 && blockIdx.y == 0) {
+            const int tid = threadIdx.x;
+            if (tid < A.nt * QG_TOP) { A.ids_out[tid] = s_ids[tid]; A.w_out[tid] = s_w[tid]; }
+            if (tid < A.nt) { A.tok_flag[tid] = s_flag[tid]; if (A.flags_out) A.flags_out[tid] = (uint8_t)s_flag[tid]; }
+            if (tid == 0 && A.resident && A.stats)
+                for (int t = 0; t < A.nt; t++) {
+                    if (s_flag[t] == 3) continue;
+                    A.stats->token_layers += 1;
+                    A.stats->missing_selections += (uint64_t)s_missing[t];
+                    if (s_flag[t] == 1) {
+                        A.stats->skipped_selections += (uint64_t)s_missing[t];
+                        A.stats->avoided_token_handoffs += 1;
+                        A.stats->skipped_mass += s_mass[t];
+                    }
+                }
+        }
+        const int e = s_ids[a];
+        const bool elig_a = e >= 0 && e < QG_EXPERTS && s_flag[a / QG_TOP] < 2;
+        if (!elig_a) return;
+        const int i = lane < SMALL_S ? lane : SMALL_S - 1;
+        const bool same = lane < A.nt * QG_TOP && s_ids[i] == e && s_flag[i / QG_TOP] < 2;
+        unsigned long long m = __ballot(same);
+        if (m & ((1ULL << a) - 1ULL)) return;  // an earlier selection owns this expert
+        while (m) {
+            const int s = __builtin_ctzll(m);
+            m &= m - 1;
+            tok[n] = s / QG_TOP; slot[n] = s; n++;
+        }
+        G = A.gate + (size_t)e * A.F * A.rb;
+        U = A.up + (size_t)e * A.F * A.rb;
+    }
+    const int row0 = (blockIdx.y * 4 + wave) * RPW;
+    const int ch = lane, q = ch & 7;
+    uint4 qg[RPW], hg[RPW], qu[RPW], hu[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const size_t rowoff = (size_t)(row0 + r) * A.rb;
+        qg[r] = qg_ld16(G + rowoff + q4k_qoff(ch)); hg[r] = qg_ld16(G + rowoff + q4k_hoff(ch));
+        qu[r] = qg_ld16(U + rowoff + q4k_qoff(ch)); hu[r] = qg_ld16(U + rowoff + q4k_hoff(ch));
+    }
+    for (int i = 0; i < n; i++) {
+        Q4kSlice xs;
+        q4k_load_slice(xs, A.x + (size_t)tok[i] * A.D, q4k_koff(ch), true);
+        float v[2 * RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            Q4kVals vals;
+            q4k_unpack(vals, qg[r]);
+            v[r] = q4k_dot(0.0f, vals, q4k_scale(hg[r], q), xs);
+            q4k_unpack(vals, qu[r]);
+            v[RPW + r] = q4k_dot(0.0f, vals, q4k_scale(hu[r], q), xs);
+        }
+        const float sum = reduce8(v, lane);
+        const float u = __shfl_xor(sum, 32);
+        if ((lane & 39) == 0) A.mid[(size_t)slot[i] * A.F + row0 + ((lane >> 3) & 3)] = qg_swiglu(sum, u);
+    }
+}
+
+struct DownSmallArgs {
+    int nt, D, F;
+    const int *ids; const float *w; const int *tok_flag;
+    const uint8_t *down, *sh_down;
+    size_t rb, sh_rb;
+    const float *sh_logit; int ld;
+    const float *mid;
+    float *out;
+};
+
+// y for 8 consecutive rows starting at `row0` of one item (routed expert or
+// shared), from mid row `mrow`; lane results land in vals[item][0..7].
+template <int FMT>
+QG_DEV void down8(const DownSmallArgs &A, const uint8_t *W, size_t rb, int row0, int mrow, float *vals_item) {
+    const int lane = threadIdx.x & 63;
+    if (FMT == QT_IQ4_NL) {
+        const int c = lane & 7, r = lane >> 3;
+        const Iq4Raw raw = iq4_load(W + (size_t)(row0 + r) * rb + 36 * c);
+        Iq4Slice xs;
+        iq4_load_slice(xs, A.mid + (size_t)mrow * A.F, 64 * c);
+        Iq4Vals vv;
+        iq4_unpack(vv, raw);
+        const float y = qg_oct_sum(iq4_dot(vv, xs));
+        if (c == 0) vals_item[r] = y;
+    } else {
+        const int c = lane & 15, r = lane >> 4;
+        const uint8_t *pa = W + (size_t)(row0 + r) * rb, *pb = W + (size_t)(row0 + 4 + r) * rb;
+        const uint4 qa = qg_ld16(pa + q4k_qoff(c)), ha = qg_ld16(pa + q4k_hoff(c));
+        const uint4 qb = qg_ld16(pb + q4k_qoff(c)), hb = qg_ld16(pb + q4k_hoff(c));
+        Q4kSlice xs;
+        q4k_load_slice(xs, A.mid + (size_t)mrow * A.F, q4k_koff(c), true);
+        Q4kVals v;
+        q4k_unpack(v, qa);
+        const float ya = qg_row_sum(q4k_dot(0.0f, v, q4k_scale(ha, c & 7), xs));
+        q4k_unpack(v, qb);
+        const float yb = qg_row_sum(q4k_dot(0.0f, v, q4k_scale(hb, c & 7), xs));
+        if (c == 0) { vals_item[r] = ya; vals_item[4 + r] = yb; }
+    }
+}
+
+template <int FR, int FS>
+__global__ __launch_bounds__(256) void down_small_kernel(DownSmallArgs A) {
+    __shared__ float vals[SMALL_S + SMALL_B][8];
+    __shared__ int s_item[SMALL_S + SMALL_B];
+    __shared__ int s_nitems;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, row0 = blockIdx.x * 8;
+    if (wave == 0) {
+        // items in ascending order: eligible routed slots, then shared rows
+        const int ns = A.nt * QG_TOP;
+        bool el = false;
+        if (lane < ns) {
+            const int e = A.ids[lane];
+            el = e >= 0 && e < QG_EXPERTS && A.tok_flag[lane / QG_TOP] < 2;
+        }
+        const unsigned long long m = __ballot(el);
+        if (el) s_item[__popcll(m & ((1ULL << lane) - 1ULL))] = lane;
+        int n = __popcll(m);
+        const bool sh = A.sh_down && lane < A.nt && A.tok_flag[lane] < 2;
+        const unsigned long long ms = __ballot(sh);
+        if (sh) s_item[n + __popcll(ms & ((1ULL << lane) - 1ULL))] = MAXS + lane;
+        n += __popcll(ms);
+        if (lane == 0) s_nitems = n;
+    }
+    __syncthreads();
+    const int nitems = s_nitems;
+    for (int it = wave; it < nitems; it += 4) {
+        const int s = s_item[it];
+        if (s < MAXS) down8<FR>(A, A.down + (size_t)A.ids[s] * A.D * A.rb, A.rb, row0, s, vals[it]);
+        else down8<FS>(A, A.sh_down, A.sh_rb, row0, s, vals[it]);
+    }
+    __syncthreads();
+    if (tid < A.nt * 8) {
+        const int t = tid >> 3, r = tid & 7;
+        float acc = 0.0f;
+        if (A.tok_flag[t] < 2) {
+            int it = 0;
+            while (it < nitems && s_item[it] < t * QG_TOP) it++;
+            for (int k = 0; k < QG_TOP; k++) {
+                const int s = t * QG_TOP + k;
+                float v = 0.0f;
+                if (it < nitems && s_item[it] == s) { v = vals[it][r] * A.w[s]; it++; }
+                acc += v;
+            }
+            if (A.sh_down) {
+                int sh = 0;
+                while (sh < nitems && s_item[sh] != MAXS + t) sh++;
+                acc = __builtin_fmaf(vals[sh][r], qg_sig(A.sh_logit[(size_t)t * A.ld]), acc);
+            }
+        }
+        A.out[(size_t)t * A.D + row0 + r] = acc;
+    }
 }
 
 // ---------------- generic fallback (any format, any width) ----------------
@@ -643,12 +827,12 @@ __global__ __launch_bounds__(64) void gateup_generic_kernel(GenericArgs A) {
     if (shared) { n = A.nt; G = A.sh_gate; U = A.sh_up; gt = A.sgt; ut = A.sut; grb = A.sgrb; urb = A.surb; }
     else {
         if (a >= A.ds->n_active) return;
-        const int e = A.ds->act_expert[a];
-        ent0 = A.ds->act_off[a];
-        n = A.ds->act_off[a + 1] - ent0;
+        const int4 info = A.ds->act[a];
+        ent0 = info.y;
+        n = info.z;
         gt = A.gt; ut = A.ut; grb = A.grb; urb = A.urb;
-        G = A.gate + (size_t)e * A.F * grb;
-        U = A.up + (size_t)e * A.F * urb;
+        G = A.gate + (size_t)info.x * A.F * grb;
+        U = A.up + (size_t)info.x * A.F * urb;
     }
     for (int i = 0; i < n; i++) {
         const int tok = shared ? i : A.ds->ent_token[ent0 + i];
@@ -669,59 +853,58 @@ struct GenericDownArgs { DownArgs d; int dt, sdt; };
 
 __global__ __launch_bounds__(64) void down_generic_kernel(GenericDownArgs G) {
     const DownArgs &A = G.d;
-    const int a = blockIdx.x, half = threadIdx.x >> 5, j = threadIdx.x & 31;
-    const int rowbase = blockIdx.y * 2, row = rowbase + half;
-    const bool shared = A.sh_down && a == A.maxa;
-    bool active = true;
-    if (shared) {
-        if (row < A.D)
-            for (int t = 0; t < A.nt; t++) {
-                const float y = exact_dot(A.sh_down + (size_t)row * A.sh_rb, G.sdt, A.F, A.mid + (size_t)(MAXS + t) * A.F, j);
-                if (j == 0) A.slots[(size_t)(MAXS + t) * A.D + row] = y;
-            }
-    } else if (a < A.ds->n_active) {
-        const int e = A.ds->act_expert[a], ent0 = A.ds->act_off[a], n = A.ds->act_off[a + 1] - ent0;
-        const uint8_t *W = A.down + (size_t)e * A.D * A.rb;
-        if (row < A.D)
-            for (int i = 0; i < n; i++) {
-                const int ent = ent0 + i;
-                const float y = exact_dot(W + (size_t)row * A.rb, G.dt, A.F, A.mid + (size_t)ent * A.F, j);
-                if (j == 0) {
-                    const int slot = A.ds->ent_slot[ent];
-                    const float v = y * A.route_w[slot];
-                    if (A.slots_out) A.slots_out[(size_t)slot * A.D + row] = v;
-                    else A.slots[(size_t)ent * A.D + row] = v;
-                }
-            }
-    } else active = false;
-    if (!A.out || !active) return;
-    __shared__ int s_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int expected = A.ds->n_active + (A.sh_down ? 1 : 0);
-        s_last = atomicAdd(&A.arrive[blockIdx.y], 1) == expected - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int has_shared = A.ds->has_shared;
-    for (int idx = threadIdx.x; idx < A.nt * 2; idx += 64) {
-        const int t = idx / 2, d = rowbase + idx % 2;
-        if (d >= A.D) continue;
-        float acc = 0.0f;
-        if (A.ds->tok_flag[t] < 2) {
-            for (int k = 0; k < QG_TOP; k++) {
-                const int se = A.ds->slot_ent[t * QG_TOP + k];
-                acc += se >= 0 ? A.slots[(size_t)se * A.D + d] : 0.0f;
-            }
-            if (has_shared)
-                acc = __builtin_fmaf(A.slots[(size_t)(MAXS + t) * A.D + d],
-                                     qg_sig(A.sh_logit[(size_t)t * A.ld]), acc);
+    const int a = blockIdx.x, half = threadIdx.x >> 5, j = threadIdx.x & 31, row = blockIdx.y * 2 + half;
+    if (row >= A.D) return;
+    if (A.sh_down && a == A.maxa) {
+        for (int t = 0; t < A.nt; t++) {
+            const float y = exact_dot(A.sh_down + (size_t)row * A.sh_rb, G.sdt, A.F, A.mid + (size_t)(MAXS + t) * A.F, j);
+            if (j == 0) A.slots[(size_t)(MAXS + t) * A.D + row] = y;
         }
-        A.out[(size_t)t * A.D + d] = acc;
+        return;
     }
-    if (threadIdx.x == 0) A.arrive[blockIdx.y] = 0;
+    if (a >= A.ds->n_active) return;
+    const int4 info = A.ds->act[a];
+    const uint8_t *W = A.down + (size_t)info.x * A.D * A.rb;
+    for (int i = 0; i < info.z; i++) {
+        const int ent = info.y + i;
+        const float y = exact_dot(W + (size_t)row * A.rb, G.dt, A.F, A.mid + (size_t)ent * A.F, j);
+        if (j == 0) down_store(A, false, ent, row, y);
+    }
+}
+
+bool small_path_ok(const qg_moe_layer *L, int nt) {
+    const bool sh = L->sh_gate != nullptr;
+    return nt <= SMALL_B && L->width == 2048 && L->ff == 512 && L->gate_type == QT_Q4_K && L->up_type == QT_Q4_K &&
+           (L->down_type == QT_Q4_K || L->down_type == QT_IQ4_NL) &&
+           (!sh || (L->sh_gate_type == QT_Q4_K && L->sh_up_type == QT_Q4_K &&
+                    (L->sh_down_type == QT_Q4_K || L->sh_down_type == QT_IQ4_NL)));
+}
+
+int launch_small(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
+                 const qg_moe_layer *L, const float *logits, int ld, Disp *ds, float *mid, hipStream_t s) {
+    const bool sh = L->sh_gate != nullptr;
+    SmallArgs A{x, nt, L->width, L->ff, logits, ld, L->resident, L->threshold,
+                (const uint8_t *)L->gate, (const uint8_t *)L->up, sh ? (const uint8_t *)L->sh_gate : nullptr,
+                sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, L->width), mid,
+                ids, weights, flags, stats, ds->tok_flag};
+    gateup_small_kernel<<<dim3(nt * QG_TOP + (sh ? 1 : 0), L->ff / 16), 256, 0, s>>>(A);
+    int rc = hipGetLastError();
+    if (rc) return rc;
+    phase_mark(2, s);
+    phase_mark(3, s);
+    DownSmallArgs D{nt, L->width, L->ff, ids, weights, ds->tok_flag, (const uint8_t *)L->down,
+                    sh ? (const uint8_t *)L->sh_down : nullptr, qg_row_bytes_host(L->down_type, L->ff),
+                    sh ? qg_row_bytes_host(L->sh_down_type, L->ff) : 0, logits + QG_EXPERTS, ld, mid, out};
+    const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
+    const dim3 grid(L->width / 8);
+    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) down_small_kernel<QT_IQ4_NL, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
+    else if (fr == QT_IQ4_NL) down_small_kernel<QT_IQ4_NL, QT_Q4_K><<<grid, 256, 0, s>>>(D);
+    else if (fs == QT_IQ4_NL) down_small_kernel<QT_Q4_K, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
+    else down_small_kernel<QT_Q4_K, QT_Q4_K><<<grid, 256, 0, s>>>(D);
+    rc = hipGetLastError();
+    phase_mark(4, s);
+    phase_mark(5, s);
+    return rc;
 }
 
 // ---------------- expert-phase launcher shared by forward and mtp_moe ----------------
@@ -730,26 +913,20 @@ struct ExpertPhase {
     const uint8_t *gate, *up, *down; int gt, ut, dt;
     const uint8_t *sh_gate, *sh_up, *sh_down; int sgt, sut, sdt;
     Disp *ds; float *mid, *mid_slot, *slots, *slots_out; const float *route_w;
-    int *arrive; const float *sh_logit; int ld; float *out;
+    const float *sh_logit; int ld; float *out;
 };
 
 int launch_experts(const ExpertPhase &P, hipStream_t s) {
     const int maxa = P.nt * QG_TOP < QG_EXPERTS ? P.nt * QG_TOP : QG_EXPERTS;
     const int gx = maxa + (P.sh_gate ? 1 : 0);
     const bool fast_gu = P.gt == QT_Q4_K && P.ut == QT_Q4_K && (!P.sh_gate || (P.sgt == QT_Q4_K && P.sut == QT_Q4_K)) &&
-                         (P.D == 2048 || P.D == 4096) && P.F % 8 == 0;
+                         P.D == 2048 && P.F % 16 == 0;
     const bool fast_dn = (P.dt == QT_IQ4_NL || P.dt == QT_Q4_K) && (!P.sh_down || P.sdt == QT_IQ4_NL || P.sdt == QT_Q4_K) &&
                          P.F == 512 && P.D % ROWS_DOWN == 0;
     if (fast_gu) {
         GateUpArgs A{P.x, P.nt, P.D, P.F, maxa, P.gate, P.up, P.sh_gate, P.sh_up, qg_row_bytes_host(QT_Q4_K, P.D), P.ds, P.mid, P.mid_slot};
-        dim3 grid(gx, P.F / 8);
-        if (P.D == 2048) {
-            if (P.nt == 1) gateup_q4k_kernel<1, 1><<<grid, 256, 0, s>>>(A);
-            else gateup_q4k_kernel<4, 1><<<grid, 256, 0, s>>>(A);
-        } else {
-            if (P.nt == 1) gateup_q4k_kernel<1, 2><<<grid, 256, 0, s>>>(A);
-            else gateup_q4k_kernel<2, 2><<<grid, 256, 0, s>>>(A);
-        }
+        dim3 grid(gx, P.F / 16);
+        gateup_q4k_kernel<1, 1><<<grid, 256, 0, s>>>(A);
     } else {
         GenericArgs A{P.x, P.nt, P.D, P.F, maxa, P.gate, P.up, P.sh_gate, P.sh_up, P.gt, P.ut, P.sgt, P.sut,
                       qg_row_bytes_host(P.gt, P.D), qg_row_bytes_host(P.ut, P.D),
@@ -759,25 +936,29 @@ int launch_experts(const ExpertPhase &P, hipStream_t s) {
     }
     int rc = hipGetLastError();
     if (rc) return rc;
+    phase_mark(3, s);
     DownArgs D{P.nt, P.D, P.F, maxa, P.down, P.sh_down, qg_row_bytes_host(P.dt, P.F),
-               P.sh_down ? qg_row_bytes_host(P.sdt, P.F) : 0, P.ds, P.mid, P.route_w, P.slots, P.slots_out,
-               P.arrive, P.sh_logit, P.ld, P.out};
+               P.sh_down ? qg_row_bytes_host(P.sdt, P.F) : 0, P.ds, P.mid, P.route_w, P.slots, P.slots_out};
     if (fast_dn) {
         dim3 grid(gx, P.D / ROWS_DOWN);
         const int fs = P.sh_down ? P.sdt : P.dt;
-#define NB_DOWN(FR, FS)                                                                     \
-        if (P.nt == 1) down_kernel<FR, FS, 1><<<grid, 256, 0, s>>>(D);                      \
-        else down_kernel<FR, FS, 2><<<grid, 256, 0, s>>>(D);
-        if (P.dt == QT_IQ4_NL && fs == QT_IQ4_NL) { NB_DOWN(QT_IQ4_NL, QT_IQ4_NL) }
-        else if (P.dt == QT_IQ4_NL) { NB_DOWN(QT_IQ4_NL, QT_Q4_K) }
-        else if (fs == QT_IQ4_NL) { NB_DOWN(QT_Q4_K, QT_IQ4_NL) }
-        else { NB_DOWN(QT_Q4_K, QT_Q4_K) }
-#undef NB_DOWN
+        if (P.dt == QT_IQ4_NL && fs == QT_IQ4_NL) down_kernel<QT_IQ4_NL, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
+        else if (P.dt == QT_IQ4_NL) down_kernel<QT_IQ4_NL, QT_Q4_K><<<grid, 256, 0, s>>>(D);
+        else if (fs == QT_IQ4_NL) down_kernel<QT_Q4_K, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
+        else down_kernel<QT_Q4_K, QT_Q4_K><<<grid, 256, 0, s>>>(D);
     } else {
         GenericDownArgs G{D, P.dt, P.sh_down ? P.sdt : 0};
         down_generic_kernel<<<dim3(gx, (P.D + 1) / 2), 64, 0, s>>>(G);
     }
-    return hipGetLastError();
+    if ((rc = hipGetLastError())) return rc;
+    phase_mark(4, s);
+    if (P.out) {
+        const int quads = P.nt * P.D / 4;
+        combine_kernel<<<(quads + 255) / 256, 256, 0, s>>>(P.out, P.slots, P.ds, P.sh_logit, P.ld, P.nt, P.D);
+        rc = hipGetLastError();
+    }
+    phase_mark(5, s);
+    return rc;
 }
 
 // ---------------- general CSR dispatch (any token count) ----------------
@@ -801,19 +982,18 @@ __global__ __launch_bounds__(64) void csr_count_kernel(int *counts, const int *i
     for (int d = 32; d >= 1; d >>= 1) { c += __shfl_xor(c, d); dup |= __shfl_xor(dup, d); bad |= __shfl_xor(bad, d); }
     if (lane == 0) counts[e] = c | (dup << 30) | (bad << 29);
 }
-__global__ __launch_bounds__(256) void csr_scan_kernel(int *offsets, int *status, const int *counts) {
-    __shared__ int s_tmp[4];
+__global__ __launch_bounds__(QG_EXPERTS) void csr_scan_kernel(int *offsets, int *status, const int *counts) {
+    __shared__ int s_tmp[RD_THREADS / 64];
     __shared__ int s_bad;
     const int tid = threadIdx.x;
     if (tid == 0) s_bad = 0;
     __syncthreads();
-    const int w0 = counts[2 * tid], w1 = counts[2 * tid + 1];
-    if ((w0 | w1) & (3 << 29)) atomicOr(&s_bad, 1);
-    const int c0 = w0 & 0x1fffffff, c1 = w1 & 0x1fffffff;
-    const int incl = block_scan256(c0 + c1, s_tmp);
-    offsets[2 * tid] = incl - c0 - c1;
-    offsets[2 * tid + 1] = incl - c1;
-    if (tid == 255) offsets[QG_EXPERTS] = incl;
+    const int w = counts[tid];
+    if (w & (3 << 29)) atomicOr(&s_bad, 1);
+    const int c = w & 0x1fffffff;
+    const int incl = block_scan(c, s_tmp);
+    offsets[tid] = incl - c;
+    if (tid == QG_EXPERTS - 1) offsets[QG_EXPERTS] = incl;
     __syncthreads();
     if (tid == 0) *status = s_bad;
 }
@@ -840,6 +1020,13 @@ __global__ __launch_bounds__(64) void csr_fill_kernel(int *row_token, int *row_s
 
 extern "C" {
 
+int qg_moe_phase_events(void **events, int n) {
+    if (n < 0 || n > 6 || (n && !events)) return hipErrorInvalidValue;
+    for (int i = 0; i < 8; i++) tl_phase_ev[i] = i < n ? events[i] : nullptr;
+    tl_phase_n = n;
+    return hipSuccess;
+}
+
 size_t qg_moe_workspace_bytes(int width, int ff, int tokens) {
     if (width < 256 || width % 256 || width > 8192 || ff < 32 || ff % 32 || ff > 4096 || tokens < 1 || tokens > MAXB) return 0;
     return ws_layout(width, ff).total;
@@ -864,19 +1051,23 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
     float *logits = (float *)(ws + lay.logits);
     Disp *ds = (Disp *)(ws + lay.disp);
     const int rows = QG_EXPERTS + (sh ? 1 : 0);
+    phase_mark(0, s);
     int rc = qg_launch_matmul_exact(logits, (const uint8_t *)L->router, QT_F32, rows, D, x, nt,
                                     sh ? (const uint8_t *)L->sh_gate_inp : nullptr, s);
     if (rc) return rc;
-    int *arrive = (int *)(ws + lay.arrive);
-    route_dispatch_kernel<<<1, 256, 0, s>>>(ids, weights, flags, stats, logits, rows, nt, L->resident, L->threshold, ds,
-                                            arrive, D / 2 + 1, sh ? 1 : 0);
+    phase_mark(1, s);
+    if (small_path_ok(L, nt))
+        return launch_small(out, ids, weights, flags, stats, x, nt, L, logits, rows, ds, (float *)(ws + lay.mid), s);
+    route_dispatch_kernel<<<1, RD_THREADS, 0, s>>>(ids, weights, flags, stats, logits, rows, nt, L->resident, L->threshold, ds,
+                                                   sh ? 1 : 0);
     if ((rc = hipGetLastError())) return rc;
+    phase_mark(2, s);
     ExpertPhase P{x, nt, D, F,
                   (const uint8_t *)L->gate, (const uint8_t *)L->up, (const uint8_t *)L->down, L->gate_type, L->up_type, L->down_type,
                   sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr,
                   sh ? (const uint8_t *)L->sh_down : nullptr, L->sh_gate_type, L->sh_up_type, L->sh_down_type,
                   ds, (float *)(ws + lay.mid), nullptr, (float *)(ws + lay.slots), nullptr, weights,
-                  arrive, logits + QG_EXPERTS, rows, out};
+                  logits + QG_EXPERTS, rows, out};
     return launch_experts(P, s);
 }
 
@@ -908,14 +1099,18 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
     hipStream_t s = qg_stream();
     uint8_t *ws = (uint8_t *)scratch;
     Disp *ds = (Disp *)(ws + lay.disp);
-    dispatch_ids_kernel<<<1, 256, 0, s>>>(ids, nt, ds, mid, slots, D, F);
+    dispatch_ids_kernel<<<1, RD_THREADS, 0, s>>>(ids, nt, ds, mid, slots, D, F);
     int rc = hipGetLastError();
     if (rc) return rc;
+    const int saved_n = tl_phase_n;
+    tl_phase_n = 0;  // phase timing covers qg_moe_forward only
     ExpertPhase P{x, nt, D, F, (const uint8_t *)g, (const uint8_t *)u, (const uint8_t *)d, gt, ut, dt,
                   nullptr, nullptr, nullptr, 0, 0, 0,
                   ds, (float *)(ws + lay.mid), mid, (float *)(ws + lay.slots), slots, weights,
-                  nullptr, nullptr, 0, nullptr};
-    return launch_experts(P, s);
+                  nullptr, 0, nullptr};
+    rc = launch_experts(P, s);
+    tl_phase_n = saved_n;
+    return rc;
 }
 
 // CSR dispatch for any batch (histogram per expert, prefix sum, ordered fill).
@@ -926,7 +1121,7 @@ int qg_moe_dispatch(int *offsets, int *row_token, int *row_slot, int *status, co
     static thread_local int *counts = nullptr;
     if (!counts && hipMalloc((void **)&counts, QG_EXPERTS * sizeof(int)) != hipSuccess) { counts = nullptr; return hipErrorOutOfMemory; }
     csr_count_kernel<<<QG_EXPERTS, 64, 0, s>>>(counts, ids, nt);
-    csr_scan_kernel<<<1, 256, 0, s>>>(offsets, status, counts);
+    csr_scan_kernel<<<1, QG_EXPERTS, 0, s>>>(offsets, status, counts);
     csr_fill_kernel<<<QG_EXPERTS, 64, 0, s>>>(row_token, row_slot, offsets, ids, nt);
     return hipGetLastError();
 }

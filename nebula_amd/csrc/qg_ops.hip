@@ -22,11 +22,15 @@ namespace {
 template <int TT>
 struct Acc { float v[TT]; };
 
+// Branch-free so that the loads of a chunk can all be in flight: tokens past
+// the tile's end re-read the last valid row and their sums are never stored.
 template <int TT>
 QG_DEV void acc_step(Acc<TT> &a, float w, const float *x, size_t cols, int k, int n) {
 #pragma unroll
-    for (int t = 0; t < TT; t++)
-        if (t < n) a.v[t] = __builtin_fmaf(w, x[(size_t)t * cols + k], a.v[t]);
+    for (int t = 0; t < TT; t++) {
+        const int tt = t < n ? t : n - 1;
+        a.v[t] = __builtin_fmaf(w, x[(size_t)tt * cols + k], a.v[t]);
+    }
 }
 
 template <int TYPE, int TT>
@@ -43,8 +47,19 @@ __global__ __launch_bounds__(64) void mm_exact_kernel(float *__restrict__ out, c
 #pragma unroll
     for (int t = 0; t < TT; t++) a.v[t] = 0.0f;
     if (TYPE == QT_F32) {
+        // Issue a whole chunk of weight (and x) loads before the dependent
+        // FMAs so the GEMV is not one memory round trip per 32 columns.
+        constexpr int CH = TT == 1 ? 64 : TT == 4 ? 32 : 8;
         const float *wf = (const float *)wr;
-        for (int k = 0; k < cols; k += 32) acc_step<TT>(a, wf[k + j], xb, cols, k + j, n);
+        int k = 0;
+        for (; k + 32 * CH <= cols; k += 32 * CH) {
+            float wv[CH];
+#pragma unroll
+            for (int i = 0; i < CH; i++) wv[i] = wf[k + 32 * i + j];
+#pragma unroll
+            for (int i = 0; i < CH; i++) acc_step<TT>(a, wv[i], xb, cols, k + 32 * i + j, n);
+        }
+        for (; k < cols; k += 32) acc_step<TT>(a, wf[k + j], xb, cols, k + j, n);
     } else if (TYPE == QT_Q4_K) {
         for (int sb = 0; sb < cols / 256; sb++) {
             const uint8_t *p = wr + (size_t)sb * 144;
@@ -89,7 +104,11 @@ void launch_mm_exact(float *out, const uint8_t *w, int type, int rows, int cols,
                      const uint8_t *extra, hipStream_t s) {
     dim3 grid((rows + 1) / 2, 1);
     if (nt == 1) { mm_exact_kernel<TYPE, 1><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra); return; }
-    if (nt <= 4) { mm_exact_kernel<TYPE, 4><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra); return; }
+    if (nt <= 64) {
+        grid.y = (nt + 3) / 4;
+        mm_exact_kernel<TYPE, 4><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra);
+        return;
+    }
     grid.y = (nt + 15) / 16;
     mm_exact_kernel<TYPE, 16><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra);
 }
@@ -139,47 +158,8 @@ __global__ void binary_kernel(float *o, const float *a, const float *b, int n, i
 // numerators exp(s - max) summed in rank order, then divided by the sum.
 // ------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void route_kernel(int *ids, float *weights, const float *logits, int nt, int ld) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *s = logits + (size_t)t * ld;
-    float v[8];
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
-    if (__any(bad)) {
-        if (lane < QG_TOP) { ids[t * QG_TOP + lane] = -1; weights[t * QG_TOP + lane] = 0.0f; }
-        return;
-    }
-    float largest = v[0];
-#pragma unroll
-    for (int i = 1; i < 8; i++) largest = fmaxf(largest, v[i]);
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) largest = fmaxf(largest, __shfl_xor(largest, d));
-    float num[QG_TOP], total = 0.0f;
-    int best_id[QG_TOP];
-#pragma unroll
-    for (int k = 0; k < QG_TOP; k++) {
-        float bv = v[0];
-        int bi = 0;
-#pragma unroll
-        for (int i = 1; i < 8; i++) if (v[i] > bv) { bv = v[i]; bi = i; }
-        int bidx = lane + 64 * bi;
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            const float ov = __shfl_xor(bv, d);
-            const int oi = __shfl_xor(bidx, d);
-            if (ov > bv || (ov == bv && oi < bidx)) { bv = ov; bidx = oi; }
-        }
-        best_id[k] = bidx;
-        num[k] = qg_expf(bv - largest);
-        total += num[k];
-        if ((bidx & 63) == lane) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) if (i == (bidx >> 6)) v[i] = -__builtin_inff();
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < QG_TOP; k++)
-        if (lane == k) { ids[t * QG_TOP + k] = best_id[k]; weights[t * QG_TOP + k] = num[k] / total; }
+    const int t = blockIdx.x;
+    qg_route_wave(ids + (size_t)t * QG_TOP, weights + (size_t)t * QG_TOP, logits + (size_t)t * ld, threadIdx.x);
 }
 
 // Pruning (gpu.cu:467-483), one thread per token, device atomics for the

@@ -33,7 +33,7 @@ SIGNATURES = {
     "dequant": ([P, P, I, I, I], I), "shared_add": ([P, P, P, I], I),
     # additions
     "moe_configure": ([I, I], I), "moe_dispatch": ([P, P, P, P, P, I], I),
-    "moe_workspace_bytes": ([I, I, I], Z), "moe_forward": ([P, P, P, P, P, P, I, P, P, Z], I),
+    "moe_workspace_bytes": ([I, I, I], Z), "moe_phase_events": ([P, I], I), "moe_forward": ([P, P, P, P, P, P, I, P, P, Z], I),
     "event_create": ([], P), "event_destroy": ([P], None), "event_record": ([P], I), "event_elapsed": ([P, P, P], I),
     "device_info": ([P, Z, P, P, P, P], I),
     "synth_matrix": ([P, I, U64, U64, I, I, F], I),

@@ -307,7 +307,7 @@ def test_layer_config0_batch1(layer0):
         _check_layer(L, H, synth.inputs(seed, 1, 2048), f"config0 seed{seed}")
 
 
-@pytest.mark.parametrize("nt", [4, 8, 17])
+@pytest.mark.parametrize("nt", [1, 2, 3, 4, 5, 8, 17])
 def test_layer_config1_verify_batches(layer1, nt):
     L, H = layer1
     _check_layer(L, H, synth.inputs(50 + nt, nt, 2048, correlated=True), f"config1 B={nt}")
@@ -318,9 +318,11 @@ def test_layer_config0_multitoken_no_shared(layer0):
     _check_layer(L, H, synth.inputs(9, 5, 2048), "config0 B=5")
 
 
-def test_layer_partial_residency_flags(layer1):
+@pytest.mark.parametrize("nt", [4, 17])
+def test_layer_partial_residency_flags(layer1, nt):
     """Config 4: 128 resident experts chosen by routed-weight mass over 4096
-    synthetic tokens; flags and pruning exact, unflagged rows in tolerance."""
+    synthetic tokens; flags and pruning exact, unflagged rows in tolerance
+    (4 tokens run the small-batch kernels, 17 the dispatch kernels)."""
     L, H = layer1
     xs = synth.inputs(4242, 4096, 2048, correlated=False)
     dx = Device(xs)
@@ -339,8 +341,8 @@ def test_layer_partial_residency_flags(layer1):
     saved = L.desc
     L.desc = desc
     try:
-        x = synth.inputs(77, 17, 2048, correlated=True)
-        fw, st = _check_layer(L, H, x, "config4 B=17", resident=resident)
+        x = synth.inputs(77, nt, 2048, correlated=True)
+        fw, st = _check_layer(L, H, x, f"config4 B={nt}", resident=resident)
         gst = qg.PruneStats.from_buffer_copy(fw.stats.get())
         assert (gst.token_layers, gst.missing_selections, gst.skipped_selections, gst.avoided_token_handoffs) == \
                (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs)
@@ -349,11 +351,11 @@ def test_layer_partial_residency_flags(layer1):
         L.desc = saved
 
 
-def test_layer_graph_replay(layer1):
+@pytest.mark.parametrize("nt", [2, 8])
+def test_layer_graph_replay(layer1, nt):
     """The fused layer captured into a graph and replayed, with eager work in
     between, equals the eager result every time."""
     L, H = layer1
-    nt = 8
     fw = synth.Forward(2048, 512, nt)
     fw.x.set(synth.inputs(5, nt, 2048, correlated=True))
     fw.run(L, nt)
