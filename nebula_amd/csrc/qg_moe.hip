@@ -35,7 +35,7 @@ struct Disp {
     int tok_flag[MAXB];
 };
 
-struct WsLayout { size_t logits, disp, mid, slots, total; };
+struct WsLayout { size_t logits, disp, mid, slots, xh, xs, midh, mids, total; };
 WsLayout ws_layout(int D, int F) {
     WsLayout L;
     size_t off = 0;
@@ -44,6 +44,10 @@ WsLayout ws_layout(int D, int F) {
     L.disp = take(sizeof(Disp));
     L.mid = take((size_t)(MAXS + MAXB) * F * 4);
     L.slots = take((size_t)(MAXS + MAXB) * D * 4);
+    L.xh = take((size_t)MAXB * 2 * D * 2);
+    L.xs = take((size_t)MAXB * (D / 32) * 4);
+    L.midh = take((size_t)(MAXS + MAXB) * 2 * F * 2);
+    L.mids = take((size_t)(MAXS + MAXB) * (F / 32) * 4);
     L.total = off;
     return L;
 }
@@ -59,6 +63,8 @@ void phase_mark(int i, hipStream_t s) {
 QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane) {
     qg_route_wave(s_ids + t * QG_TOP, s_w + t * QG_TOP, s, lane);
 }
+
+QG_DEV void act_planes_group(const float *x, int K, int r, int g, _Float16 *xh, float *xs);
 
 // Inclusive scan of one int per thread over a RD_THREADS-thread block.
 QG_DEV int block_scan(int v, int *s_tmp) {
@@ -130,13 +136,16 @@ QG_DEV void build_dispatch(const int *s_ids, const int *s_flag, int nt, Disp *ds
 // ---------------- kernel 2: route + coverage + dispatch (one block) ----------------
 __global__ __launch_bounds__(RD_THREADS) void route_dispatch_kernel(int *ids_out, float *w_out, uint8_t *flags_out,
                                                                     qg_prune_stats *stats, const float *logits, int ld, int nt,
-                                                                    const uint8_t *resident, double thr, Disp *ds, int has_shared) {
+                                                                    const uint8_t *resident, double thr, Disp *ds, int has_shared,
+                                                                    const float *x, int D, _Float16 *xh, float *xs) {
     __shared__ int s_ids[MAXS], s_rank[MAXS], s_cnt[QG_EXPERTS];
     __shared__ float s_w[MAXS];
     __shared__ int s_flag[MAXB], s_missing[MAXB];
     __shared__ double s_mass[MAXB];
     __shared__ int s_tmp[RD_THREADS / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (xh)  // fp16 hi/lo planes of the inputs for the matrix-core expert kernels
+        for (int i = tid; i < nt * (D / 32); i += RD_THREADS) act_planes_group(x, D, i / (D / 32), i % (D / 32), xh, xs);
     for (int t = wave; t < nt; t += RD_THREADS / 64) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane);
     __syncthreads();
     // Coverage (gpu.cu:470-478): mass of non-resident selections in rank order.
@@ -189,11 +198,14 @@ __global__ __launch_bounds__(RD_THREADS) void route_dispatch_kernel(int *ids_out
 // reference computes each (token, rank) independently); invalid slots get
 // NaN in mid and slots (gpu.cu:531,539).
 __global__ __launch_bounds__(RD_THREADS) void dispatch_ids_kernel(const int *ids, int nt, Disp *ds, float *mid_slot,
-                                                                  float *slots_out, int D, int F) {
+                                                                  float *slots_out, int D, int F, const float *x, _Float16 *xh,
+                                                                  float *xs) {
     __shared__ int s_ids[MAXS], s_rank[MAXS], s_cnt[QG_EXPERTS];
     __shared__ int s_flag[MAXB];
     __shared__ int s_tmp[RD_THREADS / 64];
     const int tid = threadIdx.x;
+    if (xh)
+        for (int i = tid; i < nt * (D / 32); i += RD_THREADS) act_planes_group(x, D, i / (D / 32), i % (D / 32), xh, xs);
     if (tid < nt * QG_TOP) s_ids[tid] = ids[tid];
     if (tid < MAXB) s_flag[tid] = 0;
     if (tid == 0) { ds->status = 0; ds->has_shared = 0; }
@@ -491,6 +503,8 @@ QG_DEV float iq4_dot(const Iq4Vals &v, const Iq4Slice &x) {
     s1 = __builtin_fmaf(-128.0f, x.s1, s1);
     return __builtin_fmaf(v.d0, s0, v.d1 * s1);
 }
+
+#include "qg_mfma.hip"
 
 QG_DEV void down_store(const DownArgs &A, bool shared, int mrow, int row, float y) {
     if (shared) { A.slots[(size_t)mrow * A.D + row] = y; return; }
@@ -910,15 +924,47 @@ int launch_small(float *out, int *ids, float *weights, unsigned char *flags, qg_
 // ---------------- expert-phase launcher shared by forward and mtp_moe ----------------
 struct ExpertPhase {
     const float *x; int nt, D, F;
+    _Float16 *xh; float *xs; _Float16 *midh; float *mids;
     const uint8_t *gate, *up, *down; int gt, ut, dt;
     const uint8_t *sh_gate, *sh_up, *sh_down; int sgt, sut, sdt;
     Disp *ds; float *mid, *mid_slot, *slots, *slots_out; const float *route_w;
     const float *sh_logit; int ld; float *out;
 };
 
+bool mfma_ok(const ExpertPhase &P) {
+    auto dn_ok = [&](int t) { return (t == QT_IQ4_NL && P.F % 64 == 0) || (t == QT_Q4_K && P.F % 256 == 0); };
+    return P.xh && P.gt == QT_Q4_K && P.ut == QT_Q4_K && P.D % 256 == 0 && P.D % 64 == 0 && P.F % 64 == 0 && dn_ok(P.dt) &&
+           (!P.sh_gate || (P.sgt == QT_Q4_K && P.sut == QT_Q4_K && dn_ok(P.sdt)));
+}
+
 int launch_experts(const ExpertPhase &P, hipStream_t s) {
     const int maxa = P.nt * QG_TOP < QG_EXPERTS ? P.nt * QG_TOP : QG_EXPERTS;
     const int gx = maxa + (P.sh_gate ? 1 : 0);
+    if (mfma_ok(P)) {
+        MfmaGU G{P.xh, P.xs, P.nt, P.D, P.F, maxa, P.gate, P.up, P.sh_gate, P.sh_up, qg_row_bytes_host(QT_Q4_K, P.D), P.ds,
+                 nullptr, P.mid_slot, P.midh, P.mids, P.ds->ent_token, MAXS};
+        gateup_mfma_kernel<3><<<dim3(gx, P.F / 64), 256, 0, s>>>(G);
+        int rc = hipGetLastError();
+        if (rc) return rc;
+        phase_mark(3, s);
+        MfmaDown Dn{P.nt, P.D, P.F, maxa, P.down, P.sh_down, qg_row_bytes_host(P.dt, P.F),
+                    P.sh_down ? qg_row_bytes_host(P.sdt, P.F) : 0, P.ds, P.midh, P.mids, P.route_w, P.slots, P.slots_out, MAXS};
+        const int fs = P.sh_down ? P.sdt : P.dt;
+        const dim3 grid(gx, P.D / 64);
+        if (P.dt == QT_IQ4_NL && fs == QT_IQ4_NL) down_mfma_kernel<QT_IQ4_NL, QT_IQ4_NL, 3><<<grid, 256, 0, s>>>(Dn);
+        else if (P.dt == QT_IQ4_NL) down_mfma_kernel<QT_IQ4_NL, QT_Q4_K, 3><<<grid, 256, 0, s>>>(Dn);
+        else if (fs == QT_IQ4_NL) down_mfma_kernel<QT_Q4_K, QT_IQ4_NL, 3><<<grid, 256, 0, s>>>(Dn);
+        else down_mfma_kernel<QT_Q4_K, QT_Q4_K, 3><<<grid, 256, 0, s>>>(Dn);
+        if ((rc = hipGetLastError())) return rc;
+        phase_mark(4, s);
+        if (P.out) {
+            const int quads = P.nt * P.D / 4;
+            combine_kernel<<<(quads + 255) / 256, 256, 0, s>>>(P.out, P.slots, P.ds, P.sh_logit, P.ld, P.nt, P.D);
+            rc = hipGetLastError();
+        }
+        phase_mark(5, s);
+        return rc;
+    }
     const bool fast_gu = P.gt == QT_Q4_K && P.ut == QT_Q4_K && (!P.sh_gate || (P.sgt == QT_Q4_K && P.sut == QT_Q4_K)) &&
                          P.D == 2048 && P.F % 16 == 0;
     const bool fast_dn = (P.dt == QT_IQ4_NL || P.dt == QT_Q4_K) && (!P.sh_down || P.sdt == QT_IQ4_NL || P.sdt == QT_Q4_K) &&
@@ -1058,11 +1104,13 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
     phase_mark(1, s);
     if (small_path_ok(L, nt))
         return launch_small(out, ids, weights, flags, stats, x, nt, L, logits, rows, ds, (float *)(ws + lay.mid), s);
+    _Float16 *xh = (_Float16 *)(ws + lay.xh);
+    float *xs = (float *)(ws + lay.xs);
     route_dispatch_kernel<<<1, RD_THREADS, 0, s>>>(ids, weights, flags, stats, logits, rows, nt, L->resident, L->threshold, ds,
-                                                   sh ? 1 : 0);
+                                                   sh ? 1 : 0, x, D, xh, xs);
     if ((rc = hipGetLastError())) return rc;
     phase_mark(2, s);
-    ExpertPhase P{x, nt, D, F,
+    ExpertPhase P{x, nt, D, F, xh, xs, (_Float16 *)(ws + lay.midh), (float *)(ws + lay.mids),
                   (const uint8_t *)L->gate, (const uint8_t *)L->up, (const uint8_t *)L->down, L->gate_type, L->up_type, L->down_type,
                   sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr,
                   sh ? (const uint8_t *)L->sh_down : nullptr, L->sh_gate_type, L->sh_up_type, L->sh_down_type,
@@ -1099,12 +1147,16 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
     hipStream_t s = qg_stream();
     uint8_t *ws = (uint8_t *)scratch;
     Disp *ds = (Disp *)(ws + lay.disp);
-    dispatch_ids_kernel<<<1, RD_THREADS, 0, s>>>(ids, nt, ds, mid, slots, D, F);
+    _Float16 *xh = (_Float16 *)(ws + lay.xh);
+    float *xs = (float *)(ws + lay.xs);
+    const bool planes = nt > SMALL_B;  // matrix-core expert kernels for the larger groups
+    dispatch_ids_kernel<<<1, RD_THREADS, 0, s>>>(ids, nt, ds, mid, slots, D, F, x, planes ? xh : nullptr, xs);
     int rc = hipGetLastError();
     if (rc) return rc;
     const int saved_n = tl_phase_n;
     tl_phase_n = 0;  // phase timing covers qg_moe_forward only
-    ExpertPhase P{x, nt, D, F, (const uint8_t *)g, (const uint8_t *)u, (const uint8_t *)d, gt, ut, dt,
+    ExpertPhase P{x, nt, D, F, planes ? xh : nullptr, xs, (_Float16 *)(ws + lay.midh), (float *)(ws + lay.mids),
+                  (const uint8_t *)g, (const uint8_t *)u, (const uint8_t *)d, gt, ut, dt,
                   nullptr, nullptr, nullptr, 0, 0, 0,
                   ds, (float *)(ws + lay.mid), mid, (float *)(ws + lay.slots), slots, weights,
                   nullptr, 0, nullptr};
