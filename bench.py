@@ -5,15 +5,23 @@ Default workload: BASELINE config 1 at the 17-token speculative-verify batch
 (Q4_K gate/up, IQ4_NL down, shared Q4_K expert with sigmoid gate, correlated
 RMS-normed inputs).  A step is one layer forward (router -> top-10 -> experts
 -> router-rank combine -> shared expert) through the C ABI's qg_moe_forward,
-rotating over 16 distinct seeded layers (14.5 GB) so weights stream from HBM,
-not from the 256 MB Infinity Cache.  Inputs are resident in HBM before the
-timed region.
+rotating over 16 distinct seeded layers (14.5 GB) so expert weights stream
+from HBM, not from the 256 MB Infinity Cache.  Inputs are resident in HBM
+before the timed region.
 
-Printed: one JSON line.  value = tokens/s of the layer (batch / step time);
-roofline = the dominant kernel's algorithmic bytes over its average duration,
-timed with HIP events on the library's launch stream; cpu_baseline = the
-reference's own cpu.c qc_moe (built from /root/reference into oracle/_ref) on
-the same inputs, on this host's cores.
+--config 0: one token, Q4_K experts, no shared expert.
+--config 2: the 48-layer stack at one token, h <- h + MoE(RMSNorm(h)) per
+            layer, replayed as one captured graph (43.5 GB of experts).
+--config 4: config 1 with 128 of 512 experts resident per layer and the 90 %
+            coverage flags.
+
+Printed: one JSON line.  value = tokens/s (batch / step time), the step being
+one replay of the layer's captured graph; roofline = the gate/up kernel's
+algorithmic bytes over its average duration, from HIP events recorded by the
+kernel dispatches themselves on the library's launch stream
+(hipExtLaunchKernelGGL) over the same number of eagerly launched steps; cpu_baseline = the reference's own
+cpu.c (router qc_matmul, qc_moe, shared-expert qc_matmul; built from
+/root/reference into oracle/_ref) on the same inputs, on this host's cores.
 """
 from __future__ import annotations
 
@@ -34,12 +42,14 @@ from nebula_amd import qg, synth  # noqa: E402
 
 D, FF, TOP, EXPERTS = 2048, 512, 10, 512
 EXPERT_BYTES = 1_769_472
+GATEUP_BYTES = 1_179_648          # gate + up rows of one Q4_K expert (2 x 512 x 1152 B)
 ROUTER_BYTES = EXPERTS * D * 4
 HBM_PEAK_GBS = 8000.0
 METRIC = "routed-MoE tokens/s + % HBM peak at B=1/17; int8 MFMA util at 2048-tok prefill"
+KERNELS = ["router", "route", "gate_up", "down"]
 
 
-def layer_bytes(nt: int, unique: int, shared: bool) -> int:
+def layer_bytes(nt: int, unique: float, shared: bool) -> float:
     """Algorithmic HBM bytes of one layer forward (each touched expert once)."""
     b = ROUTER_BYTES + unique * EXPERT_BYTES + nt * (2 * D * 4 + 80)
     if shared:
@@ -47,20 +57,43 @@ def layer_bytes(nt: int, unique: int, shared: bool) -> int:
     return b
 
 
-def gateup_bytes(nt: int, unique: int, shared: bool) -> int:
-    per = FF * 1152 * 2  # gate + up rows of one Q4_K expert
-    return (unique + (1 if shared else 0)) * per + nt * D * 4
+def gateup_bytes(nt: int, unique: float, shared: bool) -> float:
+    return (unique + (1 if shared else 0)) * GATEUP_BYTES + nt * D * 4
+
+
+def resident_set(layer: synth.DeviceLayer, seed: int, count: int = 128) -> np.ndarray:
+    """Config 4's resident experts: the `count` with the largest routed-weight
+    mass over 4096 seeded synthetic tokens (ties to the lower id)."""
+    xs = synth.inputs(seed, 4096, D)
+    dx = qg.Device(xs)
+    logits = qg.Device(shape=(4096, EXPERTS), dtype=np.float32)
+    ids = qg.Device(shape=(4096, TOP), dtype=np.int32)
+    w = qg.Device(shape=(4096, TOP), dtype=np.float32)
+    qg.call("matmul", logits.p, layer.bufs["router"].p, 0, EXPERTS, D, dx.p, 4096)
+    qg.call("route", ids.p, w.p, logits.p, 4096)
+    score = np.zeros(EXPERTS)
+    np.add.at(score, ids.get().ravel(), w.get().ravel().astype(np.float64))
+    order = np.lexsort((np.arange(EXPERTS), -score))
+    mask = np.zeros(EXPERTS, np.uint8)
+    mask[order[:count]] = 1
+    return mask
 
 
 class Workload:
     def __init__(self, config: int, batch: int, layers: int, seed: int):
         self.config, self.nt = config, batch
-        shared = config in (1, 4)
-        dt = 20 if config in (1, 3, 4) else 12
-        self.shared = shared
-        self.specs = [synth.LayerSpec(seed=seed + l, down_type=dt, shared=shared) for l in range(layers)]
+        self.shared = config in (1, 4)
+        dt = 20 if config in (1, 4) else 12
+        self.specs = [synth.LayerSpec(seed=seed + l, down_type=dt, shared=self.shared) for l in range(layers)]
         t0 = time.time()
-        self.layers = [synth.build_layer(s) for s in self.specs]
+        self.layers = []
+        for s in self.specs:
+            L = synth.build_layer(s)
+            if config == 4:
+                mask = resident_set(L, seed=s.seed + 77)
+                L.bufs["resident"] = qg.Device(mask)
+                L.desc.resident, L.desc.threshold = L.bufs["resident"].p, 0.10
+            self.layers.append(L)
         qg.call("sync")
         self.build_s = time.time() - t0
         self.fw = synth.Forward(D, FF, batch)
@@ -70,45 +103,76 @@ class Workload:
     def step(self, i: int) -> None:
         self.fw.run(self.layers[i % len(self.layers)], self.nt)
 
-    def unique_experts(self, i: int) -> int:
+    def routing(self, i: int):
         self.step(i)
         qg.call("sync")
         ids = self.fw.ids.get()[:self.nt]
-        return len(np.unique(ids[(ids >= 0) & (ids < EXPERTS)]))
+        flags = self.fw.flags.get()[:self.nt]
+        return ids, flags
+
+    def unique_experts(self, i: int) -> int:
+        ids, flags = self.routing(i)
+        ok = (ids >= 0) & (ids < EXPERTS) & (flags[:, None] < 2)
+        return len(np.unique(ids[ok]))
 
 
-def time_steps(wl: Workload, steps: int, warmup: int) -> float:
-    for i in range(warmup):
+def capture_graphs(wl: Workload) -> list:
+    """One captured graph per rotated layer: a step replays the layer's kernels
+    with one host call, as a serving loop would (qwen.c captures per batch
+    size, qwen.c:726-734)."""
+    graphs = []
+    for i in range(len(wl.layers)):
+        g = C.c_void_p()
+        qg.call("graph_begin", C.byref(g))
         wl.step(i)
+        qg.call("graph_end", g)
+        graphs.append(g)
+    return graphs
+
+
+def time_decode(wl: Workload, steps: int, warmup: int):
+    """Step time over `steps` timed graph replays, then the average duration of
+    each kernel of the step from dispatch-timestamped events (qg_moe_kernel_events,
+    hipExtLaunchKernelGGL) over the same number of eagerly launched steps."""
+    graphs = capture_graphs(wl)
+    n = len(graphs)
+    for i in range(warmup):
+        qg.call("graph_launch", graphs[i % n])
     qg.call("sync")
     b, e = qg.Event(), qg.Event()
     b.record()
     for i in range(steps):
-        wl.step(i)
+        qg.call("graph_launch", graphs[i % n])
     e.record()
     qg.call("sync")
-    return qg.elapsed_ms(b, e) / steps
-
-
-def time_phases(wl: Workload, steps: int) -> list[float]:
-    """Average duration of each kernel phase (ms), from events recorded by the
-    library between its launches on its own stream."""
-    evs = [qg.Event() for _ in range(6)]
-    arr = (C.c_void_p * 6)(*[e.p for e in evs])
-    acc = np.zeros(5)
+    ms = qg.elapsed_ms(b, e) / steps
+    for g in graphs:
+        qg.lib().qg_graph_destroy(g)
+    evs = [[qg.Event() for _ in range(8)] for _ in range(steps)]
+    arrs = [(C.c_void_p * 8)(*[ev.p for ev in evs_i]) for evs_i in evs]
     for i in range(steps):
-        qg.call("moe_phase_events", arr, 6)
+        qg.call("moe_kernel_events", arrs[i], 8)
         wl.step(i)
-        qg.call("moe_phase_events", None, 0)
-        qg.call("sync")
-        acc += [qg.elapsed_ms(evs[k], evs[k + 1]) for k in range(5)]
-    return list(acc / steps)
+    qg.call("moe_kernel_events", None, 0)
+    qg.call("sync")
+    kern = {}
+    for k, name in enumerate(KERNELS):
+        vals = []
+        for ev in evs:
+            t = C.c_float()
+            if qg.lib().qg_event_elapsed(C.byref(t), ev[2 * k].p, ev[2 * k + 1].p) == 0:
+                vals.append(t.value)
+        if vals:
+            kern[name] = float(np.mean(vals))
+    return ms, kern
 
 
 def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
-    """The reference's qc_moe (cpu.c) on layer 0's routed experts for this batch,
-    timed on the host cores; routing ids/weights from the GPU run of the same
-    inputs (the reference's CPU path receives them from the GPU, qwen.c:665-669)."""
+    """The reference's cpu.c on layer 0 of the workload: router qc_matmul (F32),
+    qc_moe on the routed experts, shared expert through qc_matmul x 3 plus the
+    sigmoid-gated add.  Routing ids/weights come from the GPU run of the same
+    inputs (the reference's CPU path receives them from the GPU,
+    qwen.c:665-669); routing itself is not timed (a top-10 of 512 per token)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     try:
         import oracle as O
@@ -118,9 +182,8 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
     if ref is None:
         return None
     L = wl.layers[0]
-    wl.step(0)
-    qg.call("sync")
-    ids = wl.fw.ids.get()[:wl.nt].copy()
+    ids, _ = wl.routing(0)
+    ids = ids.copy()
     w = wl.fw.w.get()[:wl.nt].copy()
     s = L.spec
     per = {"gate": FF * qg.row_bytes(s.gate_type, D), "up": FF * qg.row_bytes(s.up_type, D), "down": D * qg.row_bytes(s.down_type, FF)}
@@ -128,16 +191,40 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
     for e in np.unique(ids[ids >= 0]):
         for k in host:
             host[k][e * per[k]:(e + 1) * per[k]] = synth.read_expert(L, k, int(e))
+    router = np.empty(EXPERTS * D * 4, np.uint8)
+    qg.call("read", router.ctypes.data, L.bufs["router"].p, router.nbytes)
+    shared = {}
+    if wl.shared:
+        for name in ("sh_gate", "sh_up", "sh_down", "sh_inp"):
+            buf = np.empty(L.bufs[name].nbytes, np.uint8)
+            qg.call("read", buf.ctypes.data, L.bufs[name].p, buf.nbytes)
+            shared[name] = buf
     cores = len(os.sched_getaffinity(0))
     threads = max(1, min(28, cores))
     ws = ref.qc_create(max(wl.nt, 1), threads)
-    out = np.empty((wl.nt, D), np.float32)
+    nt = wl.nt
+    out = np.empty((nt, D), np.float32)
+    logits = np.empty((nt, EXPERTS), np.float32)
+    g = np.empty((nt, FF), np.float32)
+    u = np.empty((nt, FF), np.float32)
+    so = np.empty((nt, D), np.float32)
+    lg = np.empty((nt, 1), np.float32)
     x = np.ascontiguousarray(wl.x, np.float32)
 
     def run():
-        rc = ref.qc_moe(ws, out.ctypes.data, x.ctypes.data, ids.ctypes.data, w.ctypes.data, wl.nt,
-                        host["gate"].ctypes.data, s.gate_type, host["up"].ctypes.data, s.up_type, host["down"].ctypes.data, s.down_type)
-        assert rc == 0
+        assert ref.qc_matmul(logits.ctypes.data, router.ctypes.data, 0, EXPERTS, D, x.ctypes.data, nt, threads) == 0
+        assert ref.qc_moe(ws, out.ctypes.data, x.ctypes.data, ids.ctypes.data, w.ctypes.data, nt,
+                          host["gate"].ctypes.data, s.gate_type, host["up"].ctypes.data, s.up_type,
+                          host["down"].ctypes.data, s.down_type) == 0
+        if wl.shared:
+            st = s.sh_types
+            assert ref.qc_matmul(g.ctypes.data, shared["sh_gate"].ctypes.data, st[0], FF, D, x.ctypes.data, nt, threads) == 0
+            assert ref.qc_matmul(u.ctypes.data, shared["sh_up"].ctypes.data, st[1], FF, D, x.ctypes.data, nt, threads) == 0
+            mid = (g / (1 + np.exp(-g))) * u
+            assert ref.qc_matmul(so.ctypes.data, shared["sh_down"].ctypes.data, st[2], D, FF, mid.ctypes.data, nt, threads) == 0
+            assert ref.qc_matmul(lg.ctypes.data, shared["sh_inp"].ctypes.data, 0, 1, D, x.ctypes.data, nt, threads) == 0
+            out[:] += so / (1 + np.exp(-lg))
+
     for _ in range(3):
         run()
     times = []
@@ -148,19 +235,41 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
         times.append(time.perf_counter() - t0)
     ref.qc_destroy(ws)
     med = float(np.median(times))
-    return {"value": round(wl.nt / med, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"cpu.c qc_moe (routed experts of layer 0, {wl.nt} tokens, isa={ref.qc_backend_name().decode()}), "
+    parts = "router qc_matmul + qc_moe" + (" + shared expert (3 qc_matmul + gate)" if wl.shared else "")
+    return {"value": round(nt / med, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"cpu.c {parts} on layer 0, {nt} tokens, isa={ref.qc_backend_name().decode()}; "
                       f"median of {len(times)} runs after 3 warm-ups; OMP threads={threads} of {cores} host CPUs"}
 
 
-def load_traffic(name: str):
-    p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get(name)
-        except Exception:
-            return None
-    return None
+def bench_stack(args) -> dict:
+    """Config 2: 48 seeded config-0 layers, one token, replayed as one graph."""
+    n_layers = args.layers if args.layers != 16 else 48
+    specs = [synth.LayerSpec(seed=9000 + l) for l in range(n_layers)]
+    layers = [synth.build_layer(s) for s in specs]
+    arr = (qg.MoeLayer * n_layers)(*[l.desc for l in layers])
+    h = qg.host()
+    stack = h.nm_stack_create(arr, n_layers, 1, 0)
+    if not stack:
+        raise RuntimeError(h.nm_last_error().decode())
+    x0 = synth.inputs(31, 1, D)
+    hid = h.nm_stack_hidden(stack)
+    for _ in range(max(1, args.warmup // 10)):
+        qg.call("write", hid, x0.ctypes.data, x0.nbytes)
+        if h.nm_stack_forward(stack, 1, 1):
+            raise RuntimeError(h.nm_last_error().decode())
+    qg.call("sync")
+    steps = max(1, args.steps // 10)
+    b, e = qg.Event(), qg.Event()
+    b.record()
+    for _ in range(steps):
+        if h.nm_stack_forward(stack, 1, 1):
+            raise RuntimeError(h.nm_last_error().decode())
+    e.record()
+    qg.call("sync")
+    ms = qg.elapsed_ms(b, e) / steps
+    h.nm_stack_destroy(stack)
+    nbytes = n_layers * layer_bytes(1, 10, False)
+    return {"ms": ms, "layers": n_layers, "bytes": nbytes, "steps": steps}
 
 
 def main() -> int:
@@ -168,8 +277,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1))
-    ap.add_argument("--batch", type=int, default=17)
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 4))
+    ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -178,20 +287,41 @@ def main() -> int:
         print(f"bench.py measures one GPU's share of the layer; --gpus {args.gpus} is not supported "
               "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
         return 2
-    if not 1 <= args.batch <= 17:
+    batch = args.batch if args.batch is not None else (17 if args.config in (1, 4) else 1)
+    if not 1 <= batch <= 17:
         print("decode batch must be 1..17", file=sys.stderr)
         return 2
+    data = "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)"
 
-    wl = Workload(args.config, args.batch, args.layers, seed=9000)
+    if args.config == 2:
+        r = bench_stack(args)
+        ms = r["ms"]
+        line = {
+            "metric": METRIC, "value": round(1 / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": r["steps"], "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": data,
+            "config": {"workload": f"config2: {r['layers']}-layer routed-MoE stack, B=1, D=2048, 512 experts top-10, F=512, Q4_K; "
+                                   "h <- h + MoE(RMSNorm(h)); one captured graph",
+                       "layers": r["layers"], "stack_bytes": int(r["bytes"]),
+                       "stack_hbm_GBps": round(r["bytes"] / (ms * 1e-3) / 1e9, 1),
+                       "stack_hbm_frac": round(r["bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "us_per_layer": round(ms * 1000 / r["layers"], 3)},
+            "roofline": None, "cpu_baseline": None,
+        }
+        print(json.dumps(line), flush=True)
+        return 0
+
+    wl = Workload(args.config, batch, args.layers, seed=9000)
     uniq = [wl.unique_experts(i) for i in range(len(wl.layers))]
     U = float(np.mean(uniq))
-    ms = time_steps(wl, args.steps, args.warmup)
-    phases = time_phases(wl, min(args.steps, 64))
-    names = ["router", "route_dispatch", "gate_up", "down", "combine"]
-    gu_ms = phases[2] if phases[2] > 0 else None
+    ms, kern = time_decode(wl, args.steps, args.warmup)
+    gu_ms = kern.get("gate_up")
     nbytes = layer_bytes(wl.nt, U, wl.shared)
     gu_bytes = gateup_bytes(wl.nt, U, wl.shared)
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None
+    names = {0: f"config0: routed-MoE layer, B={wl.nt}, D=2048, 512 experts top-10, F=512, Q4_K",
+             1: f"config1: routed-MoE layer, B={wl.nt}, D=2048, 512 experts top-10, F=512, Q4_K gate/up, IQ4_NL down, shared Q4_K expert",
+             4: f"config4: config 1 at B={wl.nt} with 128/512 resident experts per layer and 90% coverage flags"}
     line = {
         "metric": METRIC,
         "value": round(wl.nt / (ms * 1e-3), 1),
@@ -204,13 +334,12 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)",
-        "config": {"workload": f"config{args.config}: routed-MoE layer, B={wl.nt}, D=2048, 512 experts top-10, F=512"
-                               + (", Q4_K gate/up, IQ4_NL down, shared Q4_K expert" if args.config == 1 else ", Q4_K"),
+        "data": data,
+        "config": {"workload": names[args.config],
                    "batch_tokens": wl.nt, "layers_rotated": len(wl.layers), "unique_experts_mean": U,
                    "layer_bytes": int(nbytes), "layer_hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                    "layer_hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                   "phase_us": {n: round(v * 1000, 2) for n, v in zip(names, phases)}},
+                   "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
         "roofline": {"bound": "hbm", "kernel": "gate_up", "achieved": round(achieved, 1) if achieved else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                      "traffic": load_traffic(f"gate_up_config{args.config}_B{wl.nt}"),
@@ -221,6 +350,18 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
+    counters (profiles/traffic.json), or None when not measured."""
+    p = ROOT / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get(name)
+        except (OSError, ValueError):
+            return None
+    return None
 
 
 if __name__ == "__main__":

@@ -4,7 +4,7 @@
  * It plays the role of the reference's moe()/shared_direct() and the
  * per-layer loop of qwen_target (qwen.c:714-735,759-762) for a stack of MoE
  * layers without attention: each layer is h <- h + MoE(RMSNorm(h)) (eps 1e-6,
- * unit weight, the norm of gpu.cu:204-214).  The whole stack for a token
+ * unit weight, the norm of gpu.cu:204-214), one qg_moe_forward_residual call.  The whole stack for a token
  * count is captured once into a graph and replayed, the way qwen.c:726-734
  * captures the shared expert per batch size; unlike the reference no routing
  * decision crosses to the host, so the routed part is captured too.

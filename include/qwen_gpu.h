@@ -106,7 +106,9 @@ typedef struct {
     double threshold;                           /* omitted-mass threshold (0.10, config.py:9) */
 } qg_moe_layer;
 
-/* Device workspace bytes for qg_moe_forward at up to `tokens` tokens. */
+/* Device workspace bytes for qg_moe_forward / qg_moe_forward_residual at up
+ * to `tokens` tokens.  The workspace needs no initialisation; one workspace
+ * per concurrent caller. */
 size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
 
 /* out [tokens, D]; ids/weights [tokens, 10] (after pruning); flags [tokens]
@@ -117,6 +119,21 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
  * tokens 1..17. */
 int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                    const float *x, int tokens, const qg_moe_layer *layer, void *workspace, size_t workspace_bytes);
+
+/* The layer applied to a residual stream, as one layer of qwen_target's loop
+ * without attention (qwen.c:759-762): x = RMSNorm(h) (eps 1e-6, unit weight,
+ * the norm of gpu.cu:204-214), h += MoE(x).  xn_out [tokens, D] (the
+ * normalised input) and out [tokens, D] (the MoE output) may be NULL.  Other
+ * arguments as qg_moe_forward. */
+int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
+                            float *xn_out, float *out, int tokens, const qg_moe_layer *layer,
+                            void *workspace, size_t workspace_bytes);
+
+/* Benchmark support: events[2i] and events[2i+1] (qg_event_create handles)
+ * are recorded at the start and end of kernel i of this thread's decode-path
+ * qg_moe_forward calls (0 router, 1 routing, 2 gate/up, 3 down), timestamped
+ * by the dispatch itself (hipExtLaunchKernelGGL).  n = 0 disables. */
+int qg_moe_kernel_events(void **events, int n);
 
 /* Benchmark support: record events[i] (qg_event_create handles) on the
  * launch stream at the phase boundaries of this thread's qg_moe_forward

@@ -21,7 +21,7 @@ const char *nm_last_error(void) { return nm_error; }
 struct nm_stack {
     int n_layers, max_tokens, width, record;
     qg_moe_layer *layers;
-    float *h, *xn, *out, *w;
+    float *h, *w;
     int *ids;
     void *ws;
     size_t ws_bytes;
@@ -33,7 +33,7 @@ struct nm_stack {
 void nm_stack_destroy(nm_stack *s) {
     if (!s) return;
     for (int i = 0; i <= NM_MAX_TOKENS; i++) if (s->graphs[i]) qg_graph_destroy(s->graphs[i]);
-    qg_free(s->h); qg_free(s->xn); qg_free(s->out); qg_free(s->w); qg_free(s->ids); qg_free(s->ws);
+    qg_free(s->h); qg_free(s->w); qg_free(s->ids); qg_free(s->ws);
     qg_free(s->rec_x); qg_free(s->rec_out); qg_free(s->rec_w); qg_free(s->rec_ids);
     free(s->layers);
     free(s);
@@ -52,9 +52,9 @@ nm_stack *nm_stack_create(const qg_moe_layer *layers, int n_layers, int max_toke
     const size_t act = (size_t)max_tokens * D * sizeof(float), sel = (size_t)max_tokens * NM_TOP * 4;
     if (!s->layers || !s->ws_bytes) { fail("invalid layer shape"); nm_stack_destroy(s); return NULL; }
     memcpy(s->layers, layers, sizeof(qg_moe_layer) * (size_t)n_layers);
-    s->h = qg_alloc(act); s->xn = qg_alloc(act); s->out = qg_alloc(act);
+    s->h = qg_alloc(act);
     s->w = qg_alloc(sel); s->ids = qg_alloc(sel); s->ws = qg_alloc(s->ws_bytes);
-    if (!s->h || !s->xn || !s->out || !s->w || !s->ids || !s->ws) { fail("device allocation"); nm_stack_destroy(s); return NULL; }
+    if (!s->h || !s->w || !s->ids || !s->ws) { fail("device allocation"); nm_stack_destroy(s); return NULL; }
     if (record) {
         s->rec_x = qg_alloc(act * n_layers); s->rec_out = qg_alloc(act * n_layers);
         s->rec_w = qg_alloc(sel * n_layers); s->rec_ids = qg_alloc(sel * n_layers);
@@ -69,19 +69,15 @@ float *nm_stack_hidden(nm_stack *s) { return s ? s->h : NULL; }
 #define GPU(call) do { int rc_ = (call); if (rc_) return fail("%s: %s", #call, qg_error(rc_)); } while (0)
 
 static int run_layers(nm_stack *s, int nt) {
-    const int D = s->width;
-    const size_t act = (size_t)nt * D * sizeof(float), sel = (size_t)nt * NM_TOP * 4;
-    const size_t act_stride = (size_t)s->max_tokens * D * sizeof(float), sel_stride = (size_t)s->max_tokens * NM_TOP * 4;
+    const size_t act_stride = (size_t)s->max_tokens * s->width, sel_stride = (size_t)s->max_tokens * NM_TOP;
     for (int l = 0; l < s->n_layers; l++) {
-        GPU(qg_norm(s->xn, s->h, NULL, D, 1, nt, 0, 0, 1e-6f));
-        GPU(qg_moe_forward(s->out, s->ids, s->w, NULL, NULL, s->xn, nt, &s->layers[l], s->ws, s->ws_bytes));
-        if (s->record) {
-            GPU(qg_copy((char *)s->rec_x + act_stride * l, s->xn, act));
-            GPU(qg_copy((char *)s->rec_out + act_stride * l, s->out, act));
-            GPU(qg_copy((char *)s->rec_ids + sel_stride * l, s->ids, sel));
-            GPU(qg_copy((char *)s->rec_w + sel_stride * l, s->w, sel));
-        }
-        GPU(qg_binary(s->h, s->h, s->out, nt * D, 0));
+        /* h <- h + MoE(RMSNorm(h)); with record on, the normalised input, the
+         * routing and the MoE output of the layer are kept */
+        float *xn = s->record ? s->rec_x + act_stride * l : NULL;
+        float *out = s->record ? s->rec_out + act_stride * l : NULL;
+        int *ids = s->record ? s->rec_ids + sel_stride * l : s->ids;
+        float *w = s->record ? s->rec_w + sel_stride * l : s->w;
+        GPU(qg_moe_forward_residual(s->h, ids, w, NULL, NULL, xn, out, nt, &s->layers[l], s->ws, s->ws_bytes));
     }
     return 0;
 }

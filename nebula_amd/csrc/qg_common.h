@@ -161,21 +161,22 @@ QG_DEV float qg_oct_sum(float v) {
     return v;
 }
 
-// Routing of one token by one wave (gpu.cu:456-465): ids/w receive the 10
-// winners in rank order (any non-finite logit -> ids -1, weights 0).
+// Routing of one token by one wave (gpu.cu:456-465).  On return lane k < 10
+// holds the rank-k winner: id (lowest index among equal maxima) and weight
+// exp(s - max) / (sum of the 10 numerators in rank order); a token with any
+// non-finite logit gets id -1, weight 0 in every rank.  Lanes >= 10 get -1/0.
 // Lane l holds logits l, l+64, ..., l+448.  Each of the 10 rounds takes the
 // wave maximum (DPP), then the lowest index holding it from per-slot ballots
 // (scalar work: the first slot i with a match, its lowest lane), which is the
 // winner of the reference's strict-greater scan from index 0.
-QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane) {
+QG_DEV void qg_route_lane(const float *s, int lane, int &id_out, float &w_out) {
     float v[8];
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
-    if (__any(bad)) {
-        if (lane < QG_TOP) { ids[lane] = -1; w[lane] = 0.0f; }
-        return;
-    }
+    id_out = -1;
+    w_out = 0.0f;
+    if (__any(bad)) return;
     float num[QG_TOP], total = 0.0f, largest = 0.0f;
     int best_id[QG_TOP];
 #pragma unroll
@@ -199,8 +200,182 @@ QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane) {
     }
 #pragma unroll
     for (int k = 0; k < QG_TOP; k++)
-        if (lane == k) { ids[k] = best_id[k]; w[k] = num[k] / total; }
+        if (lane == k) { id_out = best_id[k]; w_out = num[k] / total; }
+}
+
+// The same routing as qg_route_lane, faster: a threshold T that every top-10
+// logit reaches (the 10th largest of the 64 lane maxima, counting equal
+// values separately: at least 10 logits reach it, so the 10th largest logit
+// does), then an exact rank by (value desc, index asc) among the candidates
+// >= T, which is the order of the reference's repeated strict-greater argmax.
+// The numerators exp(s - max) are computed in parallel (lane k: rank k) and
+// summed in rank order.  lds_v/lds_i: 64 floats / 64 ints of wave-private
+// shared memory.  More than 64 candidates (heavy ties) falls back to
+// qg_route_lane.
+QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i) {
+    float v[8];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
+    id_out = -1;
+    w_out = 0.0f;
+    if (__any(bad)) return;
+    float lm = v[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) lm = fmaxf(lm, v[i]);
+    // threshold: walk down the distinct lane maxima until 10 lanes are covered
+    float largest = 0.0f, T = 0.0f, cur = lm;
+    int remaining = QG_TOP;
+    for (int r = 0; r < QG_TOP; r++) {
+        const float m = qg_wave_max(cur);
+        if (r == 0) largest = m;
+        const int cnt = __popcll(__ballot(cur == m));
+        T = m;
+        if (cnt >= remaining) break;
+        remaining -= cnt;
+        cur = cur == m ? -__builtin_inff() : cur;
+    }
+    // candidates v >= T, compacted in lane order
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) c += v[i] >= T;
+    int incl = c;  // inclusive prefix sum of c over lanes
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    const int total_c = __shfl(incl, 63);
+    if (total_c > 64) { qg_route_lane(s, lane, id_out, w_out); return; }
+    int pos = incl - c;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if (v[i] >= T) { lds_v[pos] = v[i]; lds_i[pos] = lane + 64 * i; pos++; }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rank of candidate `lane` among the total_c candidates
+    const float cv = lane < total_c ? lds_v[lane] : 0.0f;
+    const int ci = lane < total_c ? lds_i[lane] : 0;
+    int rank = 0;
+    for (int q = 0; q < total_c; q++) {
+        const float ov = lds_v[q];
+        const int oi = lds_i[q];
+        rank += (ov > cv) | ((ov == cv) & (oi < ci));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < total_c && rank < QG_TOP) { lds_v[rank] = cv; lds_i[rank] = ci; }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float num = lane < QG_TOP ? qg_expf(lds_v[lane] - largest) : 0.0f;
+    float total = 0.0f;
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) total += __shfl(num, k);
+    if (lane < QG_TOP) { id_out = lds_i[lane]; w_out = num / total; }
+}
+
+// Routing of one token written to ids[0..9] / w[0..9] by lanes 0..9
+// (lds_v/lds_i as for qg_route_fast).
+QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane, float *lds_v, int *lds_i) {
+    int id;
+    float wv;
+    qg_route_fast(s, lane, id, wv, lds_v, lds_i);
+    if (lane < QG_TOP) { ids[lane] = id; w[lane] = wv; }
+}
+
+// Coverage of one routed token (gpu.cu:467-483 with the 0.10 rule of
+// config.py:9): lane k < 10 holds rank k's (id, weight).  mass is the double
+// sum, in rank order, of the weights of non-resident experts.  Returns the
+// flag 0 (all resident), 1 (pruned: missing > 0 and mass < threshold; the
+// lane's non-resident id becomes -id-2 and its weight 0, no renormalisation),
+// 2 (handoff: missing > 0 and !(mass < threshold)) or 3 (an id outside
+// [0,512): uncounted).  resident == NULL means every expert is resident.
+QG_DEV int qg_route_cover(int &id, float &wv, const uint8_t *resident, double thr, int &missing, double &mass) {
+    missing = 0;
+    mass = 0.0;
+    int bad = 0;
+    for (int k = 0; k < QG_TOP; k++) {
+        const int ek = __shfl(id, k);
+        const float wk = __shfl(wv, k);
+        if (ek < 0 || ek >= QG_EXPERTS) { bad = 1; break; }
+        if (resident && !resident[ek]) { missing++; mass += (double)wk; }
+    }
+    const int flag = bad ? 3 : !missing ? 0 : (thr > 0 && mass < thr) ? 1 : 2;
+    if (flag == 1 && id >= 0 && id < QG_EXPERTS && !resident[id]) { id = -id - 2; wv = 0.0f; }
+    return flag;
 }
 
 // 16 bytes from global memory with one 128-bit load (address 4-byte aligned).
 QG_DEV uint4 qg_ld16(const uint8_t *p) { return *(const uint4 *)p; }
+
+// ---- operand helpers shared by the matrix-core kernels ----
+typedef _Float16 qg_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 qg_half2 __attribute__((ext_vector_type(2)));
+typedef float qg_f4 __attribute__((ext_vector_type(4)));
+
+QG_DEV int qg_perm8(int e) { return (e & 4) | ((e & 1) << 1) | ((e & 2) >> 1); }  // 0,2,1,3,4,6,5,7 self-inverse
+
+// IQ4_NL table lookup of four 4-bit indices (one per byte) with v_perm: the
+// table is stored +128 as unsigned bytes; callers remove the bias.
+QG_DEV uint32_t iq4_lookup(uint32_t idx) {
+    // lut + 128 = {1,24,45,63, 79,93,106,118, 129,141,153,166, 181,197,217,241}
+    const uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+
+// 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,
+// element order (0,2),(1,3),(4,6),(5,7).  (1024+q)*s - 1024*s is exact.
+QG_DEV qg_half8 q4_frag(uint2 b, int hi_nib, _Float16 s) {
+    const uint32_t w0 = hi_nib ? b.x >> 4 : b.x, w1 = hi_nib ? b.y >> 4 : b.y;
+    const uint32_t u[4] = {(w0 & 0x000F000Fu) | 0x64006400u, ((w0 >> 8) & 0x000F000Fu) | 0x64006400u,
+                           (w1 & 0x000F000Fu) | 0x64006400u, ((w1 >> 8) & 0x000F000Fu) | 0x64006400u};
+    const qg_half2 sv = {s, s}, off = {(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
+    qg_half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qg_half2 h = __builtin_bit_cast(qg_half2, u[i]);
+        const qg_half2 v = __builtin_elementwise_fma(h, sv, off);
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+// 8 IQ4_NL nibbles (4 bytes, one half) -> table values as fp16, same order.
+QG_DEV qg_half8 iq4_frag(uint32_t b0, uint32_t b1, int hi_nib) {
+    const uint32_t i0 = (hi_nib ? b0 >> 4 : b0) & 0x0F0F0F0Fu, i1 = (hi_nib ? b1 >> 4 : b1) & 0x0F0F0F0Fu;
+    const uint32_t l0 = iq4_lookup(i0), l1 = iq4_lookup(i1);  // lut + 128 as bytes
+    const uint32_t u[4] = {(l0 & 0x00FF00FFu) | 0x64006400u, ((l0 >> 8) & 0x00FF00FFu) | 0x64006400u,
+                           (l1 & 0x00FF00FFu) | 0x64006400u, ((l1 >> 8) & 0x00FF00FFu) | 0x64006400u};
+    const qg_half2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
+    qg_half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+
+// The 8 scales and mins of a Q4_K superblock header as integers.
+struct Q4kHeader { float d, dmin; uint32_t S[2], M[2]; };
+QG_DEV Q4kHeader q4k_header(uint4 hd) {
+    Q4kHeader h;
+    h.d = qg_half_u16(hd.x & 0xffffu);
+    h.dmin = qg_half_u16(hd.x >> 16);
+    h.S[0] = hd.y & 0x3F3F3F3Fu;
+    h.M[0] = hd.z & 0x3F3F3F3Fu;
+    h.S[1] = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+    h.M[1] = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    return h;
+}
+QG_DEV int q4k_s(const Q4kHeader &h, int g) { return (h.S[g >> 2] >> (8 * (g & 3))) & 0xff; }
+QG_DEV int q4k_m(const Q4kHeader &h, int g) { return (h.M[g >> 2] >> (8 * (g & 3))) & 0xff; }

@@ -14,3 +14,9 @@ int qg_cfg_ff(void);
 // Launchers shared between the drop-in entry points and the fused layer.
 int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt,
                            const uint8_t *w_extra_row, hipStream_t s);
+
+// The layer through the generic kernels (any format/width qg_moe_forward
+// accepts); used when the decode fast path does not cover the layer.
+extern "C" size_t qg_generic_workspace_bytes(int width, int ff, int tokens);
+extern "C" int qg_generic_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
+                       const qg_moe_layer *L, void *workspace, size_t ws_bytes);

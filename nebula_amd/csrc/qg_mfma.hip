@@ -20,11 +20,6 @@
 // nibble->fp16 conversion as pairs (0,2),(1,3),(4,6),(5,7); activation planes
 // are stored with the same order inside every 8-element chunk.
 
-typedef _Float16 qg_half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 qg_half2 __attribute__((ext_vector_type(2)));
-typedef float qg_f4 __attribute__((ext_vector_type(4)));
-
-QG_DEV int qg_perm8(int e) { return (e & 4) | ((e & 1) << 1) | ((e & 2) >> 1); }  // 0,2,1,3,4,6,5,7 self-inverse
 
 QG_DEV void act_planes_group(const float *x, int K, int r, int g, _Float16 *xh, float *xs) {
     const float *src = x + (size_t)r * K + g * 32;
@@ -63,60 +58,11 @@ __global__ __launch_bounds__(256) void act_planes_kernel(const float *x, int row
     xs[(size_t)r * groups + g] = s;
 }
 
-// 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,
-// element order (0,2),(1,3),(4,6),(5,7).  (1024+q)*s - 1024*s is exact.
-QG_DEV qg_half8 q4_frag(uint2 b, int hi_nib, _Float16 s) {
-    const uint32_t w0 = hi_nib ? b.x >> 4 : b.x, w1 = hi_nib ? b.y >> 4 : b.y;
-    const uint32_t u[4] = {(w0 & 0x000F000Fu) | 0x64006400u, ((w0 >> 8) & 0x000F000Fu) | 0x64006400u,
-                           (w1 & 0x000F000Fu) | 0x64006400u, ((w1 >> 8) & 0x000F000Fu) | 0x64006400u};
-    const qg_half2 sv = {s, s}, off = {(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
-    qg_half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const qg_half2 h = __builtin_bit_cast(qg_half2, u[i]);
-        const qg_half2 v = __builtin_elementwise_fma(h, sv, off);
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
-    }
-    return r;
-}
-
-// 8 IQ4_NL nibbles (4 bytes, one half) -> table values as fp16, same order.
-QG_DEV qg_half8 iq4_frag(uint32_t b0, uint32_t b1, int hi_nib) {
-    const uint32_t i0 = (hi_nib ? b0 >> 4 : b0) & 0x0F0F0F0Fu, i1 = (hi_nib ? b1 >> 4 : b1) & 0x0F0F0F0Fu;
-    const uint32_t l0 = iq4_lookup(i0), l1 = iq4_lookup(i1);  // lut + 128 as bytes
-    const uint32_t u[4] = {(l0 & 0x00FF00FFu) | 0x64006400u, ((l0 >> 8) & 0x00FF00FFu) | 0x64006400u,
-                           (l1 & 0x00FF00FFu) | 0x64006400u, ((l1 >> 8) & 0x00FF00FFu) | 0x64006400u};
-    const qg_half2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
-    qg_half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
-    }
-    return r;
-}
-
 // Activation fragment: row (token, plane), k-chunk starting at k.
 QG_DEV qg_half8 act_frag(const _Float16 *planes, int K, int row, int plane, int k) {
     return __builtin_bit_cast(qg_half8, *(const uint4 *)(planes + ((size_t)row * 2 + plane) * K + k));
 }
 
-// The 8 scales and mins of a Q4_K superblock header as integers.
-struct Q4kHeader { float d, dmin; uint32_t S[2], M[2]; };
-QG_DEV Q4kHeader q4k_header(uint4 hd) {
-    Q4kHeader h;
-    h.d = qg_half_u16(hd.x & 0xffffu);
-    h.dmin = qg_half_u16(hd.x >> 16);
-    h.S[0] = hd.y & 0x3F3F3F3Fu;
-    h.M[0] = hd.z & 0x3F3F3F3Fu;
-    h.S[1] = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-    h.M[1] = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-    return h;
-}
-QG_DEV int q4k_s(const Q4kHeader &h, int g) { return (h.S[g >> 2] >> (8 * (g & 3))) & 0xff; }
-QG_DEV int q4k_m(const Q4kHeader &h, int g) { return (h.M[g >> 2] >> (8 * (g & 3))) & 0xff; }
 
 // ---------------- gate/up + SwiGLU on MFMA ----------------
 struct MfmaGU {

@@ -60,8 +60,8 @@ void phase_mark(int i, hipStream_t s) {
     if (i < tl_phase_n && tl_phase_ev[i]) (void)hipEventRecord((hipEvent_t)tl_phase_ev[i], s);
 }
 
-QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane) {
-    qg_route_wave(s_ids + t * QG_TOP, s_w + t * QG_TOP, s, lane);
+QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane, float *lds_v, int *lds_i) {
+    qg_route_wave(s_ids + t * QG_TOP, s_w + t * QG_TOP, s, lane, lds_v, lds_i);
 }
 
 QG_DEV void act_planes_group(const float *x, int K, int r, int g, _Float16 *xh, float *xs);
@@ -146,7 +146,9 @@ __global__ __launch_bounds__(RD_THREADS) void route_dispatch_kernel(int *ids_out
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (xh)  // fp16 hi/lo planes of the inputs for the matrix-core expert kernels
         for (int i = tid; i < nt * (D / 32); i += RD_THREADS) act_planes_group(x, D, i / (D / 32), i % (D / 32), xh, xs);
-    for (int t = wave; t < nt; t += RD_THREADS / 64) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane);
+    __shared__ float s_rv[RD_THREADS / 64][64];
+    __shared__ int s_ri[RD_THREADS / 64][64];
+    for (int t = wave; t < nt; t += RD_THREADS / 64) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane, s_rv[wave], s_ri[wave]);
     __syncthreads();
     // Coverage (gpu.cu:470-478): mass of non-resident selections in rank order.
     if (tid < nt) {
@@ -441,14 +443,6 @@ struct DownArgs {
 // (64 columns).  The table is shifted by +128 to unsigned bytes so v_perm can
 // look it up and cvt_f32_ubyte convert; the shift is removed with the block's
 // x sum.
-QG_DEV uint32_t iq4_lookup(uint32_t idx) {
-    // lut + 128 = {1,24,45,63, 79,93,106,118, 129,141,153,166, 181,197,217,241}
-    const uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
-    const uint32_t sel = idx & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
-    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
-    return (hi & m) | (lo & ~m);
-}
 
 struct Iq4Slice { float v[64]; float s0, s1; };
 
@@ -595,224 +589,6 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *s
     *(float4 *)(out + (size_t)t * D + d4) = acc;
 }
 
-// ---------------- small-batch path (1..4 tokens): 3 kernels per layer ----------------
-// router -> gate/up (every block re-derives the routing from the logits, so
-// no dispatch kernel or host round trip is needed) -> down + combine (each
-// block owns 8 output rows for every selected expert, so the router-rank sum
-// is formed in LDS without a separate combine pass).
-constexpr int SMALL_B = 4;
-constexpr int SMALL_S = SMALL_B * QG_TOP;
-
-struct SmallArgs {
-    const float *x;
-    int nt, D, F;
-    const float *logits; int ld;            // router output, row stride 512 or 513
-    const uint8_t *resident; double thr;
-    const uint8_t *gate, *up, *sh_gate, *sh_up;
-    size_t rb;
-    float *mid;                             // [MAXS+MAXB][F]: slot-indexed rows, shared at MAXS+t
-    int *ids_out; float *w_out; uint8_t *flags_out; qg_prune_stats *stats;
-    int *tok_flag;                          // [MAXB] for the down kernel
-};
-
-// Routing of all tokens (wave w routes token w) plus coverage/pruning
-// (gpu.cu:470-478) into LDS.  Called by every thread of the block.
-QG_DEV void small_route(const SmallArgs &A, int *s_ids, float *s_w, int *s_flag, int *s_missing, double *s_mass) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (wave < A.nt) qg_route_wave(s_ids + wave * QG_TOP, s_w + wave * QG_TOP, A.logits + (size_t)wave * A.ld, lane);
-    __syncthreads();
-    if (tid < A.nt) {
-        const int t = tid;
-        int missing = 0, bad = 0;
-        double mass = 0;
-        for (int k = 0; k < QG_TOP; k++) {
-            const int e = s_ids[t * QG_TOP + k];
-            if (e < 0 || e >= QG_EXPERTS) { bad = 1; break; }
-            if (A.resident && !A.resident[e]) { missing++; mass += (double)s_w[t * QG_TOP + k]; }
-        }
-        const int flag = bad ? 3 : !missing ? 0 : (A.thr > 0 && mass < A.thr) ? 1 : 2;
-        if (flag == 1)
-            for (int k = 0; k < QG_TOP; k++) {
-                const int e = s_ids[t * QG_TOP + k];
-                if (!A.resident[e]) { s_ids[t * QG_TOP + k] = -e - 2; s_w[t * QG_TOP + k] = 0.0f; }
-            }
-        s_flag[t] = flag;
-        s_missing[t] = missing;
-        s_mass[t] = mass;
-    }
-    __syncthreads();
-}
-
-// Block (a, rows): a < nt*10 is selection (t,k) = (a/10, a%10); it computes
-// the expert only if this is the expert's first eligible selection, for every
-// token that chose it (at most one selection per token).  a == nt*10 is the
-// shared expert.  mid rows are slot-indexed: row t*10+k for every selection.
-__global__ __launch_bounds__(256) void gateup_small_kernel(SmallArgs A) {
-    constexpr int RPW = 4;
-    __shared__ int s_ids[SMALL_S], s_flag[SMALL_B], s_missing[SMALL_B];
-    __shared__ float s_w[SMALL_S];
-    __shared__ double s_mass[SMALL_B];
-    const int a = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const bool shared = A.sh_gate && a == A.nt * QG_TOP;
-    int tok[SMALL_B], slot[SMALL_B], n = 0;
-    const uint8_t *G, *U;
-    if (shared) {
-        n = A.nt;
-        for (int i = 0; i < SMALL_B; i++) { tok[i] = i < A.nt ? i : 0; slot[i] = MAXS + i; }
-        G = A.sh_gate; U = A.sh_up;
-    } else {
-        small_route(A, s_ids, s_w, s_flag, s_missing, s_mass);
-        if (a == 0 && blockIdx.y == 0) {
-            const int tid = threadIdx.x;
-            if (tid < A.nt * QG_TOP) { A.ids_out[tid] = s_ids[tid]; A.w_out[tid] = s_w[tid]; }
-            if (tid < A.nt) { A.tok_flag[tid] = s_flag[tid]; if (A.flags_out) A.flags_out[tid] = (uint8_t)s_flag[tid]; }
-            if (tid == 0 && A.resident && A.stats)
-                for (int t = 0; t < A.nt; t++) {
-                    if (s_flag[t] == 3) continue;
-                    A.stats->token_layers += 1;
-                    A.stats->missing_selections += (uint64_t)s_missing[t];
-                    if (s_flag[t] == 1) {
-                        A.stats->skipped_selections += (uint64_t)s_missing[t];
-                        A.stats->avoided_token_handoffs += 1;
-                        A.stats->skipped_mass += s_mass[t];
-                    }
-                }
-        }
-        const int e = s_ids[a];
-        const bool elig_a = e >= 0 && e < QG_EXPERTS && s_flag[a / QG_TOP] < 2;
-        if (!elig_a) return;
-        const int i = lane < SMALL_S ? lane : SMALL_S - 1;
-        const bool same = lane < A.nt * QG_TOP && s_ids[i] == e && s_flag[i / QG_TOP] < 2;
-        unsigned long long m = __ballot(same);
-        if (m & ((1ULL << a) - 1ULL)) return;  // an earlier selection owns this expert
-        while (m) {
-            const int s = __builtin_ctzll(m);
-            m &= m - 1;
-            tok[n] = s / QG_TOP; slot[n] = s; n++;
-        }
-        G = A.gate + (size_t)e * A.F * A.rb;
-        U = A.up + (size_t)e * A.F * A.rb;
-    }
-    const int row0 = (blockIdx.y * 4 + wave) * RPW;
-    const int ch = lane, q = ch & 7;
-    uint4 qg[RPW], hg[RPW], qu[RPW], hu[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const size_t rowoff = (size_t)(row0 + r) * A.rb;
-        qg[r] = qg_ld16(G + rowoff + q4k_qoff(ch)); hg[r] = qg_ld16(G + rowoff + q4k_hoff(ch));
-        qu[r] = qg_ld16(U + rowoff + q4k_qoff(ch)); hu[r] = qg_ld16(U + rowoff + q4k_hoff(ch));
-    }
-    for (int i = 0; i < n; i++) {
-        Q4kSlice xs;
-        q4k_load_slice(xs, A.x + (size_t)tok[i] * A.D, q4k_koff(ch), true);
-        float v[2 * RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            Q4kVals vals;
-            q4k_unpack(vals, qg[r]);
-            v[r] = q4k_dot(0.0f, vals, q4k_scale(hg[r], q), xs);
-            q4k_unpack(vals, qu[r]);
-            v[RPW + r] = q4k_dot(0.0f, vals, q4k_scale(hu[r], q), xs);
-        }
-        const float sum = reduce8(v, lane);
-        const float u = __shfl_xor(sum, 32);
-        if ((lane & 39) == 0) A.mid[(size_t)slot[i] * A.F + row0 + ((lane >> 3) & 3)] = qg_swiglu(sum, u);
-    }
-}
-
-struct DownSmallArgs {
-    int nt, D, F;
-    const int *ids; const float *w; const int *tok_flag;
-    const uint8_t *down, *sh_down;
-    size_t rb, sh_rb;
-    const float *sh_logit; int ld;
-    const float *mid;
-    float *out;
-};
-
-// y for 8 consecutive rows starting at `row0` of one item (routed expert or
-// shared), from mid row `mrow`; lane results land in vals[item][0..7].
-template <int FMT>
-QG_DEV void down8(const DownSmallArgs &A, const uint8_t *W, size_t rb, int row0, int mrow, float *vals_item) {
-    const int lane = threadIdx.x & 63;
-    if (FMT == QT_IQ4_NL) {
-        const int c = lane & 7, r = lane >> 3;
-        const Iq4Raw raw = iq4_load(W + (size_t)(row0 + r) * rb + 36 * c);
-        Iq4Slice xs;
-        iq4_load_slice(xs, A.mid + (size_t)mrow * A.F, 64 * c);
-        Iq4Vals vv;
-        iq4_unpack(vv, raw);
-        const float y = qg_oct_sum(iq4_dot(vv, xs));
-        if (c == 0) vals_item[r] = y;
-    } else {
-        const int c = lane & 15, r = lane >> 4;
-        const uint8_t *pa = W + (size_t)(row0 + r) * rb, *pb = W + (size_t)(row0 + 4 + r) * rb;
-        const uint4 qa = qg_ld16(pa + q4k_qoff(c)), ha = qg_ld16(pa + q4k_hoff(c));
-        const uint4 qb = qg_ld16(pb + q4k_qoff(c)), hb = qg_ld16(pb + q4k_hoff(c));
-        Q4kSlice xs;
-        q4k_load_slice(xs, A.mid + (size_t)mrow * A.F, q4k_koff(c), true);
-        Q4kVals v;
-        q4k_unpack(v, qa);
-        const float ya = qg_row_sum(q4k_dot(0.0f, v, q4k_scale(ha, c & 7), xs));
-        q4k_unpack(v, qb);
-        const float yb = qg_row_sum(q4k_dot(0.0f, v, q4k_scale(hb, c & 7), xs));
-        if (c == 0) { vals_item[r] = ya; vals_item[4 + r] = yb; }
-    }
-}
-
-template <int FR, int FS>
-__global__ __launch_bounds__(256) void down_small_kernel(DownSmallArgs A) {
-    __shared__ float vals[SMALL_S + SMALL_B][8];
-    __shared__ int s_item[SMALL_S + SMALL_B];
-    __shared__ int s_nitems;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, row0 = blockIdx.x * 8;
-    if (wave == 0) {
-        // items in ascending order: eligible routed slots, then shared rows
-        const int ns = A.nt * QG_TOP;
-        bool el = false;
-        if (lane < ns) {
-            const int e = A.ids[lane];
-            el = e >= 0 && e < QG_EXPERTS && A.tok_flag[lane / QG_TOP] < 2;
-        }
-        const unsigned long long m = __ballot(el);
-        if (el) s_item[__popcll(m & ((1ULL << lane) - 1ULL))] = lane;
-        int n = __popcll(m);
-        const bool sh = A.sh_down && lane < A.nt && A.tok_flag[lane] < 2;
-        const unsigned long long ms = __ballot(sh);
-        if (sh) s_item[n + __popcll(ms & ((1ULL << lane) - 1ULL))] = MAXS + lane;
-        n += __popcll(ms);
-        if (lane == 0) s_nitems = n;
-    }
-    __syncthreads();
-    const int nitems = s_nitems;
-    for (int it = wave; it < nitems; it += 4) {
-        const int s = s_item[it];
-        if (s < MAXS) down8<FR>(A, A.down + (size_t)A.ids[s] * A.D * A.rb, A.rb, row0, s, vals[it]);
-        else down8<FS>(A, A.sh_down, A.sh_rb, row0, s, vals[it]);
-    }
-    __syncthreads();
-    if (tid < A.nt * 8) {
-        const int t = tid >> 3, r = tid & 7;
-        float acc = 0.0f;
-        if (A.tok_flag[t] < 2) {
-            int it = 0;
-            while (it < nitems && s_item[it] < t * QG_TOP) it++;
-            for (int k = 0; k < QG_TOP; k++) {
-                const int s = t * QG_TOP + k;
-                float v = 0.0f;
-                if (it < nitems && s_item[it] == s) { v = vals[it][r] * A.w[s]; it++; }
-                acc += v;
-            }
-            if (A.sh_down) {
-                int sh = 0;
-                while (sh < nitems && s_item[sh] != MAXS + t) sh++;
-                acc = __builtin_fmaf(vals[sh][r], qg_sig(A.sh_logit[(size_t)t * A.ld]), acc);
-            }
-        }
-        A.out[(size_t)t * A.D + row0 + r] = acc;
-    }
-}
-
 // ---------------- generic fallback (any format, any width) ----------------
 // Exact reference order per (row, token), one 32-lane half per row: the same
 // arithmetic as cpu.c's dot_group for every format.
@@ -884,41 +660,6 @@ __global__ __launch_bounds__(64) void down_generic_kernel(GenericDownArgs G) {
         const float y = exact_dot(W + (size_t)row * A.rb, G.dt, A.F, A.mid + (size_t)ent * A.F, j);
         if (j == 0) down_store(A, false, ent, row, y);
     }
-}
-
-bool small_path_ok(const qg_moe_layer *L, int nt) {
-    const bool sh = L->sh_gate != nullptr;
-    return nt <= SMALL_B && L->width == 2048 && L->ff == 512 && L->gate_type == QT_Q4_K && L->up_type == QT_Q4_K &&
-           (L->down_type == QT_Q4_K || L->down_type == QT_IQ4_NL) &&
-           (!sh || (L->sh_gate_type == QT_Q4_K && L->sh_up_type == QT_Q4_K &&
-                    (L->sh_down_type == QT_Q4_K || L->sh_down_type == QT_IQ4_NL)));
-}
-
-int launch_small(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
-                 const qg_moe_layer *L, const float *logits, int ld, Disp *ds, float *mid, hipStream_t s) {
-    const bool sh = L->sh_gate != nullptr;
-    SmallArgs A{x, nt, L->width, L->ff, logits, ld, L->resident, L->threshold,
-                (const uint8_t *)L->gate, (const uint8_t *)L->up, sh ? (const uint8_t *)L->sh_gate : nullptr,
-                sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, L->width), mid,
-                ids, weights, flags, stats, ds->tok_flag};
-    gateup_small_kernel<<<dim3(nt * QG_TOP + (sh ? 1 : 0), L->ff / 16), 256, 0, s>>>(A);
-    int rc = hipGetLastError();
-    if (rc) return rc;
-    phase_mark(2, s);
-    phase_mark(3, s);
-    DownSmallArgs D{nt, L->width, L->ff, ids, weights, ds->tok_flag, (const uint8_t *)L->down,
-                    sh ? (const uint8_t *)L->sh_down : nullptr, qg_row_bytes_host(L->down_type, L->ff),
-                    sh ? qg_row_bytes_host(L->sh_down_type, L->ff) : 0, logits + QG_EXPERTS, ld, mid, out};
-    const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
-    const dim3 grid(L->width / 8);
-    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) down_small_kernel<QT_IQ4_NL, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
-    else if (fr == QT_IQ4_NL) down_small_kernel<QT_IQ4_NL, QT_Q4_K><<<grid, 256, 0, s>>>(D);
-    else if (fs == QT_IQ4_NL) down_small_kernel<QT_Q4_K, QT_IQ4_NL><<<grid, 256, 0, s>>>(D);
-    else down_small_kernel<QT_Q4_K, QT_Q4_K><<<grid, 256, 0, s>>>(D);
-    rc = hipGetLastError();
-    phase_mark(4, s);
-    phase_mark(5, s);
-    return rc;
 }
 
 // ---------------- expert-phase launcher shared by forward and mtp_moe ----------------
@@ -1073,16 +814,18 @@ int qg_moe_phase_events(void **events, int n) {
     return hipSuccess;
 }
 
-size_t qg_moe_workspace_bytes(int width, int ff, int tokens) {
+size_t qg_generic_workspace_bytes(int width, int ff, int tokens) {
     if (width < 256 || width % 256 || width > 8192 || ff < 32 || ff % 32 || ff > 4096 || tokens < 1 || tokens > MAXB) return 0;
     return ws_layout(width, ff).total;
 }
 
-int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
-                   const qg_moe_layer *L, void *workspace, size_t ws_bytes) {
+// The layer for any supported format and width (the fallback of
+// qg_moe_forward); arguments already validated by the caller.
+int qg_generic_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
+                       const qg_moe_layer *L, void *workspace, size_t ws_bytes) {
     if (!out || !ids || !weights || !x || !L || !workspace || nt < 1 || nt > MAXB) return hipErrorInvalidValue;
     const int D = L->width, F = L->ff;
-    const size_t need = qg_moe_workspace_bytes(D, F, nt);
+    const size_t need = qg_generic_workspace_bytes(D, F, nt);
     if (!need || ws_bytes < need || !L->router || !L->gate || !L->up || !L->down) return hipErrorInvalidValue;
     if (!qg_row_bytes_host(L->gate_type, D) || !qg_row_bytes_host(L->up_type, D) || !qg_row_bytes_host(L->down_type, F))
         return hipErrorInvalidValue;
@@ -1102,8 +845,6 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
                                     sh ? (const uint8_t *)L->sh_gate_inp : nullptr, s);
     if (rc) return rc;
     phase_mark(1, s);
-    if (small_path_ok(L, nt))
-        return launch_small(out, ids, weights, flags, stats, x, nt, L, logits, rows, ds, (float *)(ws + lay.mid), s);
     _Float16 *xh = (_Float16 *)(ws + lay.xh);
     float *xs = (float *)(ws + lay.xs);
     route_dispatch_kernel<<<1, RD_THREADS, 0, s>>>(ids, weights, flags, stats, logits, rows, nt, L->resident, L->threshold, ds,
@@ -1149,7 +890,7 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
     Disp *ds = (Disp *)(ws + lay.disp);
     _Float16 *xh = (_Float16 *)(ws + lay.xh);
     float *xs = (float *)(ws + lay.xs);
-    const bool planes = nt > SMALL_B;  // matrix-core expert kernels for the larger groups
+    const bool planes = nt > 4;  // matrix-core expert kernels for groups above four tokens
     dispatch_ids_kernel<<<1, RD_THREADS, 0, s>>>(ids, nt, ds, mid, slots, D, F, x, planes ? xh : nullptr, xs);
     int rc = hipGetLastError();
     if (rc) return rc;

@@ -152,14 +152,16 @@ __global__ void binary_kernel(float *o, const float *a, const float *b, int n, i
 }
 
 // ------------------------------------------------------------------------
-// Routing (gpu.cu:456-465).  One wave per token; lane l holds logits
-// l, l+64, ..., l+448.  Ten rounds of wave argmax with the lowest index
-// among equal maxima (the reference's strict-greater scan from index 0),
-// numerators exp(s - max) summed in rank order, then divided by the sum.
+// Routing (gpu.cu:456-465).  One wave per token (qg_route_fast): the 10
+// winners by value with the lowest index among equal values (the reference's
+// strict-greater scan from index 0), numerators exp(s - max) summed in rank
+// order, then divided by the sum.
 // ------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void route_kernel(int *ids, float *weights, const float *logits, int nt, int ld) {
+    __shared__ float s_v[64];
+    __shared__ int s_i[64];
     const int t = blockIdx.x;
-    qg_route_wave(ids + (size_t)t * QG_TOP, weights + (size_t)t * QG_TOP, logits + (size_t)t * ld, threadIdx.x);
+    qg_route_wave(ids + (size_t)t * QG_TOP, weights + (size_t)t * QG_TOP, logits + (size_t)t * ld, threadIdx.x, s_v, s_i);
 }
 
 // Pruning (gpu.cu:467-483), one thread per token, device atomics for the

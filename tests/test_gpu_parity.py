@@ -420,3 +420,45 @@ def test_forward_rejects_bad_arguments(layer0):
     assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 18, C.byref(L.desc), fw.ws.p, fw.ws_bytes) != 0
     assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 1, C.byref(L.desc), fw.ws.p, 16) != 0
     assert lib.qg_moe_workspace_bytes(2048, 512, 18) == 0
+
+
+def test_layer_generic_fallback_width(qgl):
+    """A width the decode fast path does not take (D=1024, F=256) runs the
+    generic kernels behind the same entry point; same bars."""
+    spec = synth.LayerSpec(seed=404, width=1024, ff=256, down_type=20, shared=True)
+    L = synth.build_layer(spec)
+    H = O.HostLayer(spec.seed, width=1024, ff=256, gt=12, ut=12, dt=20, shared=True, sh_types=(12, 12, 12))
+    for nt in (1, 6):
+        x = synth.inputs(12 + nt, nt, 1024, correlated=True)
+        fw = synth.Forward(1024, 256, nt)
+        fw.x.set(x)
+        say(f"forward generic D=1024 nt={nt}")
+        fw.run(L, nt)
+        qg.call("sync")
+        out, ids, w, *_ = H.forward(x)
+        np.testing.assert_array_equal(fw.ids.get()[:nt], ids)
+        np.testing.assert_array_equal(fw.w.get()[:nt].view('u4'), w.view('u4'))
+        assert_close(fw.out.get()[:nt], out, f"generic nt={nt}")
+
+
+@pytest.mark.parametrize("nt", [3, 17])
+def test_forward_residual_matches_forward(layer1, nt):
+    """qg_moe_forward_residual(h) == h + qg_moe_forward(RMSNorm(h)) with the
+    normalised rows it reports, and the routing of those rows is the oracle's."""
+    L, H = layer1
+    h0 = (synth.inputs(900 + nt, nt, 2048, correlated=True) * 3.0).astype(np.float32)
+    fw = synth.Forward(2048, 512, nt)
+    hd = Device(h0)
+    xn = Device(shape=(nt, 2048), dtype=np.float32)
+    out = Device(shape=(nt, 2048), dtype=np.float32)
+    say(f"forward_residual nt={nt}")
+    call("moe_forward_residual", hd.p, fw.ids.p, fw.w.p, fw.flags.p, None, xn.p, out.p, nt, C.byref(L.desc), fw.ws.p, fw.ws_bytes)
+    qg.call("sync")
+    xs = xn.get()
+    ref = synth.rmsnorm(h0)
+    np.testing.assert_allclose(xs, ref, rtol=2e-6, atol=2e-6)
+    want, ids, w, *_ = H.forward(xs)
+    np.testing.assert_array_equal(fw.ids.get()[:nt], ids)
+    np.testing.assert_array_equal(fw.w.get()[:nt].view('u4'), w.view('u4'))
+    assert_close(out.get(), want, f"residual out nt={nt}")
+    np.testing.assert_array_equal(hd.get(), (h0 + out.get()).astype(np.float32))
