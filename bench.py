@@ -14,6 +14,10 @@ before the timed region.
             layer, replayed as one captured graph (43.5 GB of experts).
 --config 4: config 1 with 128 of 512 experts resident per layer and the 90 %
             coverage flags.
+--config 3: the 2048-token prefill (Zipf(1.1)-biased router, Q4_K gate/up,
+            IQ4_NL down): value = tokens/s of the layer; roofline = the
+            matrix-core utilisation of the dense pass (experts with >= 256
+            rows) of the grouped gate/up GEMM against the int8 peak.
 
 Printed: one JSON line.  value = tokens/s (batch / step time), the step being
 one replay of the layer's captured graph; roofline = the gate/up kernel's
@@ -47,6 +51,11 @@ ROUTER_BYTES = EXPERTS * D * 4
 HBM_PEAK_GBS = 8000.0
 METRIC = "routed-MoE tokens/s + % HBM peak at B=1/17; int8 MFMA util at 2048-tok prefill"
 KERNELS = ["router", "route", "gate_up", "down"]
+PF_KERNELS = ["router", "route", "scan", "fill", "gate_up_dense", "gate_up_other", "down_dense", "down_other",
+              "down_shared", "combine"]
+INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 MFMA (POP/s x 1e3)
+FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 MFMA
+DENSE_MIN = 256                   # rows from which an expert runs in the dense pass
 
 
 def layer_bytes(nt: int, unique: float, shared: bool) -> float:
@@ -148,15 +157,23 @@ def time_decode(wl: Workload, steps: int, warmup: int):
     ms = qg.elapsed_ms(b, e) / steps
     for g in graphs:
         qg.lib().qg_graph_destroy(g)
-    evs = [[qg.Event() for _ in range(8)] for _ in range(steps)]
-    arrs = [(C.c_void_p * 8)(*[ev.p for ev in evs_i]) for evs_i in evs]
+    return ms, kernel_times(wl.step, KERNELS, steps)
+
+
+def kernel_times(step, names, steps) -> dict:
+    """Average duration (ms) of each named kernel of a step over `steps`
+    eagerly launched steps, from events the dispatches record themselves
+    (qg_moe_kernel_events); kernels that did not run are left out."""
+    n = 2 * len(names)
+    evs = [[qg.Event() for _ in range(n)] for _ in range(steps)]
+    arrs = [(C.c_void_p * n)(*[ev.p for ev in evs_i]) for evs_i in evs]
     for i in range(steps):
-        qg.call("moe_kernel_events", arrs[i], 8)
-        wl.step(i)
+        qg.call("moe_kernel_events", arrs[i], n)
+        step(i)
     qg.call("moe_kernel_events", None, 0)
     qg.call("sync")
     kern = {}
-    for k, name in enumerate(KERNELS):
+    for k, name in enumerate(names):
         vals = []
         for ev in evs:
             t = C.c_float()
@@ -164,10 +181,10 @@ def time_decode(wl: Workload, steps: int, warmup: int):
                 vals.append(t.value)
         if vals:
             kern[name] = float(np.mean(vals))
-    return ms, kern
+    return kern
 
 
-def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
+def cpu_baseline(wl, budget_s: float, tokens: int | None = None) -> dict | None:
     """The reference's cpu.c on layer 0 of the workload: router qc_matmul (F32),
     qc_moe on the routed experts, shared expert through qc_matmul x 3 plus the
     sigmoid-gated add.  Routing ids/weights come from the GPU run of the same
@@ -182,9 +199,10 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
     if ref is None:
         return None
     L = wl.layers[0]
+    nt = min(wl.nt, tokens or wl.nt)
     ids, _ = wl.routing(0)
-    ids = ids.copy()
-    w = wl.fw.w.get()[:wl.nt].copy()
+    ids = np.ascontiguousarray(ids[:nt])
+    w = np.ascontiguousarray(wl.fw.w.get()[:nt])
     s = L.spec
     per = {"gate": FF * qg.row_bytes(s.gate_type, D), "up": FF * qg.row_bytes(s.up_type, D), "down": D * qg.row_bytes(s.down_type, FF)}
     host = {k: np.zeros(EXPERTS * v, np.uint8) for k, v in per.items()}
@@ -201,15 +219,14 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
             shared[name] = buf
     cores = len(os.sched_getaffinity(0))
     threads = max(1, min(28, cores))
-    ws = ref.qc_create(max(wl.nt, 1), threads)
-    nt = wl.nt
+    ws = ref.qc_create(max(nt, 1), threads)
     out = np.empty((nt, D), np.float32)
     logits = np.empty((nt, EXPERTS), np.float32)
     g = np.empty((nt, FF), np.float32)
     u = np.empty((nt, FF), np.float32)
     so = np.empty((nt, D), np.float32)
     lg = np.empty((nt, 1), np.float32)
-    x = np.ascontiguousarray(wl.x, np.float32)
+    x = np.ascontiguousarray(wl.x[:nt], np.float32)
 
     def run():
         assert ref.qc_matmul(logits.ctypes.data, router.ctypes.data, 0, EXPERTS, D, x.ctypes.data, nt, threads) == 0
@@ -237,7 +254,9 @@ def cpu_baseline(wl: Workload, budget_s: float) -> dict | None:
     med = float(np.median(times))
     parts = "router qc_matmul + qc_moe" + (" + shared expert (3 qc_matmul + gate)" if wl.shared else "")
     return {"value": round(nt / med, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"cpu.c {parts} on layer 0, {nt} tokens, isa={ref.qc_backend_name().decode()}; "
+            "sample": f"cpu.c {parts} on layer 0, {nt} tokens"
+                      f"{f' (the first {nt} of the {wl.nt}-token batch, their GPU routing)' if nt < wl.nt else ''}, "
+                      f"isa={ref.qc_backend_name().decode()}; "
                       f"median of {len(times)} runs after 3 warm-ups; OMP threads={threads} of {cores} host CPUs"}
 
 
@@ -272,12 +291,90 @@ def bench_stack(args) -> dict:
     return {"ms": ms, "layers": n_layers, "bytes": nbytes, "steps": steps}
 
 
+class PrefillWorkload:
+    """Config 3: one layer (906 MB of experts, above the 256 MB Infinity
+    Cache), 2048 seeded RMS-normed tokens, Zipf(1.1)-biased router."""
+
+    def __init__(self, nt: int, seed: int):
+        self.nt, self.shared = nt, False
+        self.spec = synth.LayerSpec(seed=seed, gate_type=12, up_type=12, down_type=20, bias_seed=seed + 1)
+        self.layers = [synth.build_layer(self.spec)]
+        self.fw = synth.Forward(D, FF, nt)
+        self.x = synth.inputs(seed + 2, nt, D)
+        self.fw.x.set(self.x)
+
+    def step(self, i: int = 0) -> None:
+        self.fw.run(self.layers[0], self.nt)
+
+    def routing(self, i: int = 0):
+        self.step()
+        qg.call("sync")
+        return self.fw.ids.get()[:self.nt], self.fw.flags.get()[:self.nt]
+
+
+def bench_prefill(args, data: str) -> dict:
+    nt = args.batch if args.batch is not None else 2048
+    wl = PrefillWorkload(nt, seed=9300)
+    ids, _ = wl.routing()
+    n_e = np.bincount(ids[ids >= 0].ravel(), minlength=EXPERTS)
+    dense = n_e >= DENSE_MIN
+    g = C.c_void_p()
+    qg.call("graph_begin", C.byref(g))
+    wl.step()
+    qg.call("graph_end", g)
+    for _ in range(args.warmup):
+        qg.call("graph_launch", g)
+    qg.call("sync")
+    b, e = qg.Event(), qg.Event()
+    b.record()
+    for _ in range(args.steps):
+        qg.call("graph_launch", g)
+    e.record()
+    qg.call("sync")
+    ms = qg.elapsed_ms(b, e) / args.steps
+    qg.lib().qg_graph_destroy(g)
+    kern = kernel_times(wl.step, PF_KERNELS, args.steps)
+    # algorithmic matrix-core work: 2 ops per multiply-add of the useful products
+    ops_gu = lambda rows: 2.0 * rows * 2 * D * FF
+    ops_dn = lambda rows: 2.0 * rows * D * FF
+    rows_dense, rows_all = int(n_e[dense].sum()), int(n_e.sum())
+    t_gu = kern.get("gate_up_dense")
+    achieved = ops_gu(rows_dense) / (t_gu * 1e-3) / 1e12 if t_gu and rows_dense else None
+    t_dense = (kern.get("gate_up_dense", 0) + kern.get("down_dense", 0)) or None
+    util_dense = (ops_gu(rows_dense) + ops_dn(rows_dense)) / (t_dense * 1e-3) / 1e12 / INT8_PEAK_TOPS if t_dense and rows_dense else None
+    t_experts = sum(kern.get(k, 0) for k in ("gate_up_dense", "gate_up_other", "down_dense", "down_other", "down_shared"))
+    touched = int(np.count_nonzero(n_e))
+    layer_b = ROUTER_BYTES + touched * EXPERT_BYTES + nt * (2 * D * 4 + 80)
+    line = {
+        "metric": METRIC, "value": round(nt / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": data,
+        "config": {"workload": f"config3: routed-MoE prefill, B={nt}, D=2048, 512 experts top-10, F=512, Q4_K gate/up, "
+                               "IQ4_NL down, router biased to Zipf(1.1) expert popularity; one captured graph per step",
+                   "batch_tokens": nt, "experts_touched": touched, "dense_experts": int(dense.sum()),
+                   "dense_rows": rows_dense, "rows": rows_all, "max_rows": int(n_e.max()),
+                   "matrix_cores": "fp16 16x16x32 MFMA, exact integer weights x fp16 hi/lo activation planes, fp32 accumulate",
+                   "dense_pass_int8_util_algorithmic": round(util_dense, 4) if util_dense else None,
+                   "dense_pass_fp16_util_issued": round(2 * util_dense * INT8_PEAK_TOPS / FP16_PEAK_TFLOPS, 4) if util_dense else None,
+                   "expert_gemm_TOPS_all": round((ops_gu(rows_all) + ops_dn(rows_all)) / (t_experts * 1e-3) / 1e12, 1) if t_experts else None,
+                   "layer_bytes": int(layer_b), "layer_hbm_frac": round(layer_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
+        "roofline": {"bound": "mfma", "kernel": "gate_up_dense", "achieved": round(achieved, 1) if achieved else None,
+                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4) if achieved else None,
+                     "traffic": load_traffic(f"gate_up_dense_config3_B{nt}"), "algorithmic_ops": ops_gu(rows_dense)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget, tokens=min(nt, 128))
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 4))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -287,11 +384,17 @@ def main() -> int:
         print(f"bench.py measures one GPU's share of the layer; --gpus {args.gpus} is not supported "
               "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
         return 2
+    data = "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)"
+    if args.config == 3:
+        if args.batch is not None and not 18 <= args.batch <= 8192:
+            print("prefill batch must be 18..8192", file=sys.stderr)
+            return 2
+        print(json.dumps(bench_prefill(args, data)), flush=True)
+        return 0
     batch = args.batch if args.batch is not None else (17 if args.config in (1, 4) else 1)
     if not 1 <= batch <= 17:
         print("decode batch must be 1..17", file=sys.stderr)
         return 2
-    data = "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)"
 
     if args.config == 2:
         r = bench_stack(args)

@@ -85,7 +85,8 @@ int qg_moe_configure(int width, int ff);
  * [512, tokens] map and the host count loop of qwen.c:650-655.  offsets[513];
  * entries offsets[e]..offsets[e+1]-1 list (ascending token) the selections of
  * expert e: row_token = t, row_slot = t*10+k.  Ids in [-513,-2] (pruned) are
- * skipped; any other id outside [0,512) makes *status nonzero. */
+ * skipped; any other id outside [0,512), or a token listing an expert twice,
+ * makes *status nonzero (the lists are then unspecified). */
 int qg_moe_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int tokens);
 
 /* One routed-MoE layer, device-driven (no host read of routing ids), so it
@@ -104,6 +105,8 @@ typedef struct {
     const float *sh_gate_inp;                   /* F32 [1, D] (ffn_gate_inp_shexp) */
     const unsigned char *resident;              /* 512-byte device mask or NULL */
     double threshold;                           /* omitted-mass threshold (0.10, config.py:9) */
+    const float *router_bias;                   /* F32 [512] added to every logit before routing, or NULL
+                                                   (synthetic workloads; the reference's router has no bias) */
 } qg_moe_layer;
 
 /* Device workspace bytes for qg_moe_forward / qg_moe_forward_residual at up
@@ -116,7 +119,9 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
  * 2 handoff (coverage below 1-threshold), 3 invalid router distribution;
  * stats may be NULL.  With flags==2 the token's output row is not computed
  * here (it belongs to the host handoff, qwen.c:658-678) and is written as 0.
- * tokens 1..17. */
+ * tokens 1..8192: up to 17 the decode kernels (any format qg_matmul takes);
+ * above, the prefill grouped GEMMs, which need Q4_K gate/up, Q4_K or IQ4_NL
+ * down, D a multiple of 256 and F a multiple of 128 (else an error). */
 int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                    const float *x, int tokens, const qg_moe_layer *layer, void *workspace, size_t workspace_bytes);
 
@@ -130,9 +135,13 @@ int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *f
                             void *workspace, size_t workspace_bytes);
 
 /* Benchmark support: events[2i] and events[2i+1] (qg_event_create handles)
- * are recorded at the start and end of kernel i of this thread's decode-path
- * qg_moe_forward calls (0 router, 1 routing, 2 gate/up, 3 down), timestamped
- * by the dispatch itself (hipExtLaunchKernelGGL).  n = 0 disables. */
+ * are recorded at the start and end of kernel i of this thread's
+ * qg_moe_forward calls, timestamped by the dispatch itself
+ * (hipExtLaunchKernelGGL).  Decode: 0 router, 1 routing, 2 gate/up, 3 down.
+ * Prefill: 0 router, 1 routing, 2 scan, 3 fill, 4 gate/up dense pass,
+ * 5 gate/up other experts, 6 down dense pass, 7 down other experts,
+ * 8 shared-expert down (when its format differs), 9 combine.  n <= 32;
+ * n = 0 disables. */
 int qg_moe_kernel_events(void **events, int n);
 
 /* Benchmark support: record events[i] (qg_event_create handles) on the

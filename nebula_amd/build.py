@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
-HIP_SOURCES = ["qg_runtime.hip", "qg_ops.hip", "qg_moe.hip", "qg_decode.hip", "nb_synth.hip"]
+HIP_SOURCES = ["qg_runtime.hip", "qg_ops.hip", "qg_moe.hip", "qg_decode.hip", "qg_prefill.hip", "nb_synth.hip"]
 HOST_SOURCES = ["moe_host.c"]
 ARCH = os.environ.get("NEBULA_OFFLOAD_ARCH", "gfx950")
 

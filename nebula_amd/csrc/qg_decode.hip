@@ -24,20 +24,11 @@
 //                then the router-rank sum of the 10 slots, the sigmoid-gated
 //                shared expert and the optional residual add, in-block.
 //
-// Operand conventions (16x16x32 f16 MFMA, lane l: j = l%16, kq = l/16):
-//   A = activations, row j = (token j/2, plane j%2), lane supplies 8 k-values;
-//   B = weights, column j = weight row j, lane supplies the same 8 k-values;
-//   D[token-plane][weight row]: lane holds rows 4kq..4kq+3 = tokens 2kq,2kq+1
-//   (hi, lo) of column j.
-// K order inside a Q4_K superblock: MFMA m (0..7), lane kq takes 16-byte qs
-// chunks kq and kq+4; chunk c's fragment f (0..3) = (low/high nibbles) x
-// (bytes 0-7 / 8-15).  Every weight enters as s_g*q (an integer <= 945, exact
-// in fp16), so elements of different groups may share an MFMA; the superblock
-// scale d and the min term dmin*sum_g m_g*X_g are applied in fp32.  IQ4_NL:
-// one MFMA per 32-element block, lane kq takes qs bytes 4kq..4kq+3, the block
-// scale is applied in fp32.  Activation planes are stored in the matching
-// permuted order (pos_q4k / pos_iq4), so every A fragment is one 16-byte load.
+// Operand conventions and the K order of the weight formats are those of
+// qg_frag.h; here A row j = (token j/2, plane j%2), so a lane's D rows
+// 4kq..4kq+3 are tokens 2kq, 2kq+1 (hi, lo) of weight row j.
 #include "qg_internal.h"
+#include "qg_frag.h"
 #include <hip/hip_ext.h>
 
 namespace {
@@ -69,7 +60,7 @@ DecLayout dec_layout(int D, int F) {
 // Optional kernel timing (benchmark support): events[2i], events[2i+1] are
 // recorded at the start and end of kernel i (0 router, 1 route, 2 gate/up,
 // 3 down) by hipExtLaunchKernelGGL on the launch stream.
-thread_local void *tl_kev[8] = {nullptr};
+thread_local void *tl_kev[32] = {nullptr};
 thread_local int tl_kev_n = 0;
 
 template <typename K, typename... Args>
@@ -81,65 +72,6 @@ void dec_launch(int slot, K kernel, dim3 grid, dim3 block, size_t lds, hipStream
         hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
 }
 
-// Plane position of element e (0..255) of a Q4_K superblock (see header).
-QG_DEV int pos_q4k(int e) {
-    const int g = e >> 5, l = e & 31, nib = g & 1, gp = g >> 1, h = l >> 4, p = l & 15;
-    const int c = 2 * gp + h, kq = c & 3, ci = c >> 2, f = 2 * nib + (p >> 3);
-    return ((4 * ci + f) * 4 + kq) * 8 + qg_perm8(p & 7);
-}
-QG_DEV int qg_perm4(int i) { return ((i & 1) << 1) | ((i & 2) >> 1); }  // 0,2,1,3
-// Plane position of element e (0..31) of an IQ4_NL block.
-QG_DEV int pos_iq4(int e) {
-    const int hi = e >> 4, r = e & 15;
-    return (r >> 2) * 8 + 4 * hi + qg_perm4(r & 3);
-}
-QG_DEV int plane_pos(int fmt, int k) {
-    return fmt == QT_IQ4_NL ? (k & ~31) | pos_iq4(k & 31) : (k & ~255) | pos_q4k(k & 255);
-}
-
-// The 8 fp16 values s*q of one fragment of a Q4_K qs chunk (c = 16 bytes):
-// f bit 1 = high nibbles, f bit 0 = bytes 8..15.
-QG_DEV qg_half8 q4k_chunk_frag(uint4 c, int f, _Float16 s) {
-    return q4_frag((f & 1) ? make_uint2(c.z, c.w) : make_uint2(c.x, c.y), f >> 1, s);
-}
-
-// 4 IQ4_NL qs bytes -> 8 table values in fp16: slots 0..3 = low nibbles of
-// bytes (0,2,1,3), slots 4..7 = high nibbles of bytes (0,2,1,3).
-QG_DEV qg_half8 iq4_frag4(uint32_t q) {
-    const uint32_t lo = iq4_lookup(q & 0x0F0F0F0Fu), hi = iq4_lookup((q >> 4) & 0x0F0F0F0Fu);
-    const uint32_t u[4] = {(lo & 0x00FF00FFu) | 0x64006400u, ((lo >> 8) & 0x00FF00FFu) | 0x64006400u,
-                           (hi & 0x00FF00FFu) | 0x64006400u, ((hi >> 8) & 0x00FF00FFu) | 0x64006400u};
-    const qg_half2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
-    qg_half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
-    }
-    return r;
-}
-
-QG_DEV qg_half8 ld_frag(const _Float16 *p) { return __builtin_bit_cast(qg_half8, *(const uint4 *)p); }
-
-typedef __attribute__((address_space(3))) void qg_lds_void;
-
-// Direct global->shared copy of 16 bytes per lane (gfx950 global_load_lds
-// b128): lane l's 16 bytes land at lds_base + 16*l, lds_base uniform across
-// the wave.  Completion is tracked by the vector-memory counter.
-QG_DEV void dma16(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (qg_lds_void *)lds_base, 16, 0, 0);
-}
-QG_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
-
-// 1/sqrt(mean(x^2) + eps) of one row, summed lane-strided then across the
-// wave; every caller runs this same code, so all blocks agree bit for bit.
-QG_DEV float row_rms_scale(const float *xr, int D, float eps, int lane) {
-    float ss = 0.0f;
-    for (int i = lane; i < D; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
-    ss = qg_sum_lanes<64>(ss);
-    return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
-}
 
 // ---------------- K1: router + activation planes ----------------
 struct RouterArgs {
@@ -150,6 +82,7 @@ struct RouterArgs {
     int norm; float eps; float *xn; // RMS-normalise the input; normalised rows to xn
     _Float16 *xp, *xsp;             // planes [nt][2][D] (Q4_K order); planes of 32-group sums [nt][2][D/32]
     int row_pairs;                  // blockIdx.x < row_pairs: router rows; == row_pairs: planes
+    const float *bias;              // F32 [512] added to the expert logits, or null
 };
 
 // Grid (row_pairs + 1, ceil(nt/4)), 4 waves per block, wave w = token
@@ -167,23 +100,8 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     const float *xr = A.x + (size_t)t * A.D;
     const float sc = A.norm ? row_rms_scale(xr, A.D, A.eps, lane) : 1.0f;
     if (blockIdx.x == A.row_pairs) {
-        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *lo = hi + A.D;
-        for (int e = lane; e < A.D; e += 64) {
-            const float v = A.norm ? xr[e] * sc : xr[e];
-            if (A.norm && A.xn) A.xn[(size_t)t * A.D + e] = v;
-            const _Float16 h = (_Float16)v;
-            const int p = plane_pos(QT_Q4_K, e);
-            hi[p] = h;
-            lo[p] = (_Float16)(v - (float)h);
-        }
-        _Float16 *shi = A.xsp + (size_t)t * 2 * (A.D / 32), *slo = shi + A.D / 32;
-        for (int g = lane; g < A.D / 32; g += 64) {
-            float s = 0.0f;
-            for (int l = 0; l < 32; l++) s += A.norm ? xr[32 * g + l] * sc : xr[32 * g + l];
-            const _Float16 h = (_Float16)s;
-            shi[g] = h;
-            slo[g] = (_Float16)(s - (float)h);
-        }
+        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
+        token_planes(xr, A.D, A.norm != 0, sc, lane, hi, hi + A.D, shi, shi + A.D / 32, A.xn ? A.xn + (size_t)t * A.D : nullptr);
         return;
     }
     const int row = blockIdx.x * 2 + half;
@@ -209,7 +127,7 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
         acc = __builtin_fmaf(wr[k0 + j], xv, acc);
     }
     const float r = qg_tree32(acc);
-    if (j == 0 && rok) A.logits[(size_t)t * A.rows + row] = r;
+    if (j == 0 && rok) A.logits[(size_t)t * A.rows + row] = A.bias && row < QG_EXPERTS ? r + A.bias[row] : r;
 }
 
 // ---------------- KR: routing, one wave per token (B > 4) ----------------
@@ -728,7 +646,8 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     _Float16 *xsp = (_Float16 *)(ws + lay.xsum);
     const int rows = QG_EXPERTS + (sh ? 1 : 0);
     const int row_pairs = (rows + 1) / 2;
-    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_pairs};
+    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_pairs,
+                 L->router_bias};
     dec_launch(0, dec_router_kernel, dim3(row_pairs + 1, (nt + 3) / 4), dim3(256), 0, s, R);
     int rc = hipGetLastError();
     if (rc) return rc;
@@ -769,7 +688,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
 }
 
 int validate_layer(const qg_moe_layer *L, int nt) {
-    if (!L || nt < 1 || nt > MB) return hipErrorInvalidValue;
+    if (!L || nt < 1 || nt > QG_MAX_TOKENS) return hipErrorInvalidValue;
     const int D = L->width, F = L->ff;
     if (D < 256 || D % 256 || D > 8192 || F < 32 || F % 32 || F > 4096) return hipErrorInvalidValue;
     if (!L->router || !L->gate || !L->up || !L->down) return hipErrorInvalidValue;
@@ -779,6 +698,7 @@ int validate_layer(const qg_moe_layer *L, int nt) {
                        !qg_row_bytes_host(L->sh_up_type, D) || !qg_row_bytes_host(L->sh_down_type, F)))
         return hipErrorInvalidValue;
     if (L->resident && (L->threshold < 0 || L->threshold > 0.1 || !__builtin_isfinite(L->threshold))) return hipErrorInvalidValue;
+    if (nt > MB && !qg_prefill_ok(L)) return hipErrorInvalidValue;
     return hipSuccess;
 }
 
@@ -789,9 +709,17 @@ __global__ void add_rows_kernel(float *h, const float *o, size_t n) {
 
 }  // namespace
 
+bool qg_kernel_event_pair(int slot, void **begin, void **end) {
+    if (slot < 0 || 2 * slot + 1 >= tl_kev_n || !tl_kev[2 * slot] || !tl_kev[2 * slot + 1]) return false;
+    *begin = tl_kev[2 * slot];
+    *end = tl_kev[2 * slot + 1];
+    return true;
+}
+
 extern "C" {
 
 size_t qg_moe_workspace_bytes(int width, int ff, int tokens) {
+    if (tokens > MB) return qg_prefill_workspace_bytes(width, ff, tokens);
     const size_t g = qg_generic_workspace_bytes(width, ff, tokens);
     if (!g) return 0;
     // the residual form keeps the normalised input and the layer output of the
@@ -802,8 +730,8 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens) {
 }
 
 int qg_moe_kernel_events(void **events, int n) {
-    if (n < 0 || n > 8 || (n && !events)) return hipErrorInvalidValue;
-    for (int i = 0; i < 8; i++) tl_kev[i] = i < n ? events[i] : nullptr;
+    if (n < 0 || n > 32 || (n && !events)) return hipErrorInvalidValue;
+    for (int i = 0; i < 32; i++) tl_kev[i] = i < n ? events[i] : nullptr;
     tl_kev_n = n;
     return hipSuccess;
 }
@@ -814,6 +742,7 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
     if (rc) return rc;
     if (!out || !ids || !weights || !x || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt))
         return hipErrorInvalidValue;
+    if (nt > MB) return qg_prefill_forward(out, nullptr, ids, weights, flags, stats, x, nullptr, 0, nt, L, workspace);
     if (!dec_ok(L)) return qg_generic_forward(out, ids, weights, flags, stats, x, nt, L, workspace, ws_bytes);
     return dec_forward(out, nullptr, ids, weights, flags, stats, x, nullptr, 0, nt, L, (uint8_t *)workspace);
 }
@@ -824,6 +753,7 @@ int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *f
     if (rc) return rc;
     if (!h || !ids || !weights || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt))
         return hipErrorInvalidValue;
+    if (nt > MB) return qg_prefill_forward(out, h, ids, weights, flags, stats, h, xn_out, 1, nt, L, workspace);
     if (dec_ok(L)) return dec_forward(out, h, ids, weights, flags, stats, h, xn_out, 1, nt, L, (uint8_t *)workspace);
     // generic form: normalise into the workspace tail, run the layer, add
     const int D = L->width;

@@ -1,0 +1,110 @@
+// Matrix-core operand helpers shared by the decode and prefill kernels.
+//
+// Operand conventions (v_mfma_f32_16x16x32_f16, lane l: j = l%16, kq = l/16):
+// A = activations (row j = one token, or one token-plane), lane supplies 8
+// k-values; B = weights, column j = weight row j, lane supplies the same 8
+// k-values; D[row][weight row]: lane holds rows 4kq..4kq+3 of column j.
+// K order inside a Q4_K superblock: MFMA m (0..7), lane kq takes 16-byte qs
+// chunks kq and kq+4; chunk c's fragment f (0..3) = (low/high nibbles) x
+// (bytes 0-7 / 8-15).  Every weight enters as s_g*q (an integer <= 945, exact
+// in fp16), so elements of different groups may share an MFMA; the superblock
+// scale d and the min term dmin*sum_g m_g*X_g are applied in fp32.  IQ4_NL:
+// one MFMA per 32-element block, lane kq takes qs bytes 4kq..4kq+3, the block
+// scale is applied in fp32.  Activation planes (fp16 hi and lo = x - hi) are
+// stored in the matching permuted order (pos_q4k / pos_iq4), so every A
+// fragment is one 16-byte load.
+#pragma once
+#include "qg_common.h"
+
+// Plane position of element e (0..255) of a Q4_K superblock.
+QG_DEV int pos_q4k(int e) {
+    const int g = e >> 5, l = e & 31, nib = g & 1, gp = g >> 1, h = l >> 4, p = l & 15;
+    const int c = 2 * gp + h, kq = c & 3, ci = c >> 2, f = 2 * nib + (p >> 3);
+    return ((4 * ci + f) * 4 + kq) * 8 + qg_perm8(p & 7);
+}
+QG_DEV int qg_perm4(int i) { return ((i & 1) << 1) | ((i & 2) >> 1); }  // 0,2,1,3
+// Plane position of element e (0..31) of an IQ4_NL block.
+QG_DEV int pos_iq4(int e) {
+    const int hi = e >> 4, r = e & 15;
+    return (r >> 2) * 8 + 4 * hi + qg_perm4(r & 3);
+}
+QG_DEV int plane_pos(int fmt, int k) {
+    return fmt == QT_IQ4_NL ? (k & ~31) | pos_iq4(k & 31) : (k & ~255) | pos_q4k(k & 255);
+}
+
+// The 8 fp16 values s*q of one fragment of a Q4_K qs chunk (c = 16 bytes):
+// f bit 1 = high nibbles, f bit 0 = bytes 8..15.
+QG_DEV qg_half8 q4k_chunk_frag(uint4 c, int f, _Float16 s) {
+    return q4_frag((f & 1) ? make_uint2(c.z, c.w) : make_uint2(c.x, c.y), f >> 1, s);
+}
+
+// 4 IQ4_NL qs bytes -> 8 table values in fp16: slots 0..3 = low nibbles of
+// bytes (0,2,1,3), slots 4..7 = high nibbles of bytes (0,2,1,3).
+QG_DEV qg_half8 iq4_frag4(uint32_t q) {
+    const uint32_t lo = iq4_lookup(q & 0x0F0F0F0Fu), hi = iq4_lookup((q >> 4) & 0x0F0F0F0Fu);
+    const uint32_t u[4] = {(lo & 0x00FF00FFu) | 0x64006400u, ((lo >> 8) & 0x00FF00FFu) | 0x64006400u,
+                           (hi & 0x00FF00FFu) | 0x64006400u, ((hi >> 8) & 0x00FF00FFu) | 0x64006400u};
+    const qg_half2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
+    qg_half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+QG_DEV qg_half8 ld_frag(const _Float16 *p) { return __builtin_bit_cast(qg_half8, *(const uint4 *)p); }
+
+typedef __attribute__((address_space(3))) void qg_lds_void;
+
+// Direct global->shared copy of 16 bytes per lane (gfx950 global_load_lds
+// b128): lane l's 16 bytes land at lds_base + 16*l, lds_base uniform across
+// the wave.  Completion is tracked by the vector-memory counter.
+QG_DEV void dma16(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (qg_lds_void *)lds_base, 16, 0, 0);
+}
+QG_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// 1/sqrt(mean(x^2) + eps) of one row, summed lane-strided then across the
+// wave; every caller runs this same code, so all blocks agree bit for bit.
+QG_DEV float row_rms_scale(const float *xr, int D, float eps, int lane) {
+    float ss = 0.0f;
+    for (int i = lane; i < D; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    ss = qg_sum_lanes<64>(ss);
+    return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+}
+
+// The fp16 hi/lo planes of one token row (Q4_K fragment order) and the hi/lo
+// planes of its 32-group sums, optionally RMS-scaled by sc (written to xn);
+// lane g handles groups g, g+64, ... with 8 float4 loads each.
+QG_DEV void token_planes(const float *xr, int D, bool norm, float sc, int lane, _Float16 *hi, _Float16 *lo,
+                         _Float16 *shi, _Float16 *slo, float *xn) {
+    for (int g = lane; g < D / 32; g += 64) {
+        float v[32];
+        const float4 *src = (const float4 *)(xr + 32 * g);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 f = src[i];
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            if (norm) v[l] = v[l] * sc;
+            s += v[l];
+        }
+        const _Float16 sh = (_Float16)s;
+        shi[g] = sh;
+        slo[g] = (_Float16)(s - (float)sh);
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const int e = 32 * g + l, p = plane_pos(QT_Q4_K, e);
+            const _Float16 h = (_Float16)v[l];
+            hi[p] = h;
+            lo[p] = (_Float16)(v[l] - (float)h);
+            if (norm && xn) xn[e] = v[l];
+        }
+    }
+}

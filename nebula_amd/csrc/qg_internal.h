@@ -20,3 +20,15 @@ int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int
 extern "C" size_t qg_generic_workspace_bytes(int width, int ff, int tokens);
 extern "C" int qg_generic_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x, int nt,
                        const qg_moe_layer *L, void *workspace, size_t ws_bytes);
+
+// Benchmark timing: the events registered by qg_moe_kernel_events for kernel
+// `slot` of this thread's calls, if any.
+bool qg_kernel_event_pair(int slot, void **begin, void **end);
+
+// The prefill path (18..8192 tokens) of qg_moe_forward(_residual).
+bool qg_prefill_ok(const qg_moe_layer *L);
+size_t qg_prefill_workspace_bytes(int width, int ff, int tokens);
+int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
+                       const float *x, float *xn_out, int norm, int nt, const qg_moe_layer *L, void *workspace);
+size_t qg_prefill_dispatch_scratch(int nt);
+int qg_prefill_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int nt, void *scratch);

@@ -66,6 +66,11 @@ QG_DEV void route_token(int *s_ids, float *s_w, const float *s, int t, int lane,
 
 QG_DEV void act_planes_group(const float *x, int K, int r, int g, _Float16 *xh, float *xs);
 
+// logits[t][e] += bias[e] for the 512 expert logits of token blockIdx.x.
+__global__ __launch_bounds__(QG_EXPERTS) void logit_bias_kernel(float *logits, int ld, const float *bias) {
+    logits[(size_t)blockIdx.x * ld + threadIdx.x] += bias[threadIdx.x];
+}
+
 // Inclusive scan of one int per thread over a RD_THREADS-thread block.
 QG_DEV int block_scan(int v, int *s_tmp) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -748,61 +753,6 @@ int launch_experts(const ExpertPhase &P, hipStream_t s) {
     return rc;
 }
 
-// ---------------- general CSR dispatch (any token count) ----------------
-// counts[e] = tokens selecting e, with bit 30 set if some token lists e twice
-// and bit 29 (expert 0's word) set if any id is neither valid nor a pruned
-// encoding (the validation of cpu.c:242-244).
-__global__ __launch_bounds__(64) void csr_count_kernel(int *counts, const int *ids, int nt) {
-    const int e = blockIdx.x, lane = threadIdx.x;
-    int c = 0, dup = 0, bad = 0;
-    for (int t = lane; t < nt; t += 64) {
-        int m = 0;
-        for (int k = 0; k < QG_TOP; k++) {
-            const int id = ids[t * QG_TOP + k];
-            m += id == e;
-            if (e == 0 && (id >= QG_EXPERTS || (id < 0 && !(id <= -2 && id >= -QG_EXPERTS - 1)))) bad = 1;
-        }
-        c += m > 0;
-        dup |= m > 1;
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) { c += __shfl_xor(c, d); dup |= __shfl_xor(dup, d); bad |= __shfl_xor(bad, d); }
-    if (lane == 0) counts[e] = c | (dup << 30) | (bad << 29);
-}
-__global__ __launch_bounds__(QG_EXPERTS) void csr_scan_kernel(int *offsets, int *status, const int *counts) {
-    __shared__ int s_tmp[RD_THREADS / 64];
-    __shared__ int s_bad;
-    const int tid = threadIdx.x;
-    if (tid == 0) s_bad = 0;
-    __syncthreads();
-    const int w = counts[tid];
-    if (w & (3 << 29)) atomicOr(&s_bad, 1);
-    const int c = w & 0x1fffffff;
-    const int incl = block_scan(c, s_tmp);
-    offsets[tid] = incl - c;
-    if (tid == QG_EXPERTS - 1) offsets[QG_EXPERTS] = incl;
-    __syncthreads();
-    if (tid == 0) *status = s_bad;
-}
-__global__ __launch_bounds__(64) void csr_fill_kernel(int *row_token, int *row_slot, const int *offsets, const int *ids, int nt) {
-    const int e = blockIdx.x, lane = threadIdx.x;
-    int carry = offsets[e];
-    for (int base = 0; base < nt; base += 64) {
-        const int t = base + lane;
-        int k_sel = -1;
-        if (t < nt)
-            for (int k = QG_TOP - 1; k >= 0; k--) if (ids[t * QG_TOP + k] == e) k_sel = k;
-        // a token lists one entry per matching rank (duplicates are rejected upstream)
-        const unsigned long long mask = __ballot(k_sel >= 0);
-        if (k_sel >= 0) {
-            const int pos = carry + __popcll(mask & ((1ULL << lane) - 1ULL));
-            row_token[pos] = t;
-            row_slot[pos] = t * QG_TOP + k_sel;
-        }
-        carry += __popcll(mask);
-    }
-}
-
 }  // namespace
 
 extern "C" {
@@ -844,6 +794,10 @@ int qg_generic_forward(float *out, int *ids, float *weights, unsigned char *flag
     int rc = qg_launch_matmul_exact(logits, (const uint8_t *)L->router, QT_F32, rows, D, x, nt,
                                     sh ? (const uint8_t *)L->sh_gate_inp : nullptr, s);
     if (rc) return rc;
+    if (L->router_bias) {
+        logit_bias_kernel<<<nt, QG_EXPERTS, 0, s>>>(logits, rows, L->router_bias);
+        if ((rc = hipGetLastError())) return rc;
+    }
     phase_mark(1, s);
     _Float16 *xh = (_Float16 *)(ws + lay.xh);
     float *xs = (float *)(ws + lay.xs);
@@ -906,17 +860,25 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
     return rc;
 }
 
-// CSR dispatch for any batch (histogram per expert, prefix sum, ordered fill).
+// CSR dispatch for any batch (per-chunk histogram, prefix sums, stable fill).
 int qg_moe_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int nt) {
     if (!offsets || !row_token || !row_slot || !status || !ids || nt < 1 || nt > QG_MAX_TOKENS) return hipErrorInvalidValue;
-    hipStream_t s = qg_stream();
-    // counts live in offsets[0..511] until the scan overwrites them in place
-    static thread_local int *counts = nullptr;
-    if (!counts && hipMalloc((void **)&counts, QG_EXPERTS * sizeof(int)) != hipSuccess) { counts = nullptr; return hipErrorOutOfMemory; }
-    csr_count_kernel<<<QG_EXPERTS, 64, 0, s>>>(counts, ids, nt);
-    csr_scan_kernel<<<1, QG_EXPERTS, 0, s>>>(offsets, status, counts);
-    csr_fill_kernel<<<QG_EXPERTS, 64, 0, s>>>(row_token, row_slot, offsets, ids, nt);
-    return hipGetLastError();
+    // chunk histograms, grown on demand (never inside a capture: the first
+    // call per size must be eager)
+    static thread_local void *scratch = nullptr;
+    static thread_local size_t scratch_bytes = 0;
+    const size_t need = qg_prefill_dispatch_scratch(nt);
+    if (scratch_bytes < need) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (qg_stream() && hipStreamIsCapturing(qg_stream(), &st) == hipSuccess && st != hipStreamCaptureStatusNone)
+            return hipErrorInvalidValue;
+        if (scratch) (void)hipFree(scratch);
+        scratch = nullptr;
+        scratch_bytes = 0;
+        if (hipMalloc(&scratch, need) != hipSuccess) return hipErrorOutOfMemory;
+        scratch_bytes = need;
+    }
+    return qg_prefill_dispatch(offsets, row_token, row_slot, status, ids, nt, scratch);
 }
 
 }  // extern "C"

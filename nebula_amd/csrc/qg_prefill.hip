@@ -1,0 +1,867 @@
+// Routed-MoE layer for prefill batches (18..8192 tokens): the path of
+// qg_moe_forward / qg_moe_forward_residual above the decode sizes, for Q4_K
+// gate/up and Q4_K or IQ4_NL down.  It replaces the per-expert loop of
+// qwen.c:680-700 (qg_moe_map, then qg_matmul x3 and qg_moe_scatter per expert,
+// or qc_moe of cpu.c:235-261 on the CPU handoff) with grouped GEMMs over
+// per-expert row lists built on the device.
+//
+// Kernels per layer:
+//   P1 router   : qg_matmul's exact-order F32 kernel (the summation order of
+//                 cpu.c:122-139), rows 0..511 plus the shared gate vector.
+//   P2 route    : a block = 8 waves = a chunk of 32 tokens, a wave per token:
+//                 router bias, top-10, coverage/prune, flags, the activation
+//                 planes; then the chunk's per-expert token masks, whose
+//                 popcounts are the chunk's histogram counts[chunk][e].
+//   P3 scan     : per-expert totals, CSR offsets, per-chunk bases (exclusive
+//                 prefix over chunks), and the table of 64-row tiles per group.
+//   P4 fill     : the stable permutation: a selection's row is its chunk's base
+//                 plus the rank of its token in the chunk's mask, so each
+//                 expert's rows are in ascending token order (the order of
+//                 moe_map_kernel, gpu.cu:489-500).
+//   P5 gate/up  : persistent grouped GEMM; item = (group, 64-row tile, 128 F
+//                 rows); SwiGLU; mid rows as fp16 hi/lo planes.
+//   P6 down     : persistent grouped GEMM; item = (group, 64-row tile, 256 D
+//                 rows); y rows written to the selection's slot.
+//   P7 combine  : out[t] = sum over ranks k of w[t,k]*y[t,k] in rank order,
+//                 + sigmoid-gated shared expert, + optional residual.
+// Groups are the 512 experts plus the shared expert (group 512, every token).
+//
+// GEMM tiles (operand conventions of qg_frag.h): a workgroup is 4 waves; the
+// tile's activation rows (64 rows x 2 planes x 256 K, 64 KB) are staged in
+// shared memory by direct global->shared copies, double-buffered over K; each
+// wave owns 4 columns tiles of 16 weight rows whose quantised bytes it loads
+// into registers one K chunk ahead.  A 16x16x32 MFMA pair (hi and lo plane)
+// per (row tile, column tile, K step); row tiles past the group's last row are
+// skipped.  Rows in shared memory are 512 B; 16-byte chunk c of row r is
+// stored at chunk c ^ (r & 15), so the 16 rows one MFMA reads hit 16
+// different bank groups.
+#include "qg_internal.h"
+#include "qg_frag.h"
+#include <hip/hip_ext.h>
+
+namespace {
+
+constexpr int PF_MIN = QG_MAX_DECODE + 1;   // smallest batch on this path
+constexpr int PF_CHUNK = 32;                 // tokens per routing chunk (one 32-bit mask per expert)
+constexpr int PT = 64;                       // rows per GEMM tile
+constexpr int KC = 256;                      // K elements per staged chunk
+constexpr int GU_FB = 128;                   // F rows per gate/up item (32 per wave)
+constexpr int DN_DB = 256;                   // D rows per down item (64 per wave)
+constexpr int NG = QG_EXPERTS + 1;           // groups: experts + shared expert
+constexpr int DENSE_MIN = 256;               // rows from which an expert runs in the dense pass
+constexpr int STAGE_BYTES = PT * 2 * KC * 2; // [64 rows][2 planes][256] fp16
+constexpr int SUMS_BYTES = PT * 2 * 16;      // [64 rows][2 planes][8 group sums] fp16
+constexpr int PF_LDS = 2 * (STAGE_BYTES + SUMS_BYTES);
+
+// Groups in pass order (dense experts, the other experts, the shared expert);
+// tiles bounds[s] .. bounds[s+1]-1 form segment s (0 dense, 1 sparse, 2 shared);
+// order position p holds group gorder[p], whose tiles start at tbase[p].
+struct TileTable { int bounds[4]; int tbase[NG + 1]; int gorder[NG]; };
+
+struct PfLayout {
+    size_t logits, flag, missing, mass, xp, xsp, counts, offsets, tbase, row_token, row_slot, midp, msp, slots, xn, total;
+};
+PfLayout pf_layout(int D, int F, int nt) {
+    PfLayout L;
+    size_t off = 0;
+    auto take = [&](size_t n) { size_t o = off; off += (n + 255) & ~(size_t)255; return o; };
+    const size_t nch = (nt + PF_CHUNK - 1) / PF_CHUNK, rows = (size_t)nt * (QG_TOP + 1);
+    L.logits = take((size_t)nt * (QG_EXPERTS + 1) * 4);
+    L.flag = take((size_t)nt * 4);
+    L.missing = take((size_t)nt * 4);
+    L.mass = take((size_t)nt * 8);
+    L.xp = take((size_t)nt * 2 * D * 2);
+    L.xsp = take((size_t)nt * 2 * (D / 32) * 2);
+    L.counts = take(nch * QG_EXPERTS * 4);
+    L.offsets = take((QG_EXPERTS + 1) * 4);
+    L.tbase = take(sizeof(TileTable));
+    L.row_token = take((size_t)nt * QG_TOP * 4);
+    L.row_slot = take((size_t)nt * QG_TOP * 4);
+    L.midp = take(rows * 2 * F * 2);
+    L.msp = take(rows * 2 * (F / 32) * 2);
+    L.slots = take(rows * D * 4);
+    L.xn = take((size_t)nt * D * 4);
+    L.total = off;
+    return L;
+}
+
+int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            return 256;
+    }
+    return n;
+}
+
+template <typename K, typename... Args>
+void pf_launch(int slot, K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+    hipEvent_t b = nullptr, e = nullptr;
+    if (qg_kernel_event_pair(slot, (void **)&b, (void **)&e))
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, b, e, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
+
+QG_DEV void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---------------- input normalisation (residual form) ----------------
+// xn = x / sqrt(mean(x^2) + eps), one wave per row, with the decode path's
+// row_rms_scale so both paths normalise bit-identically.
+__global__ __launch_bounds__(256) void pf_norm_kernel(float *xn, const float *x, int nt, int D, float eps) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + wave;
+    if (t >= nt) return;
+    const float *xr = x + (size_t)t * D;
+    const float sc = row_rms_scale(xr, D, eps, lane);
+    for (int i = lane; i < D; i += 64) xn[(size_t)t * D + i] = xr[i] * sc;
+}
+
+// ---------------- P2: routing, planes, chunk histogram ----------------
+struct RouteArgs {
+    int nt; const float *logits; int ld; const float *bias;
+    const uint8_t *resident; double thr;
+    int *ids; float *w; uint8_t *flags_out; int *flag; int *missing; double *mass;
+    const float *x; int D; _Float16 *xp, *xsp;
+    int *counts;                     // [chunk][512]
+};
+
+__global__ __launch_bounds__(512) void pf_route_kernel(RouteArgs A) {
+    __shared__ float s_row[8][QG_EXPERTS];
+    __shared__ float s_rv[8][64];
+    __shared__ int s_ri[8][64];
+    __shared__ uint32_t s_mask[QG_EXPERTS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t0 = blockIdx.x * PF_CHUNK;
+    s_mask[tid] = 0u;  // 512 threads, one per expert
+    __syncthreads();
+    for (int i = 0; i < PF_CHUNK / 8; i++) {
+        const int tl = wave * (PF_CHUNK / 8) + i, t = t0 + tl;
+        if (t >= A.nt) break;  // wave-uniform
+        const float *lr = A.logits + (size_t)t * A.ld;
+        for (int e = lane; e < QG_EXPERTS; e += 64) s_row[wave][e] = A.bias ? lr[e] + A.bias[e] : lr[e];
+        wave_sync_lds();
+        int id, missing;
+        float wv;
+        double mass;
+        qg_route_fast(s_row[wave], lane, id, wv, s_rv[wave], s_ri[wave]);
+        const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+        if (lane < QG_TOP) {
+            A.ids[(size_t)t * QG_TOP + lane] = id;
+            A.w[(size_t)t * QG_TOP + lane] = wv;
+            if (flag < 2 && id >= 0 && id < QG_EXPERTS) atomicOr(&s_mask[id], 1u << tl);
+        }
+        if (lane == 0) {
+            A.flag[t] = flag;
+            A.missing[t] = missing;
+            A.mass[t] = mass;
+            if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
+        }
+        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
+        token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
+        wave_sync_lds();  // s_row / s_rv / s_ri are rewritten for the wave's next token
+    }
+    __syncthreads();
+    A.counts[(size_t)blockIdx.x * QG_EXPERTS + tid] = __popc(s_mask[tid]);
+}
+
+// ---------------- P3: offsets, chunk bases, tile table ----------------
+// Inclusive scan of one int per thread over a 512-thread block.
+QG_DEV int scan512(int v, int *s_tmp) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    if (lane == 63) s_tmp[wave] = v;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; w++) base += s_tmp[w];
+    __syncthreads();
+    return v + base;
+}
+
+// tt may be null (dispatch only); with `status`, *status = OR of bad[0..nch).
+__global__ __launch_bounds__(512) void pf_scan_kernel(int *counts, int nch, int *offsets, TileTable *tt, int shared_rows,
+                                                      const int *bad, int *status) {
+    __shared__ int s_tmp[8];
+    __shared__ int s_tiles[NG];
+    __shared__ int s_nd;
+    const int e = threadIdx.x;
+    if (status) {
+        int b = 0;
+        for (int c = e; c < nch; c += QG_EXPERTS) b |= bad[c];
+        b = __syncthreads_or(b);
+        if (e == 0) *status = b ? 1 : 0;
+    }
+    constexpr int U = 16;  // loads in flight per thread
+    int n = 0;
+    for (int c0 = 0; c0 < nch; c0 += U) {
+        int v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = c0 + u < nch ? counts[(size_t)(c0 + u) * QG_EXPERTS + e] : 0;
+#pragma unroll
+        for (int u = 0; u < U; u++) n += v[u];
+    }
+    const int incl = scan512(n, s_tmp), off = incl - n;
+    offsets[e] = off;
+    if (e == QG_EXPERTS - 1) offsets[QG_EXPERTS] = incl;
+    // counts[c][e] -> first CSR position of chunk c's rows of expert e
+    int run = off;
+    for (int c0 = 0; c0 < nch; c0 += U) {
+        int v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = c0 + u < nch ? counts[(size_t)(c0 + u) * QG_EXPERTS + e] : 0;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (c0 + u < nch) counts[(size_t)(c0 + u) * QG_EXPERTS + e] = run;
+            run += v[u];
+        }
+    }
+    if (!tt) return;  // block-uniform
+    // pass order: dense experts, then the others (each in expert order), then shared
+    const int dense = n >= DENSE_MIN;
+    const int dincl = scan512(dense, s_tmp);
+    if (e == QG_EXPERTS - 1) s_nd = dincl;
+    __syncthreads();
+    const int nd = s_nd, pos = dense ? dincl - 1 : nd + e - (dincl - dense);
+    s_tiles[pos] = (n + PT - 1) / PT;
+    tt->gorder[pos] = e;
+    if (e == 0) {
+        s_tiles[QG_EXPERTS] = (shared_rows + PT - 1) / PT;
+        tt->gorder[QG_EXPERTS] = QG_EXPERTS;
+    }
+    __syncthreads();
+    const int v = s_tiles[e], tincl = scan512(v, s_tmp);
+    tt->tbase[e] = tincl - v;
+    if (e == nd) tt->bounds[1] = tincl - v;
+    if (e == QG_EXPERTS - 1) {
+        const int all = tincl + s_tiles[QG_EXPERTS];
+        tt->tbase[QG_EXPERTS] = tincl;
+        tt->tbase[NG] = all;
+        tt->bounds[0] = 0;
+        if (nd == QG_EXPERTS) tt->bounds[1] = tincl;
+        tt->bounds[2] = tincl;
+        tt->bounds[3] = all;
+    }
+}
+
+// Histogram of an ids array alone (qg_moe_dispatch): chunk masks as in
+// pf_route_kernel; bad[chunk] = 1 if an id is neither in [0,512) nor a pruned
+// encoding in [-513,-2], or a token lists an expert twice (the validation of
+// cpu.c:242-244).
+__global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, const int *ids, int nt) {
+    __shared__ uint32_t s_mask[QG_EXPERTS];
+    __shared__ int s_bad;
+    const int tid = threadIdx.x, t0 = blockIdx.x * PF_CHUNK;
+    s_mask[tid] = 0u;
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    if (tid < PF_CHUNK * QG_TOP) {
+        const int tl = tid / QG_TOP, t = t0 + tl;
+        if (t < nt) {
+            const int id = ids[(size_t)t * QG_TOP + tid - tl * QG_TOP];
+            if (id >= 0 && id < QG_EXPERTS) {
+                if (atomicOr(&s_mask[id], 1u << tl) & (1u << tl)) s_bad = 1;
+            } else if (!(id <= -2 && id >= -QG_EXPERTS - 1)) {
+                s_bad = 1;
+            }
+        }
+    }
+    __syncthreads();
+    counts[(size_t)blockIdx.x * QG_EXPERTS + tid] = __popc(s_mask[tid]);
+    if (tid == 0) bad[blockIdx.x] = s_bad;
+}
+
+// ---------------- P4: stable fill ----------------
+__global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_slot, const int *bases, const int *ids,
+                                                      const int *flag, int nt) {
+    __shared__ uint32_t s_mask[QG_EXPERTS];
+    const int tid = threadIdx.x, t0 = blockIdx.x * PF_CHUNK;
+    s_mask[tid] = 0u;
+    __syncthreads();
+    int e = -1, tl = 0, k = 0;
+    if (tid < PF_CHUNK * QG_TOP) {
+        tl = tid / QG_TOP;
+        k = tid - tl * QG_TOP;
+        const int t = t0 + tl;
+        if (t < nt) {
+            const int id = ids[(size_t)t * QG_TOP + k];
+            if ((!flag || flag[t] < 2) && id >= 0 && id < QG_EXPERTS) {
+                e = id;
+                atomicOr(&s_mask[e], 1u << tl);
+            }
+        }
+    }
+    __syncthreads();
+    if (e >= 0) {
+        const int pos = bases[(size_t)blockIdx.x * QG_EXPERTS + e] + __popc(s_mask[e] & ((1u << tl) - 1u));
+        row_token[pos] = t0 + tl;
+        row_slot[pos] = (t0 + tl) * QG_TOP + k;
+    }
+}
+
+// ---------------- GEMM building blocks ----------------
+
+// Stage K chunk `chunk` of the tile's 64 rows: plane rows of `planes`
+// (row stride `stride` elements per plane, 2 planes per source row; source row
+// of tile row r = src[r]) into `stage`, swizzled; nck = 16-byte chunks per
+// plane row in this K chunk.  With `sums`, the 2 x 8 group sums of the chunk
+// ([tile row][plane][8]).
+QG_DEV void stage_rows(uint8_t *stage, uint8_t *sums, const _Float16 *planes, int stride, const _Float16 *sum_planes,
+                       int sum_stride, const int *src, int chunk, int nck, int wave, int lane) {
+    for (int q = wave; q < PT; q += 4) {
+        const int R = 2 * q + (lane >> 5), tr = R >> 1, p = R & 1;
+        int c = (lane & 31) ^ (tr & 15);
+        if (c >= nck) c = 0;  // positions no reader uses
+        dma16(planes + ((size_t)src[tr] * 2 + p) * stride + (size_t)chunk * KC + c * 8, stage + q * 1024);
+    }
+    if (sums && wave < 2) {
+        const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
+        dma16(sum_planes + ((size_t)src[tr] * 2 + p) * sum_stride + (size_t)chunk * 8, sums + wave * 1024);
+    }
+}
+
+// A fragment of tile row r (within the stage), plane p, 16-byte chunk c.
+QG_DEV qg_half8 stage_frag(const uint8_t *st, int r, int p, int c) {
+    return ld_frag((const _Float16 *)(st + (r * 2 + p) * 512 + 16 * (c ^ (r & 15))));
+}
+
+// Q4_K operands of one superblock for the wave's 4 column tiles.
+struct Q4Ops { uint4 hd[4], c0[4], c1[4]; };
+QG_DEV void q4_load(Q4Ops &o, const uint8_t *const *wrow, int sb, int kq) {
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const uint8_t *p = wrow[n] + (size_t)sb * 144;
+        o.hd[n] = qg_ld16(p);
+        o.c0[n] = qg_ld16(p + 16 + 16 * kq);
+        o.c1[n] = qg_ld16(p + 16 + 16 * (kq + 4));
+    }
+}
+
+// y[m][n] += d * (s*q . x) - dmin * (m . X) over one Q4_K superblock, for the
+// first M row tiles.
+template <int M>
+QG_DEV void q4_chunk(qg_f4 (&y)[4][4], const Q4Ops &o, const uint8_t *st, const uint8_t *ss, int j, int kq) {
+    Q4kHeader h[4];
+#pragma unroll
+    for (int n = 0; n < 4; n++) h[n] = q4k_header(o.hd[n]);
+    qg_f4 acc[M][4];
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int n = 0; n < 4; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int gA = 2 * (kq >> 1);
+#pragma unroll
+    for (int f = 0; f < 8; f++) {
+        qg_half8 a[M][2];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            a[m][0] = stage_frag(st, m * 16 + j, 0, 4 * f + kq);
+            a[m][1] = stage_frag(st, m * 16 + j, 1, 4 * f + kq);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const uint4 c = f < 4 ? o.c0[n] : o.c1[n];
+            const int g = (f < 4 ? gA : gA + 4) + ((f & 3) >> 1);
+            const qg_half8 b = q4k_chunk_frag(c, f & 3, (_Float16)q4k_s(h[n], g));
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], b, acc[m][n], 0, 0, 0);
+                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][1], b, acc[m][n], 0, 0, 0);
+            }
+        }
+    }
+    // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
+    qg_half8 as[M];
+    const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < M; m++) as[m] = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        qg_half8 bm;
+#pragma unroll
+        for (int g = 0; g < 8; g++) bm[g] = kq < 2 ? (_Float16)q4k_m(h[n], g) : (_Float16)0.0f;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as[m], bm, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                y[m][n][i] = __builtin_fmaf(h[n].d, acc[m][n][i], __builtin_fmaf(-h[n].dmin, mm[i], y[m][n][i]));
+        }
+    }
+}
+
+// IQ4_NL operands of one K chunk (up to 8 blocks) for the wave's 4 column tiles.
+struct IqOps { uint32_t q[4][8], d[4][8]; };
+QG_DEV void iq_load(IqOps &o, const uint8_t *const *wrow, int kc, int nb, int kq) {
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+            if (b < nb) {
+                const uint16_t *p16 = (const uint16_t *)(wrow[n] + (size_t)(kc * 8 + b) * 18);  // 2-byte aligned
+                o.d[n][b] = p16[0];
+                o.q[n][b] = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
+            }
+}
+
+// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk.
+template <int M>
+QG_DEV void iq_chunk(qg_f4 (&y)[4][4], const IqOps &o, const uint8_t *st, int j, int kq, int nb) {
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        if (b >= nb) break;  // uniform
+        qg_half8 a[M][2];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            a[m][0] = stage_frag(st, m * 16 + j, 0, 4 * b + kq);
+            a[m][1] = stage_frag(st, m * 16 + j, 1, 4 * b + kq);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const qg_half8 bf = iq4_frag4(o.q[n][b]);
+            const float d = qg_half_u16(o.d[n][b]);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], bf, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][1], bf, acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d, acc[i], y[m][n][i]);
+            }
+        }
+    }
+}
+
+// Tile -> order position (block-uniform): the largest p with tb[p] <= tile_idx
+// (empty groups share their successor's start).
+QG_DEV int find_group(const int *tb, int tile_idx) {
+    int lo = 0, hi = NG;  // tb[0] = 0 <= tile_idx < tb[NG]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (tb[mid] <= tile_idx) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// ---------------- P5: gate/up + SwiGLU ----------------
+struct GuArgs {
+    int nt, D, F;
+    const int *offsets; const TileTable *tt; int seg_lo, seg_hi;   // tiles of segments seg_lo .. seg_hi-1
+    const int *row_token;
+    const uint8_t *gate, *up, *sh_gate, *sh_up; size_t rb;   // Q4_K rows of D
+    const _Float16 *xp, *xsp;
+    _Float16 *midp, *msp;            // [rows][2][F] (down format order), [rows][2][F/32]
+    int down_fmt, sh_down_fmt;
+};
+
+__global__ __launch_bounds__(256, 1) void pf_gateup_kernel(GuArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    uint8_t *lds = (uint8_t *)s_dyn;
+    __shared__ int s_tb[NG + 1], s_go[NG];
+    __shared__ int s_src[PT], s_mrow[PT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    for (int i = tid; i <= NG; i += 256) {
+        s_tb[i] = A.tt->tbase[i];
+        if (i < NG) s_go[i] = A.tt->gorder[i];
+    }
+    __syncthreads();
+    const int nfb = A.F / GU_FB, NSB = A.D / 256, D32 = A.D / 32, F = A.F;
+    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        const int tile_idx = t_lo + item / nfb, fb = item % nfb;
+        const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
+        const bool shared = g == QG_EXPERTS;
+        const int n_g = shared ? A.nt : A.offsets[g + 1] - A.offsets[g];
+        const int r0 = tile * PT, nv = min(PT, n_g - r0), M = (nv + 15) >> 4;
+        if (tid < PT) {
+            const int r = r0 + min(tid, nv - 1);
+            s_src[tid] = shared ? r : A.row_token[A.offsets[g] + r];
+            s_mrow[tid] = shared ? A.nt * QG_TOP + r : A.offsets[g] + r;
+        }
+        __syncthreads();
+        const int f0 = fb * GU_FB + wave * 32;
+        const uint8_t *bg = shared ? A.sh_gate : A.gate + (size_t)g * F * A.rb;
+        const uint8_t *bu = shared ? A.sh_up : A.up + (size_t)g * F * A.rb;
+        const uint8_t *wrow[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) wrow[n] = (n < 2 ? bg : bu) + (size_t)(f0 + 16 * (n & 1) + j) * A.rb;
+        stage_rows(lds, lds + 2 * STAGE_BYTES, A.xp, A.D, A.xsp, D32, s_src, 0, 32, wave, lane);
+        Q4Ops cur, nxt;
+        q4_load(cur, wrow, 0, kq);
+        qg_f4 y[4][4];
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+#pragma unroll
+            for (int n = 0; n < 4; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sb = 0; sb < NSB; sb++) {
+            wait_vmem();
+            __syncthreads();
+            if (sb + 1 < NSB) {
+                const int b = (sb + 1) & 1;
+                stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src, sb + 1, 32,
+                           wave, lane);
+                q4_load(nxt, wrow, sb + 1, kq);
+            }
+            const uint8_t *st = lds + (sb & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (sb & 1) * SUMS_BYTES;
+            switch (M) {
+            case 1: q4_chunk<1>(y, cur, st, ss, j, kq); break;
+            case 2: q4_chunk<2>(y, cur, st, ss, j, kq); break;
+            case 3: q4_chunk<3>(y, cur, st, ss, j, kq); break;
+            default: q4_chunk<4>(y, cur, st, ss, j, kq); break;
+            }
+            cur = nxt;
+        }
+        // SwiGLU: column tiles 0/1 are gate rows f0+j / f0+16+j, tiles 2/3 the same up rows
+        const int fmt = shared ? A.sh_down_fmt : A.down_fmt;
+        const int pa = plane_pos(fmt, f0 + j), pb = plane_pos(fmt, f0 + 16 + j);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m >= M) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tr = m * 16 + 4 * kq + i;
+                const float ma = qg_swiglu(y[m][0][i], y[m][2][i]), mb = qg_swiglu(y[m][1][i], y[m][3][i]);
+                const bool ok = tr < nv;
+                const size_t mrow = (size_t)s_mrow[ok ? tr : 0];
+                if (ok) {
+                    _Float16 *hp = A.midp + mrow * 2 * F;
+                    const _Float16 ha = (_Float16)ma, hb = (_Float16)mb;
+                    hp[pa] = ha;
+                    hp[F + pa] = (_Float16)(ma - (float)ha);
+                    hp[pb] = hb;
+                    hp[F + pb] = (_Float16)(mb - (float)hb);
+                }
+                if (fmt == QT_Q4_K) {
+                    // the 32-group sum of these F rows (lanes of one kq hold all 16 j)
+                    float s = ma + mb;
+                    s += __shfl_xor(s, 1);
+                    s += __shfl_xor(s, 2);
+                    s += __shfl_xor(s, 4);
+                    s += __shfl_xor(s, 8);
+                    if (ok && j == 0) {
+                        _Float16 *sp = A.msp + mrow * 2 * (F / 32) + f0 / 32;
+                        const _Float16 hs = (_Float16)s;
+                        sp[0] = hs;
+                        sp[F / 32] = (_Float16)(s - (float)hs);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // s_src / s_mrow and the stage buffers are rewritten by the next item
+    }
+}
+
+// ---------------- P6: down ----------------
+struct DnArgs {
+    int nt, D, F;
+    const int *offsets; const TileTable *tt; int seg_lo, seg_hi;   // tiles of segments seg_lo .. seg_hi-1
+    const int *row_slot;
+    const uint8_t *down, *sh_down; size_t rb, sh_rb;   // every group in the launch has format FMT
+    const _Float16 *midp, *msp;
+    float *slots;                    // [rows][D]: slot t*10+k, shared rows at nt*10+t
+};
+
+template <int FMT>
+__global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    uint8_t *lds = (uint8_t *)s_dyn;
+    __shared__ int s_tb[NG + 1], s_go[NG];
+    __shared__ int s_src[PT], s_slot[PT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    for (int i = tid; i <= NG; i += 256) {
+        s_tb[i] = A.tt->tbase[i];
+        if (i < NG) s_go[i] = A.tt->gorder[i];
+    }
+    __syncthreads();
+    const int ndb = A.D / DN_DB, F = A.F, F32 = A.F / 32, nkc = (F + KC - 1) / KC;
+    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        const int tile_idx = t_lo + item / ndb, db = item % ndb;
+        const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
+        const bool shared = g == QG_EXPERTS;
+        const int n_g = shared ? A.nt : A.offsets[g + 1] - A.offsets[g];
+        const int r0 = tile * PT, nv = min(PT, n_g - r0), M = (nv + 15) >> 4;
+        if (tid < PT) {
+            const int r = r0 + min(tid, nv - 1);
+            s_src[tid] = shared ? A.nt * QG_TOP + r : A.offsets[g] + r;
+            s_slot[tid] = shared ? A.nt * QG_TOP + r : A.row_slot[A.offsets[g] + r];
+        }
+        __syncthreads();
+        const int d0 = db * DN_DB + wave * 64;
+        const uint8_t *bw = shared ? A.sh_down : A.down + (size_t)g * A.D * A.rb;
+        const size_t rb = shared ? A.sh_rb : A.rb;
+        const uint8_t *wrow[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) wrow[n] = bw + (size_t)(d0 + 16 * n + j) * rb;
+        qg_f4 y[4][4];
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+#pragma unroll
+            for (int n = 0; n < 4; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (FMT == QT_Q4_K) {
+            stage_rows(lds, lds + 2 * STAGE_BYTES, A.midp, F, A.msp, F32, s_src, 0, 32, wave, lane);
+            Q4Ops cur, nxt;
+            q4_load(cur, wrow, 0, kq);
+            for (int kc = 0; kc < nkc; kc++) {
+                wait_vmem();
+                __syncthreads();
+                if (kc + 1 < nkc) {
+                    const int b = (kc + 1) & 1;
+                    stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src, kc + 1,
+                               32, wave, lane);
+                    q4_load(nxt, wrow, kc + 1, kq);
+                }
+                const uint8_t *st = lds + (kc & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (kc & 1) * SUMS_BYTES;
+                switch (M) {
+                case 1: q4_chunk<1>(y, cur, st, ss, j, kq); break;
+                case 2: q4_chunk<2>(y, cur, st, ss, j, kq); break;
+                case 3: q4_chunk<3>(y, cur, st, ss, j, kq); break;
+                default: q4_chunk<4>(y, cur, st, ss, j, kq); break;
+                }
+                cur = nxt;
+            }
+        } else {
+            auto nblocks = [&](int kc) { return min(8, (F - kc * KC) / 32); };
+            stage_rows(lds, nullptr, A.midp, F, nullptr, 0, s_src, 0, 4 * nblocks(0), wave, lane);
+            IqOps cur, nxt;
+            iq_load(cur, wrow, 0, nblocks(0), kq);
+            for (int kc = 0; kc < nkc; kc++) {
+                wait_vmem();
+                __syncthreads();
+                if (kc + 1 < nkc) {
+                    stage_rows(lds + ((kc + 1) & 1) * STAGE_BYTES, nullptr, A.midp, F, nullptr, 0, s_src, kc + 1, 4 * nblocks(kc + 1),
+                               wave, lane);
+                    iq_load(nxt, wrow, kc + 1, nblocks(kc + 1), kq);
+                }
+                const uint8_t *st = lds + (kc & 1) * STAGE_BYTES;
+                const int nb = nblocks(kc);
+                switch (M) {
+                case 1: iq_chunk<1>(y, cur, st, j, kq, nb); break;
+                case 2: iq_chunk<2>(y, cur, st, j, kq, nb); break;
+                case 3: iq_chunk<3>(y, cur, st, j, kq, nb); break;
+                default: iq_chunk<4>(y, cur, st, j, kq, nb); break;
+                }
+                cur = nxt;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m >= M) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tr = m * 16 + 4 * kq + i;
+                if (tr < nv) {
+                    float *o = A.slots + (size_t)s_slot[tr] * A.D + d0 + j;
+#pragma unroll
+                    for (int n = 0; n < 4; n++) o[16 * n] = y[m][n][i];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------- P7: combine ----------------
+struct CombArgs {
+    int nt, D;
+    const int *ids; const float *w; const int *flag;
+    const float *slots;
+    const float *sh_logit; int ld;   // shared gate logit of token t at sh_logit[t*ld], or null
+    float *out, *resid;
+};
+
+// out[t] = sum_k (w[t,k] * y[t,k]) in rank order (each product rounded, as
+// the slot products of cpu.c:253-259), then + y_sh * sigmoid(logit)
+// (gpu.cu:552-553); flag >= 2 rows are 0.
+__global__ __launch_bounds__(256) void pf_combine_kernel(CombArgs A) {
+    const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d >= A.D) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (A.flag[t] < 2) {
+#pragma unroll
+        for (int k = 0; k < QG_TOP; k++) {
+            const int e = A.ids[(size_t)t * QG_TOP + k];
+            if (e < 0 || e >= QG_EXPERTS) continue;
+            const float wk = A.w[(size_t)t * QG_TOP + k];
+            const float4 v = *(const float4 *)(A.slots + ((size_t)t * QG_TOP + k) * A.D + d);
+            acc.x += __fmul_rn(v.x, wk);
+            acc.y += __fmul_rn(v.y, wk);
+            acc.z += __fmul_rn(v.z, wk);
+            acc.w += __fmul_rn(v.w, wk);
+        }
+        if (A.sh_logit) {
+            const float sg = qg_sig(A.sh_logit[(size_t)t * A.ld]);
+            const float4 v = *(const float4 *)(A.slots + ((size_t)A.nt * QG_TOP + t) * A.D + d);
+            acc.x = __builtin_fmaf(v.x, sg, acc.x);
+            acc.y = __builtin_fmaf(v.y, sg, acc.y);
+            acc.z = __builtin_fmaf(v.z, sg, acc.z);
+            acc.w = __builtin_fmaf(v.w, sg, acc.w);
+        }
+    }
+    const size_t o = (size_t)t * A.D + d;
+    if (A.out) *(float4 *)(A.out + o) = acc;
+    if (A.resid) {
+        float4 h = *(float4 *)(A.resid + o);
+        h.x += acc.x; h.y += acc.y; h.z += acc.z; h.w += acc.w;
+        *(float4 *)(A.resid + o) = h;
+    }
+}
+
+// Pruning counters (gpu.cu:484-487 semantics) over the batch, in a fixed
+// reduction order, added to *stats by one block.
+__global__ __launch_bounds__(1024) void pf_stats_kernel(qg_prune_stats *stats, const int *flag, const int *missing,
+                                                        const double *mass, int nt) {
+    __shared__ unsigned long long s_c[4][1024];
+    __shared__ double s_m[1024];
+    const int tid = threadIdx.x;
+    unsigned long long tl = 0, ms = 0, sk = 0, av = 0;
+    double sm = 0.0;
+    for (int t = tid; t < nt; t += 1024) {
+        const int f = flag[t];
+        if (f == 3) continue;
+        tl += 1;
+        ms += (unsigned long long)missing[t];
+        if (f == 1) { sk += (unsigned long long)missing[t]; av += 1; sm += mass[t]; }
+    }
+    s_c[0][tid] = tl; s_c[1][tid] = ms; s_c[2][tid] = sk; s_c[3][tid] = av;
+    s_m[tid] = sm;
+    __syncthreads();
+    for (int h = 512; h > 0; h >>= 1) {
+        if (tid < h) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) s_c[c][tid] += s_c[c][tid + h];
+            s_m[tid] += s_m[tid + h];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        stats->token_layers += s_c[0][0];
+        stats->missing_selections += s_c[1][0];
+        stats->skipped_selections += s_c[2][0];
+        stats->avoided_token_handoffs += s_c[3][0];
+        stats->skipped_mass += s_m[0];
+    }
+}
+
+}  // namespace
+
+bool qg_prefill_ok(const qg_moe_layer *L) {
+    const int D = L->width, F = L->ff;
+    if (D % DN_DB || F % GU_FB) return false;
+    auto down_ok = [&](int t) { return t == QT_IQ4_NL || (t == QT_Q4_K && F % 256 == 0); };
+    if (L->gate_type != QT_Q4_K || L->up_type != QT_Q4_K || !down_ok(L->down_type)) return false;
+    if (L->sh_gate && (L->sh_gate_type != QT_Q4_K || L->sh_up_type != QT_Q4_K || !down_ok(L->sh_down_type))) return false;
+    return true;
+}
+
+size_t qg_prefill_workspace_bytes(int width, int ff, int tokens) {
+    if (width < 256 || width % DN_DB || width > 8192 || ff < GU_FB || ff % GU_FB || ff > 4096 || tokens < PF_MIN ||
+        tokens > QG_MAX_TOKENS)
+        return 0;
+    return pf_layout(width, ff, tokens).total;
+}
+
+int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
+                       const float *x, float *xn_out, int norm, int nt, const qg_moe_layer *L, void *workspace) {
+    if (nt < PF_MIN || nt > QG_MAX_TOKENS || !qg_prefill_ok(L)) return hipErrorInvalidValue;
+    const int D = L->width, F = L->ff;
+    const PfLayout lay = pf_layout(D, F, nt);
+    uint8_t *ws = (uint8_t *)workspace;
+    hipStream_t s = qg_stream();
+    const bool sh = L->sh_gate != nullptr;
+    const int rows = QG_EXPERTS + (sh ? 1 : 0), nch = (nt + PF_CHUNK - 1) / PF_CHUNK;
+    float *logits = (float *)(ws + lay.logits);
+    int *flag = (int *)(ws + lay.flag), *counts = (int *)(ws + lay.counts), *offsets = (int *)(ws + lay.offsets);
+    TileTable *tt = (TileTable *)(ws + lay.tbase);
+    int *row_token = (int *)(ws + lay.row_token), *row_slot = (int *)(ws + lay.row_slot);
+    _Float16 *xp = (_Float16 *)(ws + lay.xp), *xsp = (_Float16 *)(ws + lay.xsp);
+    _Float16 *midp = (_Float16 *)(ws + lay.midp), *msp = (_Float16 *)(ws + lay.msp);
+    float *slots = (float *)(ws + lay.slots);
+    int rc;
+    if (norm) {
+        float *xn = xn_out ? xn_out : (float *)(ws + lay.xn);
+        pf_norm_kernel<<<(nt + 3) / 4, 256, 0, s>>>(xn, x, nt, D, 1e-6f);
+        if ((rc = hipGetLastError())) return rc;
+        x = xn;
+    }
+    // P1: router logits in the reference's order (+ shared gate row)
+    {
+        hipEvent_t b = nullptr, e = nullptr;
+        const bool timed = qg_kernel_event_pair(0, (void **)&b, (void **)&e);
+        if (timed && (rc = hipEventRecord(b, s))) return rc;
+        rc = qg_launch_matmul_exact(logits, (const uint8_t *)L->router, QT_F32, rows, D, x, nt,
+                                    sh ? (const uint8_t *)L->sh_gate_inp : nullptr, s);
+        if (rc) return rc;
+        if (timed && (rc = hipEventRecord(e, s))) return rc;
+    }
+    RouteArgs RA{nt, logits, rows, L->router_bias, L->resident, L->threshold, ids, weights, flags, flag,
+                 (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp, counts};
+    pf_launch(1, pf_route_kernel, dim3(nch), dim3(512), 0, s, RA);
+    if ((rc = hipGetLastError())) return rc;
+    pf_launch(2, pf_scan_kernel, dim3(1), dim3(512), 0, s, counts, nch, offsets, tt, sh ? nt : 0, (const int *)nullptr,
+              (int *)nullptr);
+    if ((rc = hipGetLastError())) return rc;
+    pf_launch(3, pf_fill_kernel, dim3(nch), dim3(512), 0, s, row_token, row_slot, (const int *)counts, (const int *)ids,
+              (const int *)flag, nt);
+    if ((rc = hipGetLastError())) return rc;
+    // grouped GEMMs: the dense pass (experts with >= 256 rows), then the rest
+    const int grid = cu_count();
+    for (int pass = 0; pass < 2; pass++) {
+        GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
+                 sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
+                 xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type};
+        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(256), PF_LDS, s, G);
+        if ((rc = hipGetLastError())) return rc;
+    }
+    auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
+        DnArgs DA{nt, D, F, offsets, tt, seg_lo, seg_hi, row_slot, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr,
+                  qg_row_bytes_host(L->down_type, F), sh ? qg_row_bytes_host(L->sh_down_type, F) : 0, midp, msp, slots};
+        if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel<QT_Q4_K>, dim3(grid), dim3(256), PF_LDS, s, DA);
+        else pf_launch(slot, pf_down_kernel<QT_IQ4_NL>, dim3(grid), dim3(256), PF_LDS, s, DA);
+        return hipGetLastError();
+    };
+    if ((rc = down(0, 1, L->down_type, 6))) return rc;
+    if (!sh || L->sh_down_type == L->down_type) {
+        if ((rc = down(1, 3, L->down_type, 7))) return rc;
+    } else {
+        if ((rc = down(1, 2, L->down_type, 7))) return rc;
+        if ((rc = down(2, 3, L->sh_down_type, 8))) return rc;
+    }
+    CombArgs CA{nt, D, ids, weights, flag, slots, sh ? logits + QG_EXPERTS : nullptr, rows, out, resid};
+    pf_launch(9, pf_combine_kernel, dim3((D / 4 + 255) / 256, nt), dim3(256), 0, s, CA);
+    if ((rc = hipGetLastError())) return rc;
+    if (stats) {
+        pf_stats_kernel<<<1, 1024, 0, s>>>(stats, flag, (const int *)(ws + lay.missing), (const double *)(ws + lay.mass), nt);
+        if ((rc = hipGetLastError())) return rc;
+    }
+    return hipSuccess;
+}
+
+// CSR dispatch of an ids array (qg_moe_dispatch): histogram per 32-token
+// chunk, prefix sums, stable fill.  scratch: qg_prefill_dispatch_scratch(nt) bytes.
+size_t qg_prefill_dispatch_scratch(int nt) {
+    const size_t nch = (nt + PF_CHUNK - 1) / PF_CHUNK;
+    return nch * QG_EXPERTS * 4 + nch * 4;
+}
+
+int qg_prefill_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int nt, void *scratch) {
+    const int nch = (nt + PF_CHUNK - 1) / PF_CHUNK;
+    int *counts = (int *)scratch, *bad = counts + (size_t)nch * QG_EXPERTS;
+    hipStream_t s = qg_stream();
+    pf_count_kernel<<<nch, 512, 0, s>>>(counts, bad, ids, nt);
+    int rc = hipGetLastError();
+    if (rc) return rc;
+    pf_scan_kernel<<<1, 512, 0, s>>>(counts, nch, offsets, nullptr, 0, bad, status);
+    if ((rc = hipGetLastError())) return rc;
+    pf_fill_kernel<<<nch, 512, 0, s>>>(row_token, row_slot, counts, ids, nullptr, nt);
+    return hipGetLastError();
+}

@@ -56,7 +56,7 @@ class MoeLayer(C.Structure):
     _fields_ = [("width", I), ("ff", I), ("router", P), ("gate", P), ("up", P), ("down", P),
                 ("gate_type", I), ("up_type", I), ("down_type", I),
                 ("sh_gate", P), ("sh_up", P), ("sh_down", P), ("sh_gate_type", I), ("sh_up_type", I), ("sh_down_type", I),
-                ("sh_gate_inp", P), ("resident", P), ("threshold", D64)]
+                ("sh_gate_inp", P), ("resident", P), ("threshold", D64), ("router_bias", P)]
 
 
 _LIB = None

@@ -344,6 +344,9 @@ int nbo_layer(float *out, int *ids_out, float *w_out, float *logits_out, uint8_t
     int *ids = malloc((size_t)nt * NBO_TOP * 4);
     if (!logits || !w || !ids) goto done;
     if (nbo_matmul(logits, L->router, 0, NBO_EXPERTS, L->D, x, nt)) goto done;
+    if (L->router_bias)
+        for (int t = 0; t < nt; t++)
+            for (int e = 0; e < NBO_EXPERTS; e++) logits[(size_t)t * NBO_EXPERTS + e] += L->router_bias[e];
     nbo_route(ids, w, logits, nt);
     if (resident) {
         if (flags) nbo_coverage(flags, NULL, ids, w, resident, nt);

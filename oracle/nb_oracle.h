@@ -54,6 +54,8 @@ int nbo_shared(float *out, const float *x, int nt, int D, int F, const void *gat
 
 /* One routed-MoE layer as the reference's moe() runs it (qwen.c:714-735).
  * resident may be NULL (no pruning).  shared_* may be NULL (no shared expert).
+ * router_bias (synthetic workloads only; the reference's router has none) is
+ * added to each logit with one fp32 add before routing.
  * ids/weights/logits/flags outputs may be NULL. */
 typedef struct {
     int D, F;
@@ -61,6 +63,7 @@ typedef struct {
     const void *gate, *up, *down; int gt, ut, dt;
     const void *sh_gate, *sh_up, *sh_down; int sgt, sut, sdt;
     const float *sh_inp;                     /* F32 [1, D] */
+    const float *router_bias;                /* F32 [512] added to the logits, or NULL */
 } nbo_layer_desc;
 int nbo_layer(float *out, int *ids, float *weights, float *logits, uint8_t *flags,
               const nbo_layer_desc *L, const float *x, int nt, const uint8_t *resident,

@@ -24,7 +24,8 @@ class PruneStats(C.Structure):
 
 class LayerDesc(C.Structure):
     _fields_ = [("D", I), ("F", I), ("router", P), ("gate", P), ("up", P), ("down", P), ("gt", I), ("ut", I), ("dt", I),
-                ("sh_gate", P), ("sh_up", P), ("sh_down", P), ("sgt", I), ("sut", I), ("sdt", I), ("sh_inp", P)]
+                ("sh_gate", P), ("sh_up", P), ("sh_down", P), ("sgt", I), ("sut", I), ("sdt", I), ("sh_inp", P),
+                ("router_bias", P)]
 
 
 _SIG = {
@@ -149,8 +150,9 @@ class HostLayer:
     which only the experts that are needed get generated (CPU generator) or
     copied (from the device)."""
 
-    def __init__(self, seed, width=2048, ff=512, gt=12, ut=12, dt=12, shared=False, sh_types=(12, 12, 12)):
+    def __init__(self, seed, width=2048, ff=512, gt=12, ut=12, dt=12, shared=False, sh_types=(12, 12, 12), router_bias=None):
         self.seed, self.D, self.F = seed, width, ff
+        self.router_bias = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32).reshape(EXPERTS)
         self.gt, self.ut, self.dt = gt, ut, dt
         self.per = {"gate": ff * row_bytes(gt, width), "up": ff * row_bytes(ut, width), "down": width * row_bytes(dt, ff)}
         self.gate = np.zeros(EXPERTS * self.per["gate"], np.uint8)
@@ -167,12 +169,16 @@ class HostLayer:
             self.sh_down = fill_matrix(sd, seed, 7 << 32, width, ff)
             self.sh_inp = fill_matrix(0, seed, 8 << 32, 1, width).view(np.float32)
 
-    def ensure(self, experts) -> None:
+    def ensure(self, experts, fetch=None) -> None:
+        """Make the listed experts' matrices present: generated on the CPU, or
+        fetch(name, e) -> bytes (a copy of the device's, whose generator is
+        checked equal to this one's separately)."""
         for e in sorted(set(int(v) for v in np.ravel(experts) if 0 <= v < EXPERTS) - self.have):
             for name, tensor, typ, rows, cols in (("gate", 2, self.gt, self.F, self.D), ("up", 3, self.ut, self.F, self.D),
                                                   ("down", 4, self.dt, self.D, self.F)):
                 per = self.per[name]
-                getattr(self, name)[e * per:(e + 1) * per] = fill_matrix(typ, self.seed, (tensor << 32) | e, rows, cols)
+                getattr(self, name)[e * per:(e + 1) * per] = (
+                    fetch(name, e) if fetch is not None else fill_matrix(typ, self.seed, (tensor << 32) | e, rows, cols))
             self.have.add(e)
 
     def desc(self) -> LayerDesc:
@@ -182,15 +188,24 @@ class HostLayer:
             d.sh_gate, d.sh_up, d.sh_down = self.sh_gate.ctypes.data, self.sh_up.ctypes.data, self.sh_down.ctypes.data
             d.sgt, d.sut, d.sdt = self.sh_types
             d.sh_inp = self.sh_inp.ctypes.data
+        if self.router_bias is not None:
+            d.router_bias = self.router_bias.ctypes.data
         return d
 
-    def forward(self, x, resident=None, threshold=0.10):
+    def logits(self, x):
+        """Router logits (+ the optional bias) of the rows of x."""
+        logits = matmul(self.router, 0, EXPERTS, self.D, np.ascontiguousarray(x, np.float32))
+        if self.router_bias is not None:
+            logits += self.router_bias
+        return logits
+
+    def forward(self, x, resident=None, threshold=0.10, fetch=None):
         """The reference's layer on the CPU: (out, ids, weights, logits, flags, stats)."""
         x = np.ascontiguousarray(x, np.float32)
         nt = x.shape[0]
-        logits = matmul(self.router, 0, EXPERTS, self.D, x)
+        logits = self.logits(x)
         ids, w = route(logits)
-        self.ensure(ids)
+        self.ensure(ids, fetch)
         out = np.empty((nt, self.D), np.float32)
         oids = np.empty((nt, TOP), np.int32)
         ow = np.empty((nt, TOP), np.float32)

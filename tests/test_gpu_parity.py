@@ -156,11 +156,23 @@ def test_moe_map_and_dispatch(qgl):
         np.testing.assert_array_equal(off.get(), ooff)
         np.testing.assert_array_equal(tok.get()[:len(otok)], otok)
         np.testing.assert_array_equal(slot.get()[:len(oslot)], oslot)
-    bad = ids.copy()
-    bad[3, 4] = 700
-    dids = Device(bad)
+    # pruned encodings (-e-2) are skipped
+    pruned = ids.copy()
+    pruned[::7, 9] = -pruned[::7, 9] - 2
+    dids = Device(pruned)
     call("moe_dispatch", off.p, tok.p, slot.p, status.p, dids.p, nt)
-    assert status.get()[0] != 0
+    ooff, otok, oslot = O.dispatch(pruned)
+    assert status.get()[0] == 0
+    np.testing.assert_array_equal(off.get(), ooff)
+    np.testing.assert_array_equal(tok.get()[:len(otok)], otok)
+    np.testing.assert_array_equal(slot.get()[:len(oslot)], oslot)
+    # invalid ids and duplicates set the status
+    for r, k, v in ((3, 4, 700), (5, 2, -1), (9, 1, -600), (11, 8, None)):
+        bad = ids.copy()
+        bad[r, k] = bad[r, 0] if v is None else v
+        dids = Device(bad)
+        call("moe_dispatch", off.p, tok.p, slot.p, status.p, dids.p, nt)
+        assert status.get()[0] != 0, (r, k, v)
 
 
 def test_gather_scatter_reduce_order_independent(qgl):
@@ -417,9 +429,12 @@ def test_forward_rejects_bad_arguments(layer0):
     L, _ = layer0
     fw = synth.Forward(2048, 512, 17)
     lib = qg.lib()
-    assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 18, C.byref(L.desc), fw.ws.p, fw.ws_bytes) != 0
+    for nt in (0, 8193):  # token counts outside 1..8192 (18..8192 is the prefill path)
+        assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, nt, C.byref(L.desc), fw.ws.p, fw.ws_bytes) != 0
+    # a workspace sized for 17 tokens is too small for a 2048-token prefill
+    assert lib.qg_moe_workspace_bytes(2048, 512, 2048) > fw.ws_bytes
     assert lib.qg_moe_forward(fw.out.p, fw.ids.p, fw.w.p, None, None, fw.x.p, 1, C.byref(L.desc), fw.ws.p, 16) != 0
-    assert lib.qg_moe_workspace_bytes(2048, 512, 18) == 0
+    assert lib.qg_moe_workspace_bytes(2048, 512, 8193) == 0
 
 
 def test_layer_generic_fallback_width(qgl):

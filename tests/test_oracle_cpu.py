@@ -275,6 +275,45 @@ def test_map_and_dispatch_brute_force():
     assert O.dispatch(ids) is None
 
 
+# ---------------- config 3 inputs: router bias ----------------
+
+def test_zipf_bias_closed_form():
+    """bias = log p(pi(e)) / 3 with p(r) proportional to r**-1.1: exp(3*bias)
+    is a probability vector whose sorted values are the Zipf law, and the
+    permutation depends only on the seed."""
+    from nebula_amd import synth
+    b = synth.zipf_bias(33).astype(np.float64)
+    p = np.exp(3.0 * b)
+    assert abs(p.sum() - 1.0) < 1e-5
+    r = np.arange(1, 513, dtype=np.float64)
+    want = r ** -1.1 / (r ** -1.1).sum()
+    np.testing.assert_allclose(np.sort(p)[::-1], want, rtol=2e-6)
+    np.testing.assert_array_equal(synth.zipf_bias(33), b.astype(np.float32))
+    assert not np.array_equal(synth.zipf_bias(34), synth.zipf_bias(33))
+
+
+def test_layer_router_bias_changes_routing_as_logits_plus_bias():
+    """nbo_layer with a router bias routes exactly as route(matmul(x) + bias)
+    and returns those logits; a zero bias changes nothing."""
+    from nebula_amd import synth
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (6, 256)).astype(np.float32)
+    bias = synth.zipf_bias(7)
+    H = O.HostLayer(11, width=256, ff=128, gt=12, ut=12, dt=20, router_bias=bias)
+    out, ids, w, logits, flags, _ = H.forward(x)
+    raw = O.matmul(H.router, 0, 512, 256, x)
+    np.testing.assert_array_equal(logits, raw + bias)
+    oi, ow = O.route(raw + bias)
+    np.testing.assert_array_equal(ids, oi)
+    np.testing.assert_array_equal(w.view('u4'), ow.view('u4'))
+    assert not np.array_equal(ids, O.route(raw)[0])
+    H0 = O.HostLayer(11, width=256, ff=128, gt=12, ut=12, dt=20, router_bias=np.zeros(512, np.float32))
+    H1 = O.HostLayer(11, width=256, ff=128, gt=12, ut=12, dt=20)
+    a, b = H0.forward(x), H1.forward(x)
+    np.testing.assert_array_equal(a[0].view('u4'), b[0].view('u4'))
+    np.testing.assert_array_equal(a[1], b[1])
+
+
 # ---------------- shared expert and layer composition ----------------
 
 def test_shared_expert_closed_form():
