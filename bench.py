@@ -52,7 +52,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "routed-MoE tokens/s + % HBM peak at B=1/17; int8 MFMA util at 2048-tok prefill"
 KERNELS = ["router", "route", "gate_up", "down"]
 PF_KERNELS = ["router", "route", "scan", "fill", "gate_up_dense", "gate_up_other", "down_dense", "down_other",
-              "down_shared", "combine"]
+              "down_shared", "combine", "count"]
 INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 MFMA (POP/s x 1e3)
 FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 MFMA
 DENSE_MIN = 256                   # rows from which an expert runs in the dense pass

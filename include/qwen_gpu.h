@@ -140,7 +140,8 @@ int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *f
  * (hipExtLaunchKernelGGL).  Decode: 0 router, 1 routing, 2 gate/up, 3 down.
  * Prefill: 0 router, 1 routing, 2 scan, 3 fill, 4 gate/up dense pass,
  * 5 gate/up other experts, 6 down dense pass, 7 down other experts,
- * 8 shared-expert down (when its format differs), 9 combine.  n <= 32;
+ * 8 shared-expert down (when its format differs), 9 combine, 10 chunk
+ * histogram.  n <= 32;
  * n = 0 disables. */
 int qg_moe_kernel_events(void **events, int n);
 

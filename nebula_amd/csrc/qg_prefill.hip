@@ -6,11 +6,12 @@
 // per-expert row lists built on the device.
 //
 // Kernels per layer:
-//   P1 router   : qg_matmul's exact-order F32 kernel (the summation order of
-//                 cpu.c:122-139), rows 0..511 plus the shared gate vector.
-//   P2 route    : a block = 8 waves = a chunk of 32 tokens, a wave per token:
-//                 router bias, top-10, coverage/prune, flags, the activation
-//                 planes; then the chunk's per-expert token masks, whose
+//   P1 router   : exact-order router GEMM (the summation order of
+//                 cpu.c:122-139, so logits and routing are bit-exact), rows
+//                 0..511 plus the shared gate vector, + optional bias.
+//   P2 route    : a wave per token: top-10, coverage/prune, flags, and the
+//                 token's fp16 activation planes.
+//   P2b count   : per 32-token chunk, the per-expert token masks, whose
 //                 popcounts are the chunk's histogram counts[chunk][e].
 //   P3 scan     : per-expert totals, CSR offsets, per-chunk bases (exclusive
 //                 prefix over chunks), and the table of 64-row tiles per group.
@@ -123,52 +124,129 @@ __global__ __launch_bounds__(256) void pf_norm_kernel(float *xn, const float *x,
     for (int i = lane; i < D; i += 64) xn[(size_t)t * D + i] = xr[i] * sc;
 }
 
-// ---------------- P2: routing, planes, chunk histogram ----------------
+// ---------------- P1: router logits ----------------
+// logits[t][r] = sum_k R[r][k] x[t][k] in the order of cpu.c:122-139: chain j
+// (0..31) accumulates k = j, j+32, ... ascending with fused multiply-add,
+// then the tree 16/8/4/2/1 of gpu.cu:154-180 (qg_tree32).  Block = 8 waves =
+// 64 tokens x 32 rows; half-wave h of wave w owns 16 tokens (w & 3) x 8 rows
+// ((w >> 2) * 2 + h), lane j of the half-wave owns chain j of all 128 of its
+// outputs.  K chunks of 128 columns of both operands are staged in shared
+// memory (direct global->shared copies, double-buffered); the two half-waves
+// of a wave read the same token rows (broadcast) and different router rows.
+// The final tree runs as an exchange butterfly: at offset s the lanes with
+// bit s clear keep the lower half of their outputs, the others the upper half,
+// and each adds its partner's value; float addition is commutative, so every
+// output is the same sum, paired the same way, as lane 0's of qg_tree32.
+// Lane j ends with outputs 4j..4j+3 = token j/2, rows 4(j&1)..4(j&1)+3.
+constexpr int RT_TOK = 64, RT_ROWS = 32, RT_KC = 128;
+constexpr int RT_LDS = 2 * (RT_ROWS + RT_TOK) * RT_KC * 4;
+
+struct RouterArgs {
+    const float *x; int nt, D, rows;
+    const float *router, *sh_row;    // rows 0..511, row 512 (the shared gate vector) when rows == 513
+    const float *bias;               // added to rows 0..511, or null
+    float *logits;                   // [nt][rows]
+};
+
+__global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    float *sw = (float *)s_dyn;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, j = lane & 31;
+    const int tg = wave & 3, rg = (wave >> 2) * 2 + h;
+    const int t0 = blockIdx.x * RT_TOK, r0 = blockIdx.y * RT_ROWS, nch = A.D / RT_KC;
+    auto stage = [&](int c, int b) {
+        // 32 router rows then 64 token rows, 512 B each: 48 copies of two rows
+        for (int q = wave; q < (RT_ROWS + RT_TOK) / 2; q += 8) {
+            const int R = 2 * q + h;
+            const float *src;
+            if (R < RT_ROWS) {
+                const int r = min(r0 + R, A.rows - 1);
+                src = r == QG_EXPERTS ? A.sh_row : A.router + (size_t)r * A.D;
+            } else {
+                src = A.x + (size_t)min(t0 + R - RT_ROWS, A.nt - 1) * A.D;
+            }
+            dma16(src + (size_t)c * RT_KC + 4 * j, sw + (size_t)b * (RT_ROWS + RT_TOK) * RT_KC + q * 2 * RT_KC);
+        }
+    };
+    float acc[16][8];
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+#pragma unroll
+        for (int r = 0; r < 8; r++) acc[t][r] = 0.0f;
+    stage(0, 0);
+    for (int c = 0; c < nch; c++) {
+        wait_vmem();
+        __syncthreads();
+        if (c + 1 < nch) stage(c + 1, (c + 1) & 1);
+        const float *W = sw + (size_t)(c & 1) * (RT_ROWS + RT_TOK) * RT_KC + rg * 8 * RT_KC;
+        const float *X = sw + (size_t)(c & 1) * (RT_ROWS + RT_TOK) * RT_KC + (RT_ROWS + tg * 16) * RT_KC;
+#pragma unroll
+        for (int i = 0; i < RT_KC / 32; i++) {
+            float wv[8], xv[16];
+#pragma unroll
+            for (int r = 0; r < 8; r++) wv[r] = W[r * RT_KC + 32 * i + j];
+#pragma unroll
+            for (int t = 0; t < 16; t++) xv[t] = X[t * RT_KC + 32 * i + j];
+#pragma unroll
+            for (int t = 0; t < 16; t++)
+#pragma unroll
+                for (int r = 0; r < 8; r++) acc[t][r] = __builtin_fmaf(wv[r], xv[t], acc[t][r]);
+        }
+    }
+    // exchange butterfly over the 32 lanes of the half-wave; v[o], o = 8t + r
+    float *v = &acc[0][0];
+#pragma unroll
+    for (int s = 16, n = 128; s >= 1; s >>= 1, n >>= 1) {
+        const bool up = (j & s) != 0;
+#pragma unroll
+        for (int q = 0; q < n / 2; q++) {
+            const float send = up ? v[q] : v[q + n / 2];
+            const float recv = __shfl_xor(send, s, 32);
+            v[q] = (up ? v[q + n / 2] : v[q]) + recv;
+        }
+    }
+    const int t = t0 + tg * 16 + (j >> 1);
+    if (t < A.nt) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int r = r0 + rg * 8 + 4 * (j & 1) + q;
+            if (r < A.rows) A.logits[(size_t)t * A.rows + r] = A.bias && r < QG_EXPERTS ? v[q] + A.bias[r] : v[q];
+        }
+    }
+}
+
+// ---------------- P2: routing and activation planes ----------------
 struct RouteArgs {
-    int nt; const float *logits; int ld; const float *bias;
+    int nt; const float *logits; int ld;
     const uint8_t *resident; double thr;
     int *ids; float *w; uint8_t *flags_out; int *flag; int *missing; double *mass;
     const float *x; int D; _Float16 *xp, *xsp;
-    int *counts;                     // [chunk][512]
 };
 
-__global__ __launch_bounds__(512) void pf_route_kernel(RouteArgs A) {
-    __shared__ float s_row[8][QG_EXPERTS];
-    __shared__ float s_rv[8][64];
-    __shared__ int s_ri[8][64];
-    __shared__ uint32_t s_mask[QG_EXPERTS];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int t0 = blockIdx.x * PF_CHUNK;
-    s_mask[tid] = 0u;  // 512 threads, one per expert
-    __syncthreads();
-    for (int i = 0; i < PF_CHUNK / 8; i++) {
-        const int tl = wave * (PF_CHUNK / 8) + i, t = t0 + tl;
-        if (t >= A.nt) break;  // wave-uniform
-        const float *lr = A.logits + (size_t)t * A.ld;
-        for (int e = lane; e < QG_EXPERTS; e += 64) s_row[wave][e] = A.bias ? lr[e] + A.bias[e] : lr[e];
-        wave_sync_lds();
-        int id, missing;
-        float wv;
-        double mass;
-        qg_route_fast(s_row[wave], lane, id, wv, s_rv[wave], s_ri[wave]);
-        const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
-        if (lane < QG_TOP) {
-            A.ids[(size_t)t * QG_TOP + lane] = id;
-            A.w[(size_t)t * QG_TOP + lane] = wv;
-            if (flag < 2 && id >= 0 && id < QG_EXPERTS) atomicOr(&s_mask[id], 1u << tl);
-        }
-        if (lane == 0) {
-            A.flag[t] = flag;
-            A.missing[t] = missing;
-            A.mass[t] = mass;
-            if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
-        }
-        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
-        token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
-        wave_sync_lds();  // s_row / s_rv / s_ri are rewritten for the wave's next token
+// One wave per token: top-10 of the (biased) logits, coverage/prune, flags;
+// then the token's fp16 hi/lo planes and 32-group sum planes.
+__global__ __launch_bounds__(256) void pf_route_kernel(RouteArgs A) {
+    __shared__ float s_rv[4][64];
+    __shared__ int s_ri[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + wave;
+    if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
+    int id, missing;
+    float wv;
+    double mass;
+    qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv[wave], s_ri[wave]);
+    const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+    if (lane < QG_TOP) {
+        A.ids[(size_t)t * QG_TOP + lane] = id;
+        A.w[(size_t)t * QG_TOP + lane] = wv;
     }
-    __syncthreads();
-    A.counts[(size_t)blockIdx.x * QG_EXPERTS + tid] = __popc(s_mask[tid]);
+    if (lane == 0) {
+        A.flag[t] = flag;
+        A.missing[t] = missing;
+        A.mass[t] = mass;
+        if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
+    }
+    _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
+    token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
 }
 
 // ---------------- P3: offsets, chunk bases, tile table ----------------
@@ -257,7 +335,7 @@ __global__ __launch_bounds__(512) void pf_scan_kernel(int *counts, int nch, int 
 // pf_route_kernel; bad[chunk] = 1 if an id is neither in [0,512) nor a pruned
 // encoding in [-513,-2], or a token lists an expert twice (the validation of
 // cpu.c:242-244).
-__global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, const int *ids, int nt) {
+__global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, const int *ids, const int *flag, int nt) {
     __shared__ uint32_t s_mask[QG_EXPERTS];
     __shared__ int s_bad;
     const int tid = threadIdx.x, t0 = blockIdx.x * PF_CHUNK;
@@ -266,7 +344,7 @@ __global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, co
     __syncthreads();
     if (tid < PF_CHUNK * QG_TOP) {
         const int tl = tid / QG_TOP, t = t0 + tl;
-        if (t < nt) {
+        if (t < nt && (!flag || flag[t] < 2)) {
             const int id = ids[(size_t)t * QG_TOP + tid - tl * QG_TOP];
             if (id >= 0 && id < QG_EXPERTS) {
                 if (atomicOr(&s_mask[id], 1u << tl) & (1u << tl)) s_bad = 1;
@@ -277,7 +355,7 @@ __global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, co
     }
     __syncthreads();
     counts[(size_t)blockIdx.x * QG_EXPERTS + tid] = __popc(s_mask[tid]);
-    if (tid == 0) bad[blockIdx.x] = s_bad;
+    if (tid == 0 && bad) bad[blockIdx.x] = s_bad;
 }
 
 // ---------------- P4: stable fill ----------------
@@ -310,20 +388,20 @@ __global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_s
 
 // ---------------- GEMM building blocks ----------------
 
-// Stage K chunk `chunk` of the tile's 64 rows: plane rows of `planes`
-// (row stride `stride` elements per plane, 2 planes per source row; source row
-// of tile row r = src[r]) into `stage`, swizzled; nck = 16-byte chunks per
-// plane row in this K chunk.  With `sums`, the 2 x 8 group sums of the chunk
-// ([tile row][plane][8]).
+// Stage K chunk `chunk` of the tile's first nrows rows (a multiple of 16):
+// plane rows of `planes` (row stride `stride` elements per plane, 2 planes
+// per source row; source row of tile row r = src[r]) into `stage`, swizzled;
+// nck = 16-byte chunks per plane row in this K chunk.  With `sums`, the 2 x 8
+// group sums of the chunk ([tile row][plane][8]).
 QG_DEV void stage_rows(uint8_t *stage, uint8_t *sums, const _Float16 *planes, int stride, const _Float16 *sum_planes,
-                       int sum_stride, const int *src, int chunk, int nck, int wave, int lane) {
-    for (int q = wave; q < PT; q += 4) {
+                       int sum_stride, const int *src, int chunk, int nck, int nrows, int wave, int lane) {
+    for (int q = wave; q < nrows; q += 4) {
         const int R = 2 * q + (lane >> 5), tr = R >> 1, p = R & 1;
         int c = (lane & 31) ^ (tr & 15);
         if (c >= nck) c = 0;  // positions no reader uses
         dma16(planes + ((size_t)src[tr] * 2 + p) * stride + (size_t)chunk * KC + c * 8, stage + q * 1024);
     }
-    if (sums && wave < 2) {
+    if (sums && wave * 32 < nrows) {
         const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
         dma16(sum_planes + ((size_t)src[tr] * 2 + p) * sum_stride + (size_t)chunk * 8, sums + wave * 1024);
     }
@@ -347,7 +425,9 @@ QG_DEV void q4_load(Q4Ops &o, const uint8_t *const *wrow, int sb, int kq) {
 }
 
 // y[m][n] += d * (s*q . x) - dmin * (m . X) over one Q4_K superblock, for the
-// first M row tiles.
+// first M row tiles.  The A fragments of K step f+1 are read from shared
+// memory while step f's products run (one wave per SIMD: nothing else would
+// hide the shared-memory latency).
 template <int M>
 QG_DEV void q4_chunk(qg_f4 (&y)[4][4], const Q4Ops &o, const uint8_t *st, const uint8_t *ss, int j, int kq) {
     Q4kHeader h[4];
@@ -359,25 +439,37 @@ QG_DEV void q4_chunk(qg_f4 (&y)[4][4], const Q4Ops &o, const uint8_t *st, const 
 #pragma unroll
         for (int n = 0; n < 4; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int gA = 2 * (kq >> 1);
+    qg_half8 a[2][M][2];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        a[0][m][0] = stage_frag(st, m * 16 + j, 0, kq);
+        a[0][m][1] = stage_frag(st, m * 16 + j, 1, kq);
+    }
 #pragma unroll
     for (int f = 0; f < 8; f++) {
-        qg_half8 a[M][2];
+        const int cur = f & 1;
+        if (f + 1 < 8) {
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            a[m][0] = stage_frag(st, m * 16 + j, 0, 4 * f + kq);
-            a[m][1] = stage_frag(st, m * 16 + j, 1, 4 * f + kq);
+            for (int m = 0; m < M; m++) {
+                a[cur ^ 1][m][0] = stage_frag(st, m * 16 + j, 0, 4 * (f + 1) + kq);
+                a[cur ^ 1][m][1] = stage_frag(st, m * 16 + j, 1, 4 * (f + 1) + kq);
+            }
         }
+        qg_half8 b[4];
 #pragma unroll
         for (int n = 0; n < 4; n++) {
             const uint4 c = f < 4 ? o.c0[n] : o.c1[n];
             const int g = (f < 4 ? gA : gA + 4) + ((f & 3) >> 1);
-            const qg_half8 b = q4k_chunk_frag(c, f & 3, (_Float16)q4k_s(h[n], g));
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], b, acc[m][n], 0, 0, 0);
-                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][1], b, acc[m][n], 0, 0, 0);
-            }
+            b[n] = q4k_chunk_frag(c, f & 3, (_Float16)q4k_s(h[n], g));
         }
+        // plane-major: the two products into one accumulator are 4*M apart
+#pragma unroll
+        for (int p = 0; p < 2; p++)
+#pragma unroll
+            for (int n = 0; n < 4; n++)
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][p], b[n], acc[m][n], 0, 0, 0);
     }
     // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
     qg_half8 as[M];
@@ -413,31 +505,60 @@ QG_DEV void iq_load(IqOps &o, const uint8_t *const *wrow, int kc, int nb, int kq
             }
 }
 
-// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk.
+// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk, with the A
+// fragments of block b+1 read while block b's products run.
 template <int M>
 QG_DEV void iq_chunk(qg_f4 (&y)[4][4], const IqOps &o, const uint8_t *st, int j, int kq, int nb) {
+    qg_half8 a[2][M][2];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        a[0][m][0] = stage_frag(st, m * 16 + j, 0, kq);
+        a[0][m][1] = stage_frag(st, m * 16 + j, 1, kq);
+    }
 #pragma unroll
     for (int b = 0; b < 8; b++) {
         if (b >= nb) break;  // uniform
-        qg_half8 a[M][2];
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            a[m][0] = stage_frag(st, m * 16 + j, 0, 4 * b + kq);
-            a[m][1] = stage_frag(st, m * 16 + j, 1, 4 * b + kq);
-        }
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
-            const qg_half8 bf = iq4_frag4(o.q[n][b]);
-            const float d = qg_half_u16(o.d[n][b]);
+        const int cur = b & 1;
+        if (b + 1 < nb) {
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], bf, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][1], bf, acc, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d, acc[i], y[m][n][i]);
+                a[cur ^ 1][m][0] = stage_frag(st, m * 16 + j, 0, 4 * (b + 1) + kq);
+                a[cur ^ 1][m][1] = stage_frag(st, m * 16 + j, 1, 4 * (b + 1) + kq);
             }
         }
+        qg_half8 bf[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) bf[n] = iq4_frag4(o.q[n][b]);
+        qg_f4 acc[M][4];
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int m = 0; m < M; m++)
+                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][0], bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int m = 0; m < M; m++) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][1], bf[n], acc[m][n], 0, 0, 0);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const float d = qg_half_u16(o.d[n][b]);
+#pragma unroll
+            for (int m = 0; m < M; m++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d, acc[m][n][i], y[m][n][i]);
+        }
     }
+}
+
+// Items of a persistent launch, XCD-aware: workgroup b runs on XCD b % 8
+// (round-robin dispatch), and XCD x takes the contiguous range of items
+// [x*C, (x+1)*C), C = ceil(total/8), so that the items running together on
+// one XCD share expert weights and activation rows in that XCD's L2.
+struct ItemRange { int next, end, step; };
+QG_DEV ItemRange xcd_items(int total) {
+    const int x = blockIdx.x & 7, slot = blockIdx.x >> 3, n_x = (gridDim.x - x + 7) >> 3;
+    const int C = (total + 7) >> 3;
+    return ItemRange{x * C + slot, min(total, (x + 1) * C), n_x};
 }
 
 // Tile -> order position (block-uniform): the largest p with tb[p] <= tile_idx
@@ -476,7 +597,8 @@ __global__ __launch_bounds__(256, 1) void pf_gateup_kernel(GuArgs A) {
     __syncthreads();
     const int nfb = A.F / GU_FB, NSB = A.D / 256, D32 = A.D / 32, F = A.F;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
-    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const ItemRange ir = xcd_items(total);
+    for (int item = ir.next; item < ir.end; item += ir.step) {
         const int tile_idx = t_lo + item / nfb, fb = item % nfb;
         const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
         const bool shared = g == QG_EXPERTS;
@@ -494,7 +616,7 @@ __global__ __launch_bounds__(256, 1) void pf_gateup_kernel(GuArgs A) {
         const uint8_t *wrow[4];
 #pragma unroll
         for (int n = 0; n < 4; n++) wrow[n] = (n < 2 ? bg : bu) + (size_t)(f0 + 16 * (n & 1) + j) * A.rb;
-        stage_rows(lds, lds + 2 * STAGE_BYTES, A.xp, A.D, A.xsp, D32, s_src, 0, 32, wave, lane);
+        stage_rows(lds, lds + 2 * STAGE_BYTES, A.xp, A.D, A.xsp, D32, s_src, 0, 32, 16 * M, wave, lane);
         Q4Ops cur, nxt;
         q4_load(cur, wrow, 0, kq);
         qg_f4 y[4][4];
@@ -508,7 +630,7 @@ __global__ __launch_bounds__(256, 1) void pf_gateup_kernel(GuArgs A) {
             if (sb + 1 < NSB) {
                 const int b = (sb + 1) & 1;
                 stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src, sb + 1, 32,
-                           wave, lane);
+                           16 * M, wave, lane);
                 q4_load(nxt, wrow, sb + 1, kq);
             }
             const uint8_t *st = lds + (sb & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (sb & 1) * SUMS_BYTES;
@@ -584,7 +706,8 @@ __global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
     __syncthreads();
     const int ndb = A.D / DN_DB, F = A.F, F32 = A.F / 32, nkc = (F + KC - 1) / KC;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
-    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const ItemRange ir = xcd_items(total);
+    for (int item = ir.next; item < ir.end; item += ir.step) {
         const int tile_idx = t_lo + item / ndb, db = item % ndb;
         const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
         const bool shared = g == QG_EXPERTS;
@@ -608,7 +731,7 @@ __global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
 #pragma unroll
             for (int n = 0; n < 4; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
         if (FMT == QT_Q4_K) {
-            stage_rows(lds, lds + 2 * STAGE_BYTES, A.midp, F, A.msp, F32, s_src, 0, 32, wave, lane);
+            stage_rows(lds, lds + 2 * STAGE_BYTES, A.midp, F, A.msp, F32, s_src, 0, 32, 16 * M, wave, lane);
             Q4Ops cur, nxt;
             q4_load(cur, wrow, 0, kq);
             for (int kc = 0; kc < nkc; kc++) {
@@ -617,7 +740,7 @@ __global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
                 if (kc + 1 < nkc) {
                     const int b = (kc + 1) & 1;
                     stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src, kc + 1,
-                               32, wave, lane);
+                               32, 16 * M, wave, lane);
                     q4_load(nxt, wrow, kc + 1, kq);
                 }
                 const uint8_t *st = lds + (kc & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (kc & 1) * SUMS_BYTES;
@@ -631,7 +754,7 @@ __global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
             }
         } else {
             auto nblocks = [&](int kc) { return min(8, (F - kc * KC) / 32); };
-            stage_rows(lds, nullptr, A.midp, F, nullptr, 0, s_src, 0, 4 * nblocks(0), wave, lane);
+            stage_rows(lds, nullptr, A.midp, F, nullptr, 0, s_src, 0, 4 * nblocks(0), 16 * M, wave, lane);
             IqOps cur, nxt;
             iq_load(cur, wrow, 0, nblocks(0), kq);
             for (int kc = 0; kc < nkc; kc++) {
@@ -639,7 +762,7 @@ __global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
                 __syncthreads();
                 if (kc + 1 < nkc) {
                     stage_rows(lds + ((kc + 1) & 1) * STAGE_BYTES, nullptr, A.midp, F, nullptr, 0, s_src, kc + 1, 4 * nblocks(kc + 1),
-                               wave, lane);
+                               16 * M, wave, lane);
                     iq_load(nxt, wrow, kc + 1, nblocks(kc + 1), kq);
                 }
                 const uint8_t *st = lds + (kc & 1) * STAGE_BYTES;
@@ -793,19 +916,15 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
         if ((rc = hipGetLastError())) return rc;
         x = xn;
     }
-    // P1: router logits in the reference's order (+ shared gate row)
-    {
-        hipEvent_t b = nullptr, e = nullptr;
-        const bool timed = qg_kernel_event_pair(0, (void **)&b, (void **)&e);
-        if (timed && (rc = hipEventRecord(b, s))) return rc;
-        rc = qg_launch_matmul_exact(logits, (const uint8_t *)L->router, QT_F32, rows, D, x, nt,
-                                    sh ? (const uint8_t *)L->sh_gate_inp : nullptr, s);
-        if (rc) return rc;
-        if (timed && (rc = hipEventRecord(e, s))) return rc;
-    }
-    RouteArgs RA{nt, logits, rows, L->router_bias, L->resident, L->threshold, ids, weights, flags, flag,
-                 (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp, counts};
-    pf_launch(1, pf_route_kernel, dim3(nch), dim3(512), 0, s, RA);
+    // P1: router logits in the reference's order (+ shared gate row, + bias)
+    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, L->router_bias, logits};
+    pf_launch(0, pf_router_kernel, dim3((nt + RT_TOK - 1) / RT_TOK, (rows + RT_ROWS - 1) / RT_ROWS), dim3(512), RT_LDS, s, R);
+    if ((rc = hipGetLastError())) return rc;
+    RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, flag,
+                 (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp};
+    pf_launch(1, pf_route_kernel, dim3((nt + 3) / 4), dim3(256), 0, s, RA);
+    if ((rc = hipGetLastError())) return rc;
+    pf_launch(10, pf_count_kernel, dim3(nch), dim3(512), 0, s, counts, (int *)nullptr, (const int *)ids, (const int *)flag, nt);
     if ((rc = hipGetLastError())) return rc;
     pf_launch(2, pf_scan_kernel, dim3(1), dim3(512), 0, s, counts, nch, offsets, tt, sh ? nt : 0, (const int *)nullptr,
               (int *)nullptr);
@@ -857,7 +976,7 @@ int qg_prefill_dispatch(int *offsets, int *row_token, int *row_slot, int *status
     const int nch = (nt + PF_CHUNK - 1) / PF_CHUNK;
     int *counts = (int *)scratch, *bad = counts + (size_t)nch * QG_EXPERTS;
     hipStream_t s = qg_stream();
-    pf_count_kernel<<<nch, 512, 0, s>>>(counts, bad, ids, nt);
+    pf_count_kernel<<<nch, 512, 0, s>>>(counts, bad, ids, nullptr, nt);
     int rc = hipGetLastError();
     if (rc) return rc;
     pf_scan_kernel<<<1, 512, 0, s>>>(counts, nch, offsets, nullptr, 0, bad, status);

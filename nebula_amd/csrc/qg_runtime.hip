@@ -220,7 +220,11 @@ int qg_event_record(void *e) { return e ? hipEventRecord((hipEvent_t)e, tl_strea
 int qg_event_elapsed(float *ms, void *begin, void *end) {
     if (!ms || !begin || !end) return hipErrorInvalidValue;
     int rc = hipEventSynchronize((hipEvent_t)end);
-    return rc ? rc : hipEventElapsedTime(ms, (hipEvent_t)begin, (hipEvent_t)end);
+    if (!rc) rc = hipEventElapsedTime(ms, (hipEvent_t)begin, (hipEvent_t)end);
+    // an event that was never recorded is reported here only: clear the
+    // runtime's sticky last error so the next launch check does not see it
+    if (rc) (void)hipGetLastError();
+    return rc;
 }
 
 // Device description for roofline bookkeeping.

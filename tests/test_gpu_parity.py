@@ -437,6 +437,22 @@ def test_forward_rejects_bad_arguments(layer0):
     assert lib.qg_moe_workspace_bytes(2048, 512, 8193) == 0
 
 
+def test_unrecorded_event_does_not_poison_next_call(layer0):
+    """Timing a kernel that did not run reports an error, and the next layer
+    call still succeeds (the runtime's sticky error is cleared)."""
+    L, H = layer0
+    b, e = qg.Event(), qg.Event()
+    t = C.c_float()
+    assert qg.lib().qg_event_elapsed(C.byref(t), b.p, e.p) != 0
+    fw = synth.Forward(2048, 512, 1)
+    x = synth.inputs(3, 1, 2048)
+    fw.x.set(x)
+    fw.run(L, 1)
+    qg.call("sync")
+    out, ids, *_ = H.forward(x)
+    np.testing.assert_array_equal(fw.ids.get()[:1], ids)
+
+
 def test_layer_generic_fallback_width(qgl):
     """A width the decode fast path does not take (D=1024, F=256) runs the
     generic kernels behind the same entry point; same bars."""
