@@ -402,7 +402,7 @@ def main() -> int:
         line = {
             "metric": METRIC, "value": round(1 / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": r["steps"], "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": data,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": data,
             "config": {"workload": f"config2: {r['layers']}-layer routed-MoE stack, B=1, D=2048, 512 experts top-10, F=512, Q4_K; "
                                    "h <- h + MoE(RMSNorm(h)); one captured graph",
                        "layers": r["layers"], "stack_bytes": int(r["bytes"]),
@@ -436,9 +436,11 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
         "data": data,
         "config": {"workload": names[args.config],
+                   "arithmetic": "router fp32 in the reference order; experts on fp16 16x16x32 MFMA with exact integer "
+                                 "weights x fp16 hi/lo activation planes, fp32 accumulate and scales",
                    "batch_tokens": wl.nt, "layers_rotated": len(wl.layers), "unique_experts_mean": U,
                    "layer_bytes": int(nbytes), "layer_hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                    "layer_hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
