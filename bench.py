@@ -50,7 +50,7 @@ GATEUP_BYTES = 1_179_648          # gate + up rows of one Q4_K expert (2 x 512 x
 ROUTER_BYTES = EXPERTS * D * 4
 HBM_PEAK_GBS = 8000.0
 METRIC = "routed-MoE tokens/s + % HBM peak at B=1/17; int8 MFMA util at 2048-tok prefill"
-KERNELS = ["router", "route", "gate_up", "down"]
+KERNELS = ["router", "route", "gate_up", "down", "combine"]
 PF_KERNELS = ["router", "route", "scan", "fill", "gate_up_dense", "gate_up_other", "down_dense", "down_other",
               "down_shared", "combine", "count"]
 INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 MFMA (POP/s x 1e3)

@@ -137,7 +137,8 @@ int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *f
 /* Benchmark support: events[2i] and events[2i+1] (qg_event_create handles)
  * are recorded at the start and end of kernel i of this thread's
  * qg_moe_forward calls, timestamped by the dispatch itself
- * (hipExtLaunchKernelGGL).  Decode: 0 router, 1 routing, 2 gate/up, 3 down.
+ * (hipExtLaunchKernelGGL).  Decode: 0 router, 1 routing, 2 gate/up, 3 down,
+ * 4 combine.
  * Prefill: 0 router, 1 routing, 2 scan, 3 fill, 4 gate/up dense pass,
  * 5 gate/up other experts, 6 down dense pass, 7 down other experts,
  * 8 shared-expert down (when its format differs), 9 combine, 10 chunk

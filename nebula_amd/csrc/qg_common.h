@@ -330,11 +330,14 @@ QG_DEV uint32_t iq4_lookup(uint32_t idx) {
 }
 
 // 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,
-// element order (0,2),(1,3),(4,6),(5,7).  (1024+q)*s - 1024*s is exact.
+// element order (0,2),(1,3),(4,6),(5,7).  Each nibble is masked to a byte, a
+// byte permute puts it under the exponent byte 0x64 (fp16 1024 + q), and
+// (1024+q)*s - 1024*s is exact.
 QG_DEV qg_half8 q4_frag(uint2 b, int hi_nib, _Float16 s) {
-    const uint32_t w0 = hi_nib ? b.x >> 4 : b.x, w1 = hi_nib ? b.y >> 4 : b.y;
-    const uint32_t u[4] = {(w0 & 0x000F000Fu) | 0x64006400u, ((w0 >> 8) & 0x000F000Fu) | 0x64006400u,
-                           (w1 & 0x000F000Fu) | 0x64006400u, ((w1 >> 8) & 0x000F000Fu) | 0x64006400u};
+    const uint32_t n0 = (hi_nib ? b.x >> 4 : b.x) & 0x0F0F0F0Fu, n1 = (hi_nib ? b.y >> 4 : b.y) & 0x0F0F0F0Fu;
+    const uint32_t M = 0x64646464u;  // permute selectors 4 pick these bytes
+    const uint32_t u[4] = {__builtin_amdgcn_perm(M, n0, 0x04020400u), __builtin_amdgcn_perm(M, n0, 0x04030401u),
+                           __builtin_amdgcn_perm(M, n1, 0x04020400u), __builtin_amdgcn_perm(M, n1, 0x04030401u)};
     const qg_half2 sv = {s, s}, off = {(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
     qg_half8 r;
 #pragma unroll

@@ -3,7 +3,7 @@
 // Q4_K or IQ4_NL down.  It replaces moe()/grouped_moe()/shared_direct() of
 // qwen.c:633-735 for one layer without any host round trip.
 //
-// Kernels per layer (3 for B <= 4, 4 above).  No kernel waits on another block
+// Kernels per layer (4 for B = 1, 5 above).  No kernel waits on another block
 // of its own grid: on MI355X a grid-wide ticket costs ~12 ns per block of
 // serialised atomics and a device-scope fence ~17 us per 1000 waves, more than
 // a kernel boundary (~1.7-2.4 us).
@@ -12,17 +12,18 @@
 //                order, so logits, ids and weights are bit-exact.  Extra
 //                blocks write the fp16 hi/lo activation planes and per-32
 //                sums; optionally the input is RMS-normalised first.
-//   KR route   : B > 4 only; one wave per token: top-10, coverage/prune, flags.
+//   KR route   : B > 1 only; one wave per token: top-10, coverage/prune, flags.
 //   K2 gate/up : one workgroup per (selection, 32 rows of F).  A selection
 //                computes its expert only if it is the expert's first
 //                eligible selection (no dispatch list needed), for every token
-//                that chose the expert.  B <= 4 routes inline.  Products on the
+//                that chose the expert.  B = 1 routes inline.  Products on the
 //                matrix cores (v_mfma_f32_16x16x32_f16) with exact integer
 //                weights; SwiGLU; mid rows written as fp16 hi/lo planes.
-//   K3 down    : one workgroup per 16 output rows, owning every selected
-//                expert for those rows: down products on the matrix cores,
-//                then the router-rank sum of the 10 slots, the sigmoid-gated
-//                shared expert and the optional residual add, in-block.
+//   K3 down    : item = (owning expert, 64 output rows): weight slab and the
+//                tokens' mid planes staged in shared memory, products on the
+//                matrix cores, weighted results to per-selection slots.
+//   K4 combine : router-rank sum of the 10 slots, the sigmoid-gated shared
+//                expert and the optional residual add.
 //
 // Operand conventions and the K order of the weight formats are those of
 // qg_frag.h; here A row j = (token j/2, plane j%2), so a lane's D rows
@@ -36,13 +37,13 @@ namespace {
 constexpr int MB = QG_MAX_DECODE;         // 17 tokens
 constexpr int MS = MB * QG_TOP;           // 170 selections
 constexpr int ME = MS + MB;               // selection rows + shared-expert rows
-constexpr int RCH = 64;                   // router k-steps held in registers
 constexpr int INLINE_MAX = 1;             // tokens routed inside the gate/up kernel
 constexpr int GU_WGS = 512;               // gate/up grid cap (workgroups)
+constexpr int DN_WGS = 1024;              // down grid cap (workgroups)
 
 struct TokRoute { int flag[MB]; int missing[MB]; double mass[MB]; };
 
-struct DecLayout { size_t tok, logits, xp, xsum, midp, msum, total; };
+struct DecLayout { size_t tok, logits, xp, xsum, midp, msum, slots, total; };
 DecLayout dec_layout(int D, int F) {
     DecLayout L;
     size_t off = 0;
@@ -53,6 +54,7 @@ DecLayout dec_layout(int D, int F) {
     L.xsum = take((size_t)MB * 2 * (D / 32) * 2);
     L.midp = take((size_t)ME * 2 * F * 2);
     L.msum = take((size_t)ME * (F / 8) * 4);
+    L.slots = take((size_t)ME * D * 4);
     L.total = off;
     return L;
 }
@@ -81,53 +83,82 @@ struct RouterArgs {
     float *logits;                  // [nt][rows]
     int norm; float eps; float *xn; // RMS-normalise the input; normalised rows to xn
     _Float16 *xp, *xsp;             // planes [nt][2][D] (Q4_K order); planes of 32-group sums [nt][2][D/32]
-    int row_pairs;                  // blockIdx.x < row_pairs: router rows; == row_pairs: planes
+    int row_pairs;                  // blockIdx.x < row_pairs: router rows; above: planes
     const float *bias;              // F32 [512] added to the expert logits, or null
 };
 
-// Grid (row_pairs + 1, ceil(nt/4)), 4 waves per block, wave w = token
-// 4*blockIdx.y + w.  Router block x: each 32-lane half owns row 2x+half; lane j
-// accumulates columns k = j (mod 32) in ascending k with fma, then the
-// 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal the
-// reference's qc_matmul bit for bit.  All 64 weight and 64 input loads of a
-// lane (D = 2048) are issued before the first fma.  Block x = row_pairs: the
-// token's (optionally normalised) row as fp16 hi/lo planes in the Q4_K
-// fragment order, plus hi/lo planes of the sums of each 32-group.
+// Router: grid (row_pairs + ceil(nt/4)), 4 waves per block.  Router block x <
+// row_pairs: each 32-lane half owns row 2x+half, wave w the tokens w, w+4, ...,
+// w+4(TPW-1); lane j accumulates columns k = j (mod 32) in ascending k with
+// fma, then the 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal
+// the reference's qc_matmul bit for bit.  The router rows are read from HBM
+// once per block (the 4 waves share them through the L1); the loads of the
+// next chunk of k-steps are in flight while a chunk's fmas run.  Blocks x >=
+// row_pairs: one token per wave, its (optionally normalised) row as fp16
+// hi/lo planes in the Q4_K fragment order, plus hi/lo planes of the sums of
+// each 32-group.
+template <int TPW>
 __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
-    const int t = blockIdx.y * 4 + wave;
-    if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
-    const float *xr = A.x + (size_t)t * A.D;
-    const float sc = A.norm ? row_rms_scale(xr, A.D, A.eps, lane) : 1.0f;
-    if (blockIdx.x == A.row_pairs) {
+    if (blockIdx.x >= A.row_pairs) {
+        const int t = (blockIdx.x - A.row_pairs) * 4 + wave;
+        if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
+        const float *xr = A.x + (size_t)t * A.D;
+        const float sc = A.norm ? row_rms_scale(xr, A.D, A.eps, lane) : 1.0f;
         _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
         token_planes(xr, A.D, A.norm != 0, sc, lane, hi, hi + A.D, shi, shi + A.D / 32, A.xn ? A.xn + (size_t)t * A.D : nullptr);
         return;
     }
+    if (wave >= A.nt) return;  // whole wave
     const int row = blockIdx.x * 2 + half;
     const bool rok = row < A.rows;
     const float *wr = !rok ? A.router : row == QG_EXPERTS ? A.sh_row : A.router + (size_t)row * A.D;
-    float acc = 0.0f;
-    int k0 = 0;
-    for (; k0 + 32 * RCH <= A.D; k0 += 32 * RCH) {
-        float wv[RCH], xv[RCH];
+    // the wave's tokens; past the batch they repeat the wave's first token and are not stored
+    const float *xr[TPW];
+    float sc[TPW], acc[TPW];
 #pragma unroll
-        for (int i = 0; i < RCH; i++) {
-            wv[i] = wr[k0 + 32 * i + j];
-            xv[i] = xr[k0 + 32 * i + j];
+    for (int u = 0; u < TPW; u++) {
+        const int t = wave + 4 * u < A.nt ? wave + 4 * u : wave;
+        xr[u] = A.x + (size_t)t * A.D;
+        sc[u] = A.norm ? row_rms_scale(xr[u], A.D, A.eps, lane) : 1.0f;
+        acc[u] = 0.0f;
+    }
+    // chunks of CH k-steps; the loads of chunk c+1 are in flight while chunk c's fmas run
+    constexpr int CH = TPW == 1 ? 16 : 8;
+    const int nfull = A.D / (32 * CH);
+    float wv[2][CH], xv[2][TPW][CH];
+    auto load = [&](int b, int k0) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) wv[b][i] = wr[k0 + 32 * i + j];
+#pragma unroll
+        for (int u = 0; u < TPW; u++)
+#pragma unroll
+            for (int i = 0; i < CH; i++) xv[b][u][i] = xr[u][k0 + 32 * i + j];
+    };
+    if (nfull > 0) load(0, 0);
+    for (int c = 0; c < nfull; c += 2) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            if (c + b >= nfull) break;
+            if (c + b + 1 < nfull) load(b ^ 1, (c + b + 1) * 32 * CH);
+#pragma unroll
+            for (int i = 0; i < CH; i++)
+#pragma unroll
+                for (int u = 0; u < TPW; u++)
+                    acc[u] = __builtin_fmaf(wv[b][i], A.norm ? xv[b][u][i] * sc[u] : xv[b][u][i], acc[u]);
         }
-        if (A.norm)
-#pragma unroll
-            for (int i = 0; i < RCH; i++) xv[i] = xv[i] * sc;
-#pragma unroll
-        for (int i = 0; i < RCH; i++) acc = __builtin_fmaf(wv[i], xv[i], acc);
     }
-    for (; k0 < A.D; k0 += 32) {
-        const float xv = A.norm ? xr[k0 + j] * sc : xr[k0 + j];
-        acc = __builtin_fmaf(wr[k0 + j], xv, acc);
+    for (int k0 = nfull * 32 * CH; k0 < A.D; k0 += 32) {  // D not a multiple of 32*CH
+        const float w1 = wr[k0 + j];
+#pragma unroll
+        for (int u = 0; u < TPW; u++) acc[u] = __builtin_fmaf(w1, A.norm ? xr[u][k0 + j] * sc[u] : xr[u][k0 + j], acc[u]);
     }
-    const float r = qg_tree32(acc);
-    if (j == 0 && rok) A.logits[(size_t)t * A.rows + row] = A.bias && row < QG_EXPERTS ? r + A.bias[row] : r;
+#pragma unroll
+    for (int u = 0; u < TPW; u++) {
+        const float r = qg_tree32(acc[u]);
+        const int t = wave + 4 * u;
+        if (j == 0 && rok && t < A.nt) A.logits[(size_t)t * A.rows + row] = A.bias && row < QG_EXPERTS ? r + A.bias[row] : r;
+    }
 }
 
 // ---------------- KR: routing, one wave per token (B > 4) ----------------
@@ -391,34 +422,34 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     }
 }
 
-// ---------------- K3: down + router-rank combine + shared + residual ----------------
+// ---------------- K3: down ----------------
 struct DnArgs {
     int nt, D, F;
     const int *ids; const float *w; const TokRoute *tr;
-    qg_prune_stats *stats;               // accumulated by block 0 when pruning is active
     const uint8_t *down, *sh_down; size_t rb, sh_rb;
     const _Float16 *midp; const float *msum8;
-    const float *sh_logit; int ld;       // shared-expert gate logit of token t at sh_logit[t*ld]
-    float *out;                          // [nt][D] or null
-    float *resid;                        // [nt][D] residual updated in place, or null
+    float *slots;                        // [ME][D]: selection t*10+k (weighted), shared rows MS+t
 };
 
-constexpr int DN_ROWS = 8;               // output rows per workgroup
-constexpr int DN_WAVES = 8;              // waves per down workgroup
-constexpr int DN_LDS = 144 * 1024;       // shared memory for staged weight slabs
+constexpr int DN_ROWS = 64;              // output rows per item (16 per wave)
 
-// y (hi and lo planes) of one item for one 8-token tile (NB = F/32 blocks).  W: the item's 8
-// rows in LDS (row stride rb); MFMA columns j and j+8 both read row j&7.
-template <int FMT, int NB>
-QG_DEV qg_f4 down_tile(const DnArgs &A, const uint8_t *W, int rb, int j, int kq, int arow_slot, const int *oslot) {
+// A fragment of staged plane row r (0..15 = token r/2, plane r%2), 16-byte
+// chunk c; rows are F fp16 long, chunk c of row r stored at c ^ (r & 15).
+QG_DEV qg_half8 dn_frag(const uint8_t *ast, int F, int r, int c) {
+    return ld_frag((const _Float16 *)(ast + (size_t)r * F * 2 + 16 * (c ^ (r & 15))));
+}
+
+// y (rows 4kq..4kq+3 = tokens 2kq, 2kq+1 x {hi, lo}) of weight row wr
+// (shared memory) against the staged tile; F/32 IQ4_NL blocks or F/256 Q4_K
+// superblocks.  Q4_K min terms from the 8-row sums of the tile's tokens.
+template <int FMT>
+QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq, const float *msum8, const int *oslot) {
     qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint8_t *wr = W + (j & 7) * rb;
-    const _Float16 *ap = A.midp + ((size_t)arow_slot * 2 + (j & 1)) * A.F;
     if (FMT == QT_Q4_K) {
-        for (int sb = 0; sb < A.F / 256; sb++) {
+        for (int sb = 0; sb < F / 256; sb++) {
             qg_half8 af[8];
 #pragma unroll
-            for (int m = 0; m < 8; m++) af[m] = ld_frag(ap + sb * 256 + (m * 4 + kq) * 8);
+            for (int m = 0; m < 8; m++) af[m] = dn_frag(ast, F, j, sb * 32 + m * 4 + kq);
             const uint8_t *p = wr + sb * 144;
             const Q4kHeader h = q4k_header(*(const uint4 *)p);
             const uint4 ca = *(const uint4 *)(p + 16 + 16 * kq), cb = *(const uint4 *)(p + 16 + 16 * (kq + 4));
@@ -433,7 +464,7 @@ QG_DEV qg_f4 down_tile(const DnArgs &A, const uint8_t *W, int rb, int j, int kq,
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++) {
                 // group sums of mid: 4 partial sums of 8 rows per 32-group
-                const float4 *X = (const float4 *)(A.msum8 + (size_t)oslot[t2] * (A.F / GU_ROWS) + sb * 32);
+                const float4 *X = (const float4 *)(msum8 + (size_t)oslot[t2] * (F / 8) + sb * 32);
                 float M = 0.0f;
 #pragma unroll
                 for (int g = 0; g < 8; g++) {
@@ -445,51 +476,58 @@ QG_DEV qg_f4 down_tile(const DnArgs &A, const uint8_t *W, int rb, int j, int kq,
             }
         }
     } else {
-        // all NB activation fragments and all NB block products first, then the
-        // block scales: the products do not wait on one another
-        qg_half8 af[NB];
+        // per 8 blocks: every fragment and every product first, then the block scales
+        for (int b0 = 0; b0 < F / 32; b0 += 8) {
+            const int nb = min(8, F / 32 - b0);
+            qg_half8 af[8];
+            qg_f4 acc[8];
+            float d[8];
 #pragma unroll
-        for (int b = 0; b < NB; b++) af[b] = ld_frag(ap + b * 32 + kq * 8);
-        qg_f4 acc[NB];
-        float d[NB];
+            for (int b = 0; b < 8; b++)
+                if (b < nb) af[b] = dn_frag(ast, F, j, (b0 + b) * 4 + kq);
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const uint16_t *p16 = (const uint16_t *)(wr + 18 * b);  // 2-byte aligned
-            d[b] = qg_half_u16(p16[0]);
-            const uint32_t q = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
-            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[b], iq4_frag4(q), qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            for (int b = 0; b < 8; b++) {
+                if (b < nb) {
+                    const uint16_t *p16 = (const uint16_t *)(wr + 18 * (b0 + b));  // 2-byte aligned
+                    d[b] = qg_half_u16(p16[0]);
+                    const uint32_t q = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[b], iq4_frag4(q), qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+                if (b < nb)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(d[b], acc[b][i], y[i]);
         }
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(d[b], acc[b][i], y[i]);
     }
     return y;
 }
 
-// Workgroup = 8 waves owning output rows r0..r0+7 of every selected expert.
-// Items (the shared expert first, then each expert at its owning selection)
-// are staged in batches: one flat direct global->shared copy of every item's
-// 8-row weight slab (contiguous in memory), then the waves take the items
-// round robin; a wave loads an item's activation fragments in one batch.
-template <int FMT, int SFMT, int NB>
-__global__ __launch_bounds__(DN_WAVES * 64) void dec_down_kernel(DnArgs A) {
-    extern __shared__ uint4 s_wbuf[];   // slabs of 8 rows x rb bytes, slab stride rbmax*8
+// Persistent; item = (owner, 64 output rows): the shared expert first, then
+// each routed expert at its owning selection (its first eligible selection).
+// An item's 64-row weight slab (contiguous) and its tokens' mid planes (8 at a
+// time) are staged in shared memory by direct global->shared copies; each of
+// the 4 waves takes 16 rows (MFMA columns).  Results go to the selection's
+// slot, weighted by its routing weight (shared rows unweighted); the combine
+// kernel sums the slots in router-rank order.
+template <int FMT, int SFMT>
+__global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
+    extern __shared__ uint4 s_dyn[];
     __shared__ int s_first[QG_EXPERTS];
     __shared__ int s_ids[MS];
     __shared__ int s_flag[MB];
     __shared__ int s_items[MS + 1];
-    __shared__ int s_nitems;
-    __shared__ int s_list[DN_WAVES][MB];
-    __shared__ float s_val[ME][DN_ROWS];
+    __shared__ int s_nitems, s_n;
+    __shared__ int s_list[MB];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    const int ns = A.nt * QG_TOP, r0 = blockIdx.x * DN_ROWS;
+    const int ns = A.nt * QG_TOP, F = A.F;
     const bool has_shared = A.sh_down != nullptr;
-    for (int i = tid; i < QG_EXPERTS; i += DN_WAVES * 64) s_first[i] = 0x7fffffff;
-    for (int i = tid; i < ns; i += DN_WAVES * 64) s_ids[i] = A.ids[i];
+    for (int i = tid; i < QG_EXPERTS; i += 256) s_first[i] = 0x7fffffff;
+    for (int i = tid; i < ns; i += 256) s_ids[i] = A.ids[i];
     if (tid < A.nt) s_flag[tid] = A.tr->flag[tid];
     __syncthreads();
-    for (int i = tid; i < ns; i += DN_WAVES * 64) {
+    for (int i = tid; i < ns; i += 256) {
         const int e = s_ids[i];
         if (e >= 0 && e < QG_EXPERTS && s_flag[i / QG_TOP] < 2) atomicMin(&s_first[e], i);
     }
@@ -511,100 +549,146 @@ __global__ __launch_bounds__(DN_WAVES * 64) void dec_down_kernel(DnArgs A) {
         if (lane == 0) s_nitems = n;
     }
     __syncthreads();
-    const int nitems = s_nitems;
+    const int dblocks = A.D / DN_ROWS, total = s_nitems * dblocks;
     const int rbmax = (int)(A.rb > A.sh_rb ? A.rb : A.sh_rb);
-    const int slab = DN_ROWS * rbmax;                 // bytes per staged item (multiple of 16)
-    const int cps = slab / 16;                        // 16-byte chunks per slab
-    const int cap = (DN_LDS - 1024) / slab;           // items per batch (a partial last copy spills < 1 KB)
-    uint8_t *wbuf = (uint8_t *)s_wbuf;
-    for (int b0 = 0; b0 < nitems; b0 += cap) {
-        const int nb = min(cap, nitems - b0);
-        // one flat copy of nb slabs; chunks past a shorter slab copy its first chunk
-        for (int q = wave; q * 64 < nb * cps; q += DN_WAVES) {
-            int c = q * 64 + lane;
-            if (c >= nb * cps) c = 0;
-            const int bi = c / cps, off = c - bi * cps;
-            const int sidx = s_items[b0 + bi];
-            const bool shared = sidx == MS;
-            const int rb = (int)(shared ? A.sh_rb : A.rb);
-            const uint8_t *W = shared ? A.sh_down + (size_t)r0 * rb : A.down + ((size_t)s_ids[sidx] * A.D + r0) * rb;
-            dma16(W + 16 * (size_t)(off < DN_ROWS * rb / 16 ? off : 0), wbuf + (size_t)q * 64 * 16);
-        }
-        wait_vmem();
-        __syncthreads();
-        for (int bi = wave; bi < nb; bi += DN_WAVES) {
-            const int s = s_items[b0 + bi];
-            const bool shared = s == MS;
+    const int slab = (DN_ROWS * rbmax + 1023) & ~1023;
+    uint8_t *wbuf = (uint8_t *)s_dyn, *abuf = wbuf + slab;
+    const int cpr = F / 8;  // 16-byte chunks per staged plane row
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        const int it = item / dblocks, d0 = (item - it * dblocks) * DN_ROWS;
+        const int sidx = s_items[it];
+        const bool shared = sidx == MS;
+        const int rb = (int)(shared ? A.sh_rb : A.rb);
+        if (wave == 0) {
             int n;
             if (shared) {
                 n = A.nt;
-                if (lane < A.nt) s_list[wave][lane] = MS + lane;
+                if (lane < A.nt) s_list[lane] = MS + lane;
             } else {
-                const int e = s_ids[s];
+                const int e = s_ids[sidx];
                 n = 0;
                 for (int c0 = 0; c0 < ns; c0 += 64) {
                     const int q = c0 + lane;
                     const bool m = q < ns && s_ids[q] == e && s_flag[q / QG_TOP] < 2;
                     const unsigned long long b = __ballot(m);
                     const int pos = n + __popcll(b & ((1ULL << lane) - 1ULL));
-                    if (m && pos < MB) s_list[wave][pos] = q;  // a token lists an expert at most once
+                    if (m && pos < MB) s_list[pos] = q;  // a token lists an expert at most once
                     n += __popcll(b);
                 }
                 n = min(n, MB);
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int rb = (int)(shared ? A.sh_rb : A.rb);
-            const uint8_t *W = wbuf + (size_t)bi * slab;
-            for (int c = 0; 8 * c < n; c++) {
-                const int arow = s_list[wave][min(8 * c + (j >> 1), n - 1)];
-                int oslot[2];
+            if (lane == 0) s_n = n;
+        }
+        // the item's weight slab: 64 consecutive rows, one flat copy
+        {
+            const uint8_t *W = shared ? A.sh_down + (size_t)d0 * rb : A.down + ((size_t)s_ids[sidx] * A.D + d0) * rb;
+            const int nch = DN_ROWS * rb / 16;
+            for (int q = wave; q * 64 < nch; q += 4) {
+                int c = q * 64 + lane;
+                if (c >= nch) c = 0;  // lanes past the slab copy its first chunk into unused space
+                dma16(W + 16 * (size_t)c, wbuf + (size_t)q * 1024);
+            }
+        }
+        __syncthreads();  // s_list / s_n
+        const int n = s_n;
+        const uint8_t *wr = wbuf + (size_t)(16 * wave + j) * rb;
+        for (int c0 = 0; c0 < n; c0 += 8) {
+            // 16 plane rows (8 tokens x {hi, lo}) of mid, swizzled
+            for (int q = wave; q * 64 < 16 * cpr; q += 4) {
+                const int C = q * 64 + lane, r = C / cpr, pos = C - r * cpr;
+                const int sl = s_list[min(c0 + (r >> 1), n - 1)];
+                dma16(A.midp + ((size_t)sl * 2 + (r & 1)) * F + (size_t)(pos ^ (r & 15)) * 8, abuf + (size_t)q * 1024);
+            }
+            wait_vmem();
+            __syncthreads();
+            int oslot[2];
 #pragma unroll
-                for (int t2 = 0; t2 < 2; t2++) oslot[t2] = s_list[wave][min(8 * c + 2 * kq + t2, n - 1)];
-                const qg_f4 y = shared ? down_tile<SFMT, NB>(A, W, rb, j, kq, arow, oslot) : down_tile<FMT, NB>(A, W, rb, j, kq, arow, oslot);
+            for (int t2 = 0; t2 < 2; t2++) oslot[t2] = s_list[min(c0 + 2 * kq + t2, n - 1)];
+            const qg_f4 y = shared ? dn_tile<SFMT>(wr, abuf, F, j, kq, A.msum8, oslot) : dn_tile<FMT>(wr, abuf, F, j, kq, A.msum8, oslot);
 #pragma unroll
-                for (int t2 = 0; t2 < 2; t2++) {
-                    const int idx = 8 * c + 2 * kq + t2;
-                    if (idx < n && j < DN_ROWS) {
-                        const int sl = oslot[t2];
-                        const float v = y[2 * t2] + y[2 * t2 + 1];
-                        s_val[sl][j] = shared ? v : v * A.w[sl];
-                    }
+            for (int t2 = 0; t2 < 2; t2++) {
+                const int idx = c0 + 2 * kq + t2;
+                if (idx < n) {
+                    const int sl = oslot[t2];
+                    const float v = y[2 * t2] + y[2 * t2 + 1];
+                    A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * A.w[sl];
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            __syncthreads();  // the stage is rewritten by the next tile
         }
-        __syncthreads();  // the slabs are overwritten by the next batch
+        __syncthreads();  // s_list, s_n and the slab are rewritten by the next item
     }
-    for (int i = tid; i < A.nt * DN_ROWS; i += DN_WAVES * 64) {
-        const int t = i / DN_ROWS, r = i % DN_ROWS;
-        float acc = 0.0f;
-        if (s_flag[t] < 2) {
+}
+
+// ---------------- K4: router-rank combine + shared + residual ----------------
+struct CombArgs {
+    int nt, D;
+    const int *ids; const TokRoute *tr;
+    const float *slots;
+    const float *sh_logit; int ld; int has_shared;
+    float *out, *resid;
+    qg_prune_stats *stats;               // accumulated by block (0, 0) when pruning is active
+};
+
+// out[t] = sum over ranks k of the weighted slots (cpu.c:257-259 order), then
+// + y_sh * sigmoid(logit) (gpu.cu:552-553), then the optional residual add;
+// flag >= 2 rows are 0.
+__global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
+    const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d < A.D) {
+        // every load is independent of the others (slot addresses do not depend
+        // on the ids): one memory round trip; invalid selections are selected away
+        const int flag = A.tr->flag[t];
+        int e[QG_TOP];
+        float4 v[QG_TOP];
+#pragma unroll
+        for (int k = 0; k < QG_TOP; k++) {
+            e[k] = A.ids[t * QG_TOP + k];
+            v[k] = *(const float4 *)(A.slots + (size_t)(t * QG_TOP + k) * A.D + d);
+        }
+        float4 vs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float lg = 0.0f;
+        if (A.has_shared) {
+            vs = *(const float4 *)(A.slots + (size_t)(MS + t) * A.D + d);
+            lg = A.sh_logit[(size_t)t * A.ld];
+        }
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (flag < 2) {
 #pragma unroll
             for (int k = 0; k < QG_TOP; k++) {
-                const int sl = t * QG_TOP + k, e = s_ids[sl];
-                acc += (e >= 0 && e < QG_EXPERTS) ? s_val[sl][r] : 0.0f;
+                const bool ok = e[k] >= 0 && e[k] < QG_EXPERTS;
+                acc.x += ok ? v[k].x : 0.0f;
+                acc.y += ok ? v[k].y : 0.0f;
+                acc.z += ok ? v[k].z : 0.0f;
+                acc.w += ok ? v[k].w : 0.0f;
             }
-            if (has_shared) acc = __builtin_fmaf(s_val[MS + t][r], qg_sig(A.sh_logit[(size_t)t * A.ld]), acc);
+            if (A.has_shared) {
+                const float sg = qg_sig(lg);
+                acc.x = __builtin_fmaf(vs.x, sg, acc.x);
+                acc.y = __builtin_fmaf(vs.y, sg, acc.y);
+                acc.z = __builtin_fmaf(vs.z, sg, acc.z);
+                acc.w = __builtin_fmaf(vs.w, sg, acc.w);
+            }
         }
-        const size_t o = (size_t)t * A.D + r0 + r;
-        if (A.out) A.out[o] = acc;
-        if (A.resid) A.resid[o] = A.resid[o] + acc;
+        const size_t o = (size_t)t * A.D + d;
+        if (A.out) *(float4 *)(A.out + o) = acc;
+        if (A.resid) {
+            float4 h = *(float4 *)(A.resid + o);
+            h.x += acc.x; h.y += acc.y; h.z += acc.z; h.w += acc.w;
+            *(float4 *)(A.resid + o) = h;
+        }
     }
-    if (A.stats && blockIdx.x == 0 && tid == 0) {
+    if (A.stats && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
         // counters in token order (deterministic, unlike the reference's atomics)
-        for (int t = 0; t < A.nt; t++) {
-            const int f = A.tr->flag[t];
+        for (int u = 0; u < A.nt; u++) {
+            const int f = A.tr->flag[u];
             if (f == 3) continue;
             A.stats->token_layers += 1;
-            A.stats->missing_selections += (uint64_t)A.tr->missing[t];
+            A.stats->missing_selections += (uint64_t)A.tr->missing[u];
             if (f == 1) {
-                A.stats->skipped_selections += (uint64_t)A.tr->missing[t];
+                A.stats->skipped_selections += (uint64_t)A.tr->missing[u];
                 A.stats->avoided_token_handoffs += 1;
-                A.stats->skipped_mass += A.tr->mass[t];
+                A.stats->skipped_mass += A.tr->mass[u];
             }
         }
     }
@@ -625,13 +709,12 @@ bool dec_ok(const qg_moe_layer *L) {
     return true;
 }
 
-template <int NB>
 void launch_down(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStream_t s) {
-    const dim3 block(DN_WAVES * 64);
-    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_IQ4_NL, NB>, grid, block, lds, s, DA);
-    else if (fr == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_Q4_K, NB>, grid, block, lds, s, DA);
-    else if (fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_Q4_K, QT_IQ4_NL, NB>, grid, block, lds, s, DA);
-    else dec_launch(3, dec_down_kernel<QT_Q4_K, QT_Q4_K, NB>, grid, block, lds, s, DA);
+    const dim3 block(256);
+    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_IQ4_NL>, grid, block, lds, s, DA);
+    else if (fr == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_Q4_K>, grid, block, lds, s, DA);
+    else if (fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_Q4_K, QT_IQ4_NL>, grid, block, lds, s, DA);
+    else dec_launch(3, dec_down_kernel<QT_Q4_K, QT_Q4_K>, grid, block, lds, s, DA);
 }
 
 int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
@@ -648,7 +731,11 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const int row_pairs = (rows + 1) / 2;
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_pairs,
                  L->router_bias};
-    dec_launch(0, dec_router_kernel, dim3(row_pairs + 1, (nt + 3) / 4), dim3(256), 0, s, R);
+    const dim3 rgrid(row_pairs + (nt + 3) / 4);
+    if (nt <= 4) dec_launch(0, dec_router_kernel<1>, rgrid, dim3(256), 0, s, R);
+    else if (nt <= 8) dec_launch(0, dec_router_kernel<2>, rgrid, dim3(256), 0, s, R);
+    else if (nt <= 12) dec_launch(0, dec_router_kernel<3>, rgrid, dim3(256), 0, s, R);
+    else dec_launch(0, dec_router_kernel<5>, rgrid, dim3(256), 0, s, R);
     int rc = hipGetLastError();
     if (rc) return rc;
     const bool inl = nt <= INLINE_MAX;
@@ -676,14 +763,20 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     else dec_launch(2, dec_gateup_kernel<10>, dim3(nwg), dim3(256), act_lds, s, G2);
     if ((rc = hipGetLastError())) return rc;
     const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;
-    DnArgs DA{nt, D, F, ids, weights, tr, (L->resident && stats) ? stats : nullptr,
-              (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb, midp, msum8,
-              logits + QG_EXPERTS, rows, out, resid};
-    const size_t lds = DN_LDS;
+    float *slots = (float *)(ws + lay.slots);
+    DnArgs DA{nt, D, F, ids, weights, tr, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
+              midp, msum8, slots};
+    const size_t rbmax = rb > srb ? rb : srb;
+    const size_t dn_lds = ((DN_ROWS * rbmax + 1023) & ~(size_t)1023) + (size_t)16 * F * 2;
     const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
-    const dim3 grid(D / DN_ROWS);
-    if (F == 512) launch_down<16>(DA, fr, fs, grid, lds, s);
-    else launch_down<20>(DA, fr, fs, grid, lds, s);
+    // upper bound of the items: every selection its own expert, plus the shared expert
+    const int owners = (nt * QG_TOP < QG_EXPERTS ? nt * QG_TOP : QG_EXPERTS) + (sh ? 1 : 0);
+    const int dn_items = owners * (D / DN_ROWS);
+    launch_down(DA, fr, fs, dim3(dn_items < DN_WGS ? dn_items : DN_WGS), dn_lds, s);
+    if ((rc = hipGetLastError())) return rc;
+    CombArgs CA{nt, D, ids, tr, slots, logits + QG_EXPERTS, rows, sh ? 1 : 0, out, resid,
+                (L->resident && stats) ? stats : nullptr};
+    dec_launch(4, dec_combine_kernel, dim3((D / 4 + 255) / 256, nt), dim3(256), 0, s, CA);
     return hipGetLastError();
 }
 

@@ -958,7 +958,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     CombArgs CA{nt, D, ids, weights, flag, slots, sh ? logits + QG_EXPERTS : nullptr, rows, out, resid};
     pf_launch(9, pf_combine_kernel, dim3((D / 4 + 255) / 256, nt), dim3(256), 0, s, CA);
     if ((rc = hipGetLastError())) return rc;
-    if (stats) {
+    if (stats && L->resident) {  // counters exist only with a resident mask (gpu.cu:484-488)
         pf_stats_kernel<<<1, 1024, 0, s>>>(stats, flag, (const int *)(ws + lay.missing), (const double *)(ws + lay.mass), nt);
         if ((rc = hipGetLastError())) return rc;
     }

@@ -365,6 +365,48 @@ def test_layer_partial_residency_flags(layer1, nt):
         L.desc = saved
 
 
+@pytest.mark.parametrize("nt", [4, 17])
+def test_layer_partial_residency_mixed_flags(layer1, nt):
+    """Residency with the 16 experts of largest routed mass over the batch
+    itself: the batch mixes covered (0), pruned (1) and handoff (2) tokens, so
+    the pruned computation is checked against the oracle row by row."""
+    L, H = layer1
+    x = synth.inputs(77, nt, 2048, correlated=True)
+    ids, w = O.route(H.logits(x))
+    score = np.zeros(512)
+    np.add.at(score, ids.ravel(), w.ravel().astype(np.float64))
+    resident = np.zeros(512, np.uint8)
+    resident[np.lexsort((np.arange(512), -score))[:16]] = 1
+    desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    rdev = Device(resident)
+    desc.resident, desc.threshold = rdev.p, 0.10
+    saved = L.desc
+    L.desc = desc
+    try:
+        fw = synth.Forward(2048, 512, nt)
+        call("zero", fw.stats.p, fw.stats.nbytes)
+        fw.x.set(x)
+        say(f"forward mixed residency nt={nt}")
+        fw.run(L, nt)
+        qg.call("sync")
+        out, oids, ow, _, flags, st = H.forward(x, resident)
+        counts = np.bincount(flags, minlength=4)
+        assert counts[0] > 0 and counts[1] > 0 and counts[2] > 0, counts
+        np.testing.assert_array_equal(fw.ids.get()[:nt], oids)
+        np.testing.assert_array_equal(fw.w.get()[:nt].view('u4'), ow.view('u4'))
+        np.testing.assert_array_equal(fw.flags.get()[:nt], flags)
+        keep = flags < 2
+        maxabs, rel = assert_close(fw.out.get()[:nt][keep], out[keep], f"mixed residency B={nt}")
+        assert np.all(fw.out.get()[:nt][~keep] == 0)
+        gst = qg.PruneStats.from_buffer_copy(fw.stats.get())
+        assert (gst.token_layers, gst.missing_selections, gst.skipped_selections, gst.avoided_token_handoffs) == \
+               (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs)
+        assert gst.skipped_mass == st.skipped_mass
+        say(f"  flags {counts}, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
+    finally:
+        L.desc = saved
+
+
 @pytest.mark.parametrize("nt", [2, 8])
 def test_layer_graph_replay(layer1, nt):
     """The fused layer captured into a graph and replayed, with eager work in
