@@ -104,6 +104,14 @@ QG_DEV float qg_expf(float x) { return (float)qg_exp_d((double)x); }
 QG_DEV float qg_sig(float a) { return 1.0f / (1.0f + qg_expf(-a)); }
 // SwiGLU as cpu.c:216 writes it: (g*(1/(1+exp(-g))))*u.
 QG_DEV float qg_swiglu(float g, float u) { return (g * (1.0f / (1.0f + qg_expf(-g)))) * u; }
+// The same with the hardware base-2 exponential and reciprocal (about 1 ulp
+// each) for the matrix-core kernels, whose outputs are held to a tolerance
+// (the routing weights, which must match exactly, keep qg_expf); a few
+// registers instead of the double-precision polynomial's constants.
+QG_DEV float qg_swiglu_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
 
 // ---- cross-lane helpers (wave64) ----
 // Pairwise tree over 32-lane halves with strides 16,8,4,2,1: lane 0 (and 32)
@@ -239,15 +247,15 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     int c = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) c += v[i] >= T;
-    int incl = c;  // inclusive prefix sum of c over lanes
+    // exclusive prefix sum of c (0..8) over the lanes from bit-sliced ballots
+    int pos = 0, total_c = 0;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
+    for (int bit = 0; bit < 4; bit++) {
+        const unsigned long long b = __ballot((c >> bit) & 1);
+        pos += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u)) << bit;
+        total_c += __popcll(b) << bit;
     }
-    const int total_c = __shfl(incl, 63);
     if (total_c > 64) { qg_route_lane(s, lane, id_out, w_out); return; }
-    int pos = incl - c;
 #pragma unroll
     for (int i = 0; i < 8; i++)
         if (v[i] >= T) { lds_v[pos] = v[i]; lds_i[pos] = lane + 64 * i; pos++; }
@@ -258,9 +266,9 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     const float cv = lane < total_c ? lds_v[lane] : 0.0f;
     const int ci = lane < total_c ? lds_i[lane] : 0;
     int rank = 0;
-    for (int q = 0; q < total_c; q++) {
-        const float ov = lds_v[q];
-        const int oi = lds_i[q];
+    for (int q = 0; q < total_c; q++) {  // candidate q from its lane's registers (wave-uniform q)
+        const float ov = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), q));
+        const int oi = __builtin_amdgcn_readlane(ci, q);
         rank += (ov > cv) | ((ov == cv) & (oi < ci));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -273,7 +281,7 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     const float num = lane < QG_TOP ? qg_expf(lds_v[lane] - largest) : 0.0f;
     float total = 0.0f;
 #pragma unroll
-    for (int k = 0; k < QG_TOP; k++) total += __shfl(num, k);
+    for (int k = 0; k < QG_TOP; k++) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), k));
     if (lane < QG_TOP) { id_out = lds_i[lane]; w_out = num / total; }
 }
 
@@ -294,17 +302,19 @@ QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane, float *l
 // 2 (handoff: missing > 0 and !(mass < threshold)) or 3 (an id outside
 // [0,512): uncounted).  resident == NULL means every expert is resident.
 QG_DEV int qg_route_cover(int &id, float &wv, const uint8_t *resident, double thr, int &missing, double &mass) {
-    missing = 0;
+    const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const bool mine = lane < QG_TOP, valid = id >= 0 && id < QG_EXPERTS;
+    // one residency lookup per lane, all in flight together
+    const bool nonres = mine && valid && resident && !resident[id];
+    const unsigned long long nb = __ballot(nonres);
+    const bool bad = __ballot(mine && !valid) != 0;
+    missing = __popcll(nb);
     mass = 0.0;
-    int bad = 0;
-    for (int k = 0; k < QG_TOP; k++) {
-        const int ek = __shfl(id, k);
-        const float wk = __shfl(wv, k);
-        if (ek < 0 || ek >= QG_EXPERTS) { bad = 1; break; }
-        if (resident && !resident[ek]) { missing++; mass += (double)wk; }
-    }
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++)
+        if ((nb >> k) & 1) mass += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), k));
     const int flag = bad ? 3 : !missing ? 0 : (thr > 0 && mass < thr) ? 1 : 2;
-    if (flag == 1 && id >= 0 && id < QG_EXPERTS && !resident[id]) { id = -id - 2; wv = 0.0f; }
+    if (flag == 1 && nonres) { id = -id - 2; wv = 0.0f; }
     return flag;
 }
 
@@ -330,15 +340,19 @@ QG_DEV uint32_t iq4_lookup(uint32_t idx) {
 }
 
 // 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,
-// element order (0,2),(1,3),(4,6),(5,7).  Each nibble is masked to a byte, a
-// byte permute puts it under the exponent byte 0x64 (fp16 1024 + q), and
-// (1024+q)*s - 1024*s is exact.
+// element order (0,2),(1,3),(4,6),(5,7).  Each nibble is masked in place under
+// the exponent byte 0x64: a low nibble q reads as fp16 1024 + q, a high one as
+// 1024 + 16q, and (1024+q)*s - 1024*s, (1024+16q)*(s/16) - 64*s are both q*s,
+// exact (q*s <= 945; one rounding in the fused multiply-add).
 QG_DEV qg_half8 q4_frag(uint2 b, int hi_nib, _Float16 s) {
-    const uint32_t n0 = (hi_nib ? b.x >> 4 : b.x) & 0x0F0F0F0Fu, n1 = (hi_nib ? b.y >> 4 : b.y) & 0x0F0F0F0Fu;
-    const uint32_t M = 0x64646464u;  // permute selectors 4 pick these bytes
-    const uint32_t u[4] = {__builtin_amdgcn_perm(M, n0, 0x04020400u), __builtin_amdgcn_perm(M, n0, 0x04030401u),
-                           __builtin_amdgcn_perm(M, n1, 0x04020400u), __builtin_amdgcn_perm(M, n1, 0x04030401u)};
-    const qg_half2 sv = {s, s}, off = {(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
+    // E as an opaque register value lets each mask-and-insert be one v_and_or_b32
+    // (a VOP3 instruction takes at most one literal or scalar operand here)
+    uint32_t E;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(E));
+    const uint32_t m = hi_nib ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t u[4] = {(b.x & m) | E, ((b.x >> 8) & m) | E, (b.y & m) | E, ((b.y >> 8) & m) | E};
+    const _Float16 sc = hi_nib ? s * (_Float16)0.0625f : s, of = hi_nib ? (_Float16)(-64.0f) * s : (_Float16)(-1024.0f) * s;
+    const qg_half2 sv = {sc, sc}, off = {of, of};
     qg_half8 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -382,3 +396,23 @@ QG_DEV Q4kHeader q4k_header(uint4 hd) {
 }
 QG_DEV int q4k_s(const Q4kHeader &h, int g) { return (h.S[g >> 2] >> (8 * (g & 3))) & 0xff; }
 QG_DEV int q4k_m(const Q4kHeader &h, int g) { return (h.M[g >> 2] >> (8 * (g & 3))) & 0xff; }
+// The 8 mins m_0..m_7 of a superblock as an fp16 fragment in group order: a
+// byte permute puts each 6-bit value under the exponent byte 0x64 (1024 + m),
+// one packed add removes the 1024.
+QG_DEV qg_half8 q4k_min_frag(const Q4kHeader &h) {
+    const uint32_t X = 0x64646464u;
+    const uint32_t u[4] = {__builtin_amdgcn_perm(X, h.M[0], 0x04010400u), __builtin_amdgcn_perm(X, h.M[0], 0x04030402u),
+                           __builtin_amdgcn_perm(X, h.M[1], 0x04010400u), __builtin_amdgcn_perm(X, h.M[1], 0x04030402u)};
+    const qg_half2 off = {(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+    qg_half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+// the same 6-bit values as fp16 (one integer-to-half conversion)
+QG_DEV _Float16 q4k_sh(const Q4kHeader &h, int g) { return (_Float16)(unsigned short)q4k_s(h, g); }
+QG_DEV _Float16 q4k_mh(const Q4kHeader &h, int g) { return (_Float16)(unsigned short)q4k_m(h, g); }

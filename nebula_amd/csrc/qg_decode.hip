@@ -41,14 +41,29 @@ constexpr int INLINE_MAX = 1;             // tokens routed inside the gate/up ke
 constexpr int GU_WGS = 512;               // gate/up grid cap (workgroups)
 constexpr int DN_WGS = 1024;              // down grid cap (workgroups)
 
-struct TokRoute { int flag[MB]; int missing[MB]; double mass[MB]; };
+// Routing results of the batch and its tile plan, written once per layer by
+// the routing step (the routing kernel, or gate/up workgroup 0 at one token)
+// and read by gate/up, down and combine.  A selection q = t*10 + rank is
+// eligible when its id is an expert (pruned selections carry -id-2) and its
+// token is computed here (flag 0 or 1).  Each expert with eligible selections
+// (in order of its first one) contributes tiles of up to 8 of them in token
+// order (a token lists an expert at most once).  The shared expert's tiles
+// (tokens 8i..8i+7) come first and are implicit.
+constexpr int TILE_TOK = 8;
+constexpr int MAX_TILES = MS;                // at most one tile per selection
+struct DecTile { int e, n, q[TILE_TOK]; };
+struct DecPlan {
+    int flag[MB]; int missing[MB]; double mass[MB];
+    int n_tiles;                             // routed tiles
+    DecTile tile[MAX_TILES];
+};
 
 struct DecLayout { size_t tok, logits, xp, xsum, midp, msum, slots, total; };
 DecLayout dec_layout(int D, int F) {
     DecLayout L;
     size_t off = 0;
     auto take = [&](size_t n) { size_t o = off; off += (n + 255) & ~(size_t)255; return o; };
-    L.tok = take(sizeof(TokRoute));
+    L.tok = take(sizeof(DecPlan));
     L.logits = take((size_t)MB * (QG_EXPERTS + 1) * 4);
     L.xp = take((size_t)MB * 2 * D * 2);
     L.xsum = take((size_t)MB * 2 * (D / 32) * 2);
@@ -123,10 +138,12 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
         sc[u] = A.norm ? row_rms_scale(xr[u], A.D, A.eps, lane) : 1.0f;
         acc[u] = 0.0f;
     }
-    // chunks of CH k-steps; the loads of chunk c+1 are in flight while chunk c's fmas run
-    constexpr int CH = TPW == 1 ? 16 : 8;
+    // chunks of CH k-steps in a ring of NBUF register buffers: the loads of
+    // chunks c+1 .. c+NBUF-1 are in flight while chunk c's fmas run (one token:
+    // the whole row of a 2048-wide layer is requested at once)
+    constexpr int CH = TPW == 1 ? 16 : 8, NBUF = TPW == 1 ? 4 : 2;
     const int nfull = A.D / (32 * CH);
-    float wv[2][CH], xv[2][TPW][CH];
+    float wv[NBUF][CH], xv[NBUF][TPW][CH];
     auto load = [&](int b, int k0) {
 #pragma unroll
         for (int i = 0; i < CH; i++) wv[b][i] = wr[k0 + 32 * i + j];
@@ -135,12 +152,14 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
 #pragma unroll
             for (int i = 0; i < CH; i++) xv[b][u][i] = xr[u][k0 + 32 * i + j];
     };
-    if (nfull > 0) load(0, 0);
-    for (int c = 0; c < nfull; c += 2) {
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
+    for (int b = 0; b < NBUF - 1; b++)
+        if (b < nfull) load(b, b * 32 * CH);
+    for (int c = 0; c < nfull; c += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; b++) {
             if (c + b >= nfull) break;
-            if (c + b + 1 < nfull) load(b ^ 1, (c + b + 1) * 32 * CH);
+            if (c + b + NBUF - 1 < nfull) load((b + NBUF - 1) % NBUF, (c + b + NBUF - 1) * 32 * CH);
 #pragma unroll
             for (int i = 0; i < CH; i++)
 #pragma unroll
@@ -161,29 +180,92 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     }
 }
 
-// ---------------- KR: routing, one wave per token (B > 4) ----------------
+// ---------------- KR: routing and the expert plan (B > 1), one block ----------------
 struct RouteArgs {
     int nt; const float *logits; int ld;
     const uint8_t *resident; double thr;
-    int *ids; float *w; uint8_t *flags_out; TokRoute *tr;
+    int *ids; float *w; uint8_t *flags_out; DecPlan *pl;
 };
 
-__global__ __launch_bounds__(256) void dec_route_kernel(RouteArgs A) {
-    __shared__ float s_rv[4][64];
-    __shared__ int s_ri[4][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + wave;
-    if (t >= A.nt) return;  // the whole wave; this kernel has no block barrier
-    int id, missing;
-    float wv;
-    double mass;
-    qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv[wave], s_ri[wave]);
-    const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
-    if (lane < QG_TOP) { A.ids[t * QG_TOP + lane] = id; A.w[t * QG_TOP + lane] = wv; }
-    if (lane == 0) {
-        A.tr->flag[t] = flag;
-        A.tr->missing[t] = missing;
-        A.tr->mass[t] = mass;
-        if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
+constexpr int RT_WAVES = 16;
+
+// Wave w routes tokens w, w + 16; then the block builds the plan: each
+// expert's first eligible selection and eligible count (shared-memory
+// atomics), the experts in selection order with the prefix of their tile
+// counts (wave 0), and each expert's tiles (one wave per expert).
+__global__ __launch_bounds__(1024) void dec_route_kernel(RouteArgs A) {
+    __shared__ float s_rv[RT_WAVES][64];
+    __shared__ int s_ri[RT_WAVES][64];
+    __shared__ int s_ids[MS], s_flag[MB], s_first[QG_EXPERTS], s_cnt[QG_EXPERTS], s_own[MS], s_tbase[MS];
+    __shared__ int s_nown;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ns = A.nt * QG_TOP;
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    for (int i = tid; i < QG_EXPERTS; i += 64 * RT_WAVES) { s_first[i] = 0x7fffffff; s_cnt[i] = 0; }
+    for (int t = wave; t < A.nt; t += RT_WAVES) {
+        int id, missing;
+        float wv;
+        double mass;
+        qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv[wave], s_ri[wave]);
+        const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+        if (lane < QG_TOP) {
+            A.ids[t * QG_TOP + lane] = id;
+            A.w[t * QG_TOP + lane] = wv;
+            s_ids[t * QG_TOP + lane] = id;
+        }
+        if (lane == 0) {
+            A.pl->flag[t] = flag;
+            A.pl->missing[t] = missing;
+            A.pl->mass[t] = mass;
+            s_flag[t] = flag;
+            if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < ns; q += 64 * RT_WAVES) {
+        const int e = s_ids[q];
+        if (e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2) {
+            atomicMin(&s_first[e], q);
+            atomicAdd(&s_cnt[e], 1);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // experts in order of their first eligible selection, and the prefix of their tile counts
+        int n = 0, tiles = 0;
+        for (int c0 = 0; c0 < ns; c0 += 64) {
+            const int q = c0 + lane;
+            const int e = q < ns ? s_ids[q] : -1;
+            const bool own = e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2 && s_first[e] == q;
+            const int nt8 = own ? (min(s_cnt[e], MB) + TILE_TOK - 1) / TILE_TOK : 0;  // 0..3
+            const unsigned long long b = __ballot(own), b0 = __ballot(nt8 & 1), b1 = __ballot(nt8 & 2);
+            if (own) {
+                const int k = n + __popcll(b & below);
+                s_own[k] = q;
+                s_tbase[k] = tiles + __popcll(b0 & below) + 2 * __popcll(b1 & below);
+            }
+            n += __popcll(b);
+            tiles += __popcll(b0) + 2 * __popcll(b1);
+        }
+        if (lane == 0) { s_nown = n; A.pl->n_tiles = tiles; }
+    }
+    __syncthreads();
+    // one wave per expert: its eligible selections in token order, 8 per tile
+    for (int k = wave; k < s_nown; k += RT_WAVES) {
+        const int e = s_ids[s_own[k]], tb = s_tbase[k];
+        int n = 0;
+        for (int c0 = 0; c0 < ns; c0 += 64) {
+            const int q = c0 + lane;
+            const bool m = q < ns && s_ids[q] == e && s_flag[q / QG_TOP] < 2;
+            const unsigned long long b = __ballot(m);
+            const int pos = n + __popcll(b & below);
+            if (m && pos < MB) A.pl->tile[tb + pos / TILE_TOK].q[pos % TILE_TOK] = q;
+            n += __popcll(b);
+        }
+        n = min(n, MB);
+        if (lane < (n + TILE_TOK - 1) / TILE_TOK) {
+            A.pl->tile[tb + lane].e = e;
+            A.pl->tile[tb + lane].n = min(TILE_TOK, n - TILE_TOK * lane);
+        }
     }
 }
 
@@ -191,152 +273,129 @@ __global__ __launch_bounds__(256) void dec_route_kernel(RouteArgs A) {
 struct GuArgs {
     int nt, D, F;
     int inline_route; const float *logits; int ld; const uint8_t *resident; double thr;
-    int *ids; float *w; uint8_t *flags_out; TokRoute *tr;
+    int *ids; float *w; uint8_t *flags_out; DecPlan *pl;
     const uint8_t *gate, *up, *sh_gate, *sh_up; size_t rb;
     const _Float16 *xp, *xsp;
     _Float16 *midp; float *msum8;    // mid planes [ME][2][F] in the down format's order; sums of 8 rows [ME][F/8]
     int fmt, sh_fmt;                 // down formats of the routed and shared experts
-    int tt;                          // tokens per tile (8)
 };
 
 constexpr int GU_ROWS = 8;           // F rows of gate and of up per wave
 constexpr int GU_WROWS = 4 * GU_ROWS; // F rows per workgroup (4 waves)
 
-// Workgroup = 4 waves, persistent over work items.  Item = (expert, tile of
-// tt <= 8 of its tokens, 32 F rows): the shared expert's items first (no routing
-// needed), then the routed experts in order of their owning selection (the
-// expert's first eligible selection).  The tile's activation planes (real
-// tokens only) are staged in shared memory while every wave loads its weight
-// rows into registers; MFMA A fragments are then shared-memory reads.  In a
-// wave, MFMA columns 0..7 are 8 gate rows and 8..15 the same 8 up rows, so
-// lane l and lane l^8 hold gate and up of one (row, token) pair.
-template <int NSB>
+// Shared-memory layout of the gate/up kernel (fp16 units): 16 staged plane
+// rows (8 tokens x {hi, lo}) of D values each padded by 8, 16 rows of D/32
+// group sums each padded by 8, then per wave 16 rows of NSB Q4_K headers (16
+// bytes each) padded by one header.  The padding puts the 16 rows of every
+// fragment read in distinct banks while each read keeps a constant offset.
+// Copies into it are direct global->shared with the lanes of padding slots
+// masked off.
+struct GuLds { int arow, srow, hrow, sums, hdr, hdr_wave, total; };  // strides and offsets in fp16 units
+static __host__ __device__ inline GuLds gu_lds(int D) {
+    GuLds L;
+    L.arow = D + 8;
+    L.srow = D / 32 + 8;
+    L.hrow = 8 * (D / 256 + 1);
+    L.sums = 16 * L.arow;
+    L.hdr = L.sums + 16 * L.srow;
+    L.hdr_wave = 16 * L.hrow;
+    L.total = L.hdr + 4 * L.hdr_wave;
+    return L;
+}
+
+// Persistent; item = (tile, 32 F rows): the shared expert's tiles first (no
+// routing needed), then the plan's routed tiles.  The item's weight rows go to
+// registers (8 gate and the same 8 up rows per wave) and their headers to
+// shared memory, while the tile's activation planes and sum planes are staged
+// by direct global->shared copies; then the products on the matrix cores.  In
+// a wave, MFMA columns 0..7 are the gate rows and 8..15 the up rows, so lanes
+// l and l^8 hold gate and up of one (row, token) pair.  Tiles of one expert
+// and row block are items rblocks apart, on workgroups of one XCD, so their
+// repeated weight reads meet in that XCD's L2.
+template <int NSB, bool INL>
 __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
-    // dynamic shared memory: [tt tokens][2 planes][D] fp16 activations, the
-    // tokens' [2][D/32] sum planes (rounded up to 1 KB), then per wave the
-    // 16 rows x NSB Q4_K superblock headers (16 B each)
-    extern __shared__ uint4 s_act[];
-    // planning scratch shares the staging buffer (planning precedes any staging
-    // of the same item, and every item ends with a barrier)
-    int *s_first = (int *)s_act, *s_cnt = s_first + QG_EXPERTS;
-    float *s_rv = (float *)(s_cnt + QG_EXPERTS);
-    int *s_ri = (int *)(s_rv + 64);
-    __shared__ int s_nown;
-    __shared__ int s_ids[MS];
-    __shared__ int s_flag[MB];
-    __shared__ int s_owner[MS];      // owning selection of routed expert k
-    __shared__ int s_tbase[MS + 1];  // first tile of routed expert k (prefix over owners)
-    __shared__ int s_slot[MB];
-    __shared__ int s_item[3];        // expert (-1 shared), list length n, tile
+    extern __shared__ uint4 s_dyn[];
+    __shared__ int s_item[2];        // expert (-1: shared), token count (-1: no more items)
+    __shared__ int s_list[MB];       // the item's selections (shared expert: MS + t)
+    __shared__ float s_rv[64];
+    __shared__ int s_ri[64];
+    __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
+    __shared__ int s_nent;
+    __shared__ uint4 s_zero[NSB];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    const int ns = A.nt * QG_TOP, rblocks = A.F / GU_WROWS, D = A.D, D32 = A.D / 32;
-    const int TT = A.tt, sh_tiles = A.sh_gate ? (A.nt + TT - 1) / TT : 0;
-    _Float16 *act = (_Float16 *)s_act;
-    _Float16 *acts = act + TT * 2 * D;
-    uint8_t *hbuf = (uint8_t *)acts + (((size_t)TT * 2 * D32 * 2 + 1023) & ~(size_t)1023) + (size_t)wave * 16 * NSB * 16;
-    bool planned = false;
-    for (int item = blockIdx.x;; item += gridDim.x) {
-        const int tile_g = item / rblocks, rb0 = item % rblocks;
-        if (tile_g >= sh_tiles && !planned) {
-            // routing of this batch (inline for one token, else from the routing kernel)
-            if (A.inline_route) {
-                if (wave == 0) {
-                    int id, missing;
-                    float wv;
-                    double mass;
-                    qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri);
-                    const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
-                    if (lane < QG_TOP) s_ids[lane] = id;
-                    if (lane == 0) s_flag[0] = flag;
-                    if (blockIdx.x == 0) {
-                        if (lane < QG_TOP) { A.ids[lane] = id; A.w[lane] = wv; }
-                        if (lane == 0) {
-                            A.tr->flag[0] = flag;
-                            A.tr->missing[0] = missing;
-                            A.tr->mass[0] = mass;
-                            if (A.flags_out) A.flags_out[0] = (uint8_t)flag;
-                        }
-                    }
-                }
-            } else {
-                for (int i = tid; i < ns; i += 256) s_ids[i] = A.ids[i];
-                if (tid < A.nt) s_flag[tid] = A.tr->flag[tid];
-            }
-            for (int i = tid; i < QG_EXPERTS; i += 256) { s_first[i] = 0x7fffffff; s_cnt[i] = 0; }
-            __syncthreads();
-            for (int i = tid; i < ns; i += 256) {
-                const int e = s_ids[i];
-                if (e >= 0 && e < QG_EXPERTS && s_flag[i / QG_TOP] < 2) { atomicMin(&s_first[e], i); atomicAdd(&s_cnt[e], 1); }
-            }
-            __syncthreads();
-            if (wave == 0) {
-                int n = 0, tiles = 0;
-                for (int c0 = 0; c0 < ns; c0 += 64) {
-                    const int q = c0 + lane;
-                    const int e = q < ns ? s_ids[q] : -1;
-                    const bool own = e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2 && s_first[e] == q;
-                    const int nt8 = own ? (min(s_cnt[e], MB) + TT - 1) / TT : 0;
-                    int incl = nt8;
-#pragma unroll
-                    for (int d = 1; d < 64; d <<= 1) {
-                        const int o = __shfl_up(incl, d);
-                        if (lane >= d) incl += o;
-                    }
-                    const unsigned long long b = __ballot(own);
-                    if (own) {
-                        const int k = n + __popcll(b & ((1ULL << lane) - 1ULL));
-                        s_owner[k] = q;
-                        s_tbase[k] = tiles + incl - nt8;
-                    }
-                    n += __popcll(b);
-                    tiles += __shfl(incl, 63);
-                }
-                if (lane == 0) { s_tbase[n] = tiles; s_nown = n; }
-            }
-            __syncthreads();
-            planned = true;
-        }
-        // item -> expert, token list, tile (wave 0), shared with the other waves
+    const int D = A.D, D32 = D / 32, cps = D / 256, bpr = D / 512;
+    if (tid < NSB) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first barrier
+    const int rblocks = A.F / GU_WROWS, sh = A.sh_gate ? 1 : 0;
+    constexpr int HROW = NSB + 1;    // header slots per padded row
+    const GuLds LY = gu_lds(D);
+    _Float16 *act = (_Float16 *)s_dyn;
+    _Float16 *acts = act + LY.sums;
+    uint8_t *hbuf = (uint8_t *)(act + LY.hdr + wave * LY.hdr_wave);
+    if (INL) {
+        // one token: every workgroup routes it (wave 0); workgroup 0 publishes
+        // the results and the plan (entry k = k-th eligible rank)
         if (wave == 0) {
-            int e = -1, n, tile = tile_g;
-            bool done = false;
-            if (tile_g >= sh_tiles) {
-                const int n_owner = s_nown, rt = tile_g - sh_tiles;
-                if (rt >= s_tbase[n_owner]) done = true;
-                else {
-                    int k = 0;
-                    while (s_tbase[k + 1] <= rt) k++;
-                    e = s_ids[s_owner[k]];
-                    tile = rt - s_tbase[k];
+            int id, missing;
+            float wv;
+            double mass;
+            qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri);
+            const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+            const bool el = lane < QG_TOP && flag < 2 && id >= 0 && id < QG_EXPERTS;
+            const unsigned long long b = __ballot(el);
+            const int k = __popcll(b & ((1ULL << lane) - 1ULL));
+            if (el) { s_rank[k] = lane; s_rid[k] = id; }
+            if (lane == 0) s_nent = __popcll(b);
+            if (blockIdx.x == 0) {
+                if (lane < QG_TOP) { A.ids[lane] = id; A.w[lane] = wv; }
+                if (el) { A.pl->tile[k].e = id; A.pl->tile[k].n = 1; A.pl->tile[k].q[0] = lane; }
+                if (lane == 0) {
+                    A.pl->flag[0] = flag;
+                    A.pl->missing[0] = missing;
+                    A.pl->mass[0] = mass;
+                    A.pl->n_tiles = __popcll(b);
+                    if (A.flags_out) A.flags_out[0] = (uint8_t)flag;
                 }
             }
-            if (done) n = -1;
-            else if (e < 0) {
-                n = A.nt;
-                if (lane < A.nt) s_slot[lane] = MS + lane;
-            } else {
-                n = 0;
-                for (int c0 = 0; c0 < ns; c0 += 64) {
-                    const int q = c0 + lane;
-                    const bool m = q < ns && s_ids[q] == e && s_flag[q / QG_TOP] < 2;
-                    const unsigned long long b = __ballot(m);
-                    const int pos = n + __popcll(b & ((1ULL << lane) - 1ULL));
-                    if (m && pos < MB) s_slot[pos] = q;  // a token lists an expert at most once
-                    n += __popcll(b);
-                }
-                n = min(n, MB);
-            }
-            if (lane == 0) { s_item[0] = e; s_item[1] = n; s_item[2] = tile; }
         }
         __syncthreads();
-        const int e = s_item[0], n = s_item[1], tile = s_item[2];
-        if (n < 0) break;  // block-uniform
+    }
+    const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    for (int item = blockIdx.x;; item += gridDim.x) {
+        const int T = item / rblocks, rb0 = item - T * rblocks;
+        if (wave == 0) {
+            int e = -1, n = -1;
+            if (T < sh_tiles) {
+                n = min(TILE_TOK, A.nt - TILE_TOK * T);
+                if (lane < n) s_list[lane] = MS + TILE_TOK * T + lane;
+            } else if (INL) {
+                const int k = T - sh_tiles;
+                if (k < s_nent) {
+                    e = s_rid[k];
+                    n = 1;
+                    if (lane == 0) s_list[0] = s_rank[k];
+                }
+            } else if (T - sh_tiles < MAX_TILES) {
+                // one round trip: the tile count and the tile are independent loads
+                const int k = T - sh_tiles;
+                const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
+                const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
+                if (k < ntl) {
+                    e = ek;
+                    n = nk;
+                    if (lane < nk) s_list[lane] = qk;
+                }
+            }
+            if (lane == 0) { s_item[0] = e; s_item[1] = n; }
+        }
+        __syncthreads();
+        const int e = s_item[0], n = s_item[1];
+        if (n < 0) break;  // block-uniform; every later item is past the plan too
         const bool shared = e < 0;
-        const int t0 = tile * TT, nl = min(TT, n - t0);
+        const uint8_t *gm = shared ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
+        const uint8_t *um = shared ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
+        const int wrow0 = rb0 * GU_WROWS + wave * GU_ROWS;
         // weight rows of this wave into registers
-        const int row = rb0 * GU_WROWS + wave * GU_ROWS + (j & 7);
-        const uint8_t *mat = j < 8 ? (shared ? A.sh_gate : A.gate) : (shared ? A.sh_up : A.up);
-        const uint8_t *wrow = mat + (shared ? 0 : (size_t)e * A.F * A.rb) + (size_t)row * A.rb;
+        const uint8_t *wrow = (j < 8 ? gm : um) + (size_t)(wrow0 + (j & 7)) * A.rb;
         uint4 c0[NSB], c1[NSB];
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
@@ -345,87 +404,79 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
             c1[sb] = qg_ld16(p + 16 + 16 * (kq + 4));
         }
         // the wave's 16 x NSB superblock headers, straight into shared memory
-        for (int q = 0; q * 64 < 16 * NSB; q++) {
-            int h = q * 64 + lane;
-            if (h >= 16 * NSB) h = 0;  // lanes past the end copy header 0 into unused space
-            const int rr = h / NSB, sb = h - rr * NSB;
-            const uint8_t *hm = rr < 8 ? (shared ? A.sh_gate : A.gate) : (shared ? A.sh_up : A.up);
-            dma16(hm + (shared ? 0 : (size_t)e * A.F * A.rb) + (size_t)(rb0 * GU_WROWS + wave * GU_ROWS + (rr & 7)) * A.rb + sb * 144,
-                  hbuf + (size_t)q * 64 * 16);
+        for (int q = 0; q * 64 < 16 * HROW; q++) {
+            const int slot = q * 64 + lane, rr = slot / HROW, sb = slot - rr * HROW;
+            if (rr < 16 && sb < NSB)
+                dma16((rr < 8 ? gm : um) + (size_t)(wrow0 + (rr & 7)) * A.rb + sb * 144, hbuf + (size_t)q * 1024);
         }
-        // stage the nl tokens' planes and sum planes by direct global->shared
-        // copies (1 KB per wave instruction), in flight with the weight loads
-        {
-            const int per = 2 * D / 8, pers = 2 * D32 / 8;  // 16-byte chunks per token
-            for (int q = wave; q * 64 < nl * per; q += 4) {
-                const int c = q * 64 + lane, ti = c / per, off = c - ti * per;
-                const int sl = s_slot[t0 + ti], tok = shared ? sl - MS : sl / QG_TOP;
-                dma16(A.xp + (size_t)tok * 2 * D + (size_t)off * 8, act + (size_t)q * 64 * 8);
-            }
-            for (int q = wave; q * 64 < nl * pers; q += 4) {
-                int c = q * 64 + lane;
-                if (c >= nl * pers) c = 0;  // lanes past the tile copy a valid chunk into unused space
-                const int ti = c / pers, off = c - ti * pers;
-                const int sl = s_slot[t0 + ti], tok = shared ? sl - MS : sl / QG_TOP;
-                dma16(A.xsp + (size_t)tok * 2 * D32 + (size_t)off * 8, acts + (size_t)q * 64 * 8);
+        const int fmt = shared ? A.sh_fmt : A.fmt;
+        const int pos = plane_pos(fmt, wrow0 + (j & 7));
+        // stage rows r < 2n (token r/2, plane r%2) and their sum rows, in flight
+        // with the weight loads
+        for (int q = wave; q < 2 * n * bpr; q += 4) {
+            const int r = q / bpr, b = q - r * bpr;
+            const int sl = s_list[r >> 1], tok = shared ? sl - MS : sl / QG_TOP;
+            dma16(A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)(b * 64 + lane) * 8, act + (size_t)r * LY.arow + b * 512);
+        }
+        for (int q = wave; q * 64 < 2 * n * (cps + 1); q += 4) {
+            const int slot = q * 64 + lane, r = slot / (cps + 1), c = slot - r * (cps + 1);
+            if (r < 2 * n && c < cps) {
+                const int sl = s_list[r >> 1], tok = shared ? sl - MS : sl / QG_TOP;
+                dma16(A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)c * 8, acts + (size_t)q * 512);
             }
         }
         wait_vmem();
         __syncthreads();
-        const int ti = min(j >> 1, nl - 1);
-        const _Float16 *ap = act + ((size_t)ti * 2 + (j & 1)) * D + kq * 8;
-        const _Float16 *sp = acts + ((size_t)ti * 2 + (j & 1)) * D32;
+        const int r = 2 * min(j >> 1, n - 1) + (j & 1);
+        // the min-term product takes its 8 group sums from lanes kq = 0; the
+        // other lanes read zeros
+        const _Float16 *ap = act + (size_t)r * LY.arow + kq * 8, *sp = kq ? (const _Float16 *)s_zero : acts + (size_t)r * LY.srow;
+        const uint8_t *hp = hbuf + (size_t)j * HROW * 16;
+        const int gA = 2 * (kq >> 1), gB = gA + 4;
         qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
-            const Q4kHeader h = q4k_header(*(const uint4 *)(hbuf + ((size_t)j * NSB + sb) * 16));
-            const int gA = 2 * (kq >> 1), gB = gA + 4;
-            qg_f4 p = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, mm = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const Q4kHeader h = q4k_header(*(const uint4 *)(hp + sb * 16));
+            qg_f4 p0 = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, p1 = p0, mm = p0;
 #pragma unroll
-            for (int f = 0; f < 4; f++)
-                p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + f * 32),
-                                                           q4k_chunk_frag(c0[sb], f, (_Float16)q4k_s(h, gA + (f >> 1))), p, 0, 0, 0);
+            for (int f = 0; f < 4; f++) {
+                p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + f * 32),
+                                                            q4k_chunk_frag(c0[sb], f, q4k_sh(h, gA + (f >> 1))), p0, 0, 0, 0);
+                p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + (4 + f) * 32),
+                                                            q4k_chunk_frag(c1[sb], f, q4k_sh(h, gB + (f >> 1))), p1, 0, 0, 0);
+            }
+            mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(sp + sb * 8), q4k_min_frag(h), mm, 0, 0, 0);
 #pragma unroll
-            for (int f = 0; f < 4; f++)
-                p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + (4 + f) * 32),
-                                                           q4k_chunk_frag(c1[sb], f, (_Float16)q4k_s(h, gB + (f >> 1))), p, 0, 0, 0);
-            qg_half8 mf;
-#pragma unroll
-            for (int g = 0; g < 8; g++) mf[g] = kq == 0 ? (_Float16)q4k_m(h, g) : (_Float16)0.0f;
-            mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(sp + sb * 8), mf, mm, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(h.d, p[i], __builtin_fmaf(-h.dmin, mm[i], y[i]));
+            for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(h.d, p0[i] + p1[i], __builtin_fmaf(-h.dmin, mm[i], y[i]));
         }
-        const int fmt = shared ? A.sh_fmt : A.fmt;
-        const int pos = plane_pos(fmt, row);
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++) {
             const float v = y[2 * t2] + y[2 * t2 + 1];  // gate (j < 8) or up (j >= 8)
             const float u = __shfl_xor(v, 8);
-            const float m = qg_swiglu(v, u);
+            const float m = qg_swiglu_fast(v, u);
             // sum of the wave's 8 rows for this token (lanes j = 0..7)
             float s8 = m;
             s8 += __shfl_xor(s8, 1);
             s8 += __shfl_xor(s8, 2);
             s8 += __shfl_xor(s8, 4);
             const int idx = 2 * kq + t2;
-            if (j < 8 && idx < nl) {
-                const int sl = s_slot[t0 + idx];
-                _Float16 *hp = A.midp + (size_t)sl * 2 * A.F;
+            if (j < 8 && idx < n) {
+                const int sl = s_list[idx];
+                _Float16 *mp = A.midp + (size_t)sl * 2 * A.F;
                 const _Float16 hv = (_Float16)m;
-                hp[pos] = hv;
-                hp[A.F + pos] = (_Float16)(m - (float)hv);
+                mp[pos] = hv;
+                mp[A.F + pos] = (_Float16)(m - (float)hv);
                 if (j == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + rb0 * 4 + wave] = s8;
             }
         }
-        __syncthreads();  // shared buffers are rewritten by the next item
+        __syncthreads();  // the stage, the headers and the item are rewritten next
     }
 }
 
 // ---------------- K3: down ----------------
 struct DnArgs {
     int nt, D, F;
-    const int *ids; const float *w; const TokRoute *tr;
+    const float *w; const DecPlan *pl;
     const uint8_t *down, *sh_down; size_t rb, sh_rb;
     const _Float16 *midp; const float *msum8;
     float *slots;                        // [ME][D]: selection t*10+k (weighted), shared rows MS+t
@@ -441,9 +492,10 @@ QG_DEV qg_half8 dn_frag(const uint8_t *ast, int F, int r, int c) {
 
 // y (rows 4kq..4kq+3 = tokens 2kq, 2kq+1 x {hi, lo}) of weight row wr
 // (shared memory) against the staged tile; F/32 IQ4_NL blocks or F/256 Q4_K
-// superblocks.  Q4_K min terms from the 8-row sums of the tile's tokens.
+// superblocks.  Q4_K min terms from the 8-row sums of the tile's tokens,
+// staged as rows of F/8 floats padded by 4 (token mrow[t2]).
 template <int FMT>
-QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq, const float *msum8, const int *oslot) {
+QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq, const float *ms, const int *mrow) {
     qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     if (FMT == QT_Q4_K) {
         for (int sb = 0; sb < F / 256; sb++) {
@@ -464,7 +516,7 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++) {
                 // group sums of mid: 4 partial sums of 8 rows per 32-group
-                const float4 *X = (const float4 *)(msum8 + (size_t)oslot[t2] * (F / 8) + sb * 32);
+                const float4 *X = (const float4 *)(ms + mrow[t2] * (F / 8 + 4) + sb * 32);
                 float M = 0.0f;
 #pragma unroll
                 for (int g = 0; g < 8; g++) {
@@ -514,116 +566,88 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
 template <int FMT, int SFMT>
 __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
-    __shared__ int s_first[QG_EXPERTS];
-    __shared__ int s_ids[MS];
-    __shared__ int s_flag[MB];
-    __shared__ int s_items[MS + 1];
-    __shared__ int s_nitems, s_n;
+    __shared__ int s_e, s_n;
     __shared__ int s_list[MB];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    const int ns = A.nt * QG_TOP, F = A.F;
-    const bool has_shared = A.sh_down != nullptr;
-    for (int i = tid; i < QG_EXPERTS; i += 256) s_first[i] = 0x7fffffff;
-    for (int i = tid; i < ns; i += 256) s_ids[i] = A.ids[i];
-    if (tid < A.nt) s_flag[tid] = A.tr->flag[tid];
-    __syncthreads();
-    for (int i = tid; i < ns; i += 256) {
-        const int e = s_ids[i];
-        if (e >= 0 && e < QG_EXPERTS && s_flag[i / QG_TOP] < 2) atomicMin(&s_first[e], i);
-    }
-    __syncthreads();
-    if (wave == 0) {
-        int n = 0;
-        if (has_shared) {
-            if (lane == 0) s_items[0] = MS;
-            n = 1;
-        }
-        for (int c0 = 0; c0 < ns; c0 += 64) {
-            const int q = c0 + lane;
-            const int e = q < ns ? s_ids[q] : -1;
-            const bool own = e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2 && s_first[e] == q;
-            const unsigned long long b = __ballot(own);
-            if (own) s_items[n + __popcll(b & ((1ULL << lane) - 1ULL))] = q;
-            n += __popcll(b);
-        }
-        if (lane == 0) s_nitems = n;
-    }
-    __syncthreads();
-    const int dblocks = A.D / DN_ROWS, total = s_nitems * dblocks;
+    const int F = A.F, sh = A.sh_down != nullptr ? 1 : 0;
+    const int dblocks = A.D / DN_ROWS;
     const int rbmax = (int)(A.rb > A.sh_rb ? A.rb : A.sh_rb);
     const int slab = (DN_ROWS * rbmax + 1023) & ~1023;
     uint8_t *wbuf = (uint8_t *)s_dyn, *abuf = wbuf + slab;
+    float *mbuf = (float *)(abuf + 16 * F * 2);
     const int cpr = F / 8;  // 16-byte chunks per staged plane row
-    for (int item = blockIdx.x; item < total; item += gridDim.x) {
-        const int it = item / dblocks, d0 = (item - it * dblocks) * DN_ROWS;
-        const int sidx = s_items[it];
-        const bool shared = sidx == MS;
-        const int rb = (int)(shared ? A.sh_rb : A.rb);
+    const int sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    for (int item = blockIdx.x;; item += gridDim.x) {
+        const int T = item / dblocks, d0 = (item - T * dblocks) * DN_ROWS;
         if (wave == 0) {
-            int n;
-            if (shared) {
-                n = A.nt;
-                if (lane < A.nt) s_list[lane] = MS + lane;
-            } else {
-                const int e = s_ids[sidx];
-                n = 0;
-                for (int c0 = 0; c0 < ns; c0 += 64) {
-                    const int q = c0 + lane;
-                    const bool m = q < ns && s_ids[q] == e && s_flag[q / QG_TOP] < 2;
-                    const unsigned long long b = __ballot(m);
-                    const int pos = n + __popcll(b & ((1ULL << lane) - 1ULL));
-                    if (m && pos < MB) s_list[pos] = q;  // a token lists an expert at most once
-                    n += __popcll(b);
+            int e = -1, n = -1;
+            if (T < sh_tiles) {
+                n = min(TILE_TOK, A.nt - TILE_TOK * T);
+                if (lane < n) s_list[lane] = MS + TILE_TOK * T + lane;
+            } else if (T - sh_tiles < MAX_TILES) {
+                const int k = T - sh_tiles;
+                const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
+                const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
+                if (k < ntl) {
+                    e = ek;
+                    n = nk;
+                    if (lane < nk) s_list[lane] = qk;
                 }
-                n = min(n, MB);
             }
-            if (lane == 0) s_n = n;
+            if (lane == 0) { s_e = e; s_n = n; }
         }
+        __syncthreads();
+        const int e = s_e, n = s_n;
+        if (n < 0) break;  // block-uniform; every later item is past the plan too
+        const bool shared = e < 0;
+        const int rb = (int)(shared ? A.sh_rb : A.rb);
         // the item's weight slab: 64 consecutive rows, one flat copy
         {
-            const uint8_t *W = shared ? A.sh_down + (size_t)d0 * rb : A.down + ((size_t)s_ids[sidx] * A.D + d0) * rb;
+            const uint8_t *W = shared ? A.sh_down + (size_t)d0 * rb : A.down + ((size_t)e * A.D + d0) * rb;
             const int nch = DN_ROWS * rb / 16;
             for (int q = wave; q * 64 < nch; q += 4) {
-                int c = q * 64 + lane;
-                if (c >= nch) c = 0;  // lanes past the slab copy its first chunk into unused space
-                dma16(W + 16 * (size_t)c, wbuf + (size_t)q * 1024);
+                const int c = q * 64 + lane;
+                if (c < nch) dma16(W + 16 * (size_t)c, wbuf + (size_t)q * 1024);
             }
         }
-        __syncthreads();  // s_list / s_n
-        const int n = s_n;
+        // the tile's 2n plane rows (token r/2, plane r%2) of mid, swizzled; rows
+        // past them are not read into any kept result
+        for (int q = wave; q * 64 < 2 * n * cpr; q += 4) {
+            const int C = q * 64 + lane, r = C / cpr, pos = C - r * cpr;
+            if (r < 2 * n) dma16(A.midp + ((size_t)s_list[r >> 1] * 2 + (r & 1)) * F + (size_t)(pos ^ (r & 15)) * 8, abuf + (size_t)q * 1024);
+        }
+        if ((shared ? SFMT : FMT) == QT_Q4_K) {
+            // the tile tokens' 8-row sums of mid (Q4_K min terms), padded rows
+            const int cpm = F / 32;  // 16-byte chunks per row
+            for (int q = wave; q * 64 < n * (cpm + 1); q += 4) {
+                const int slot = q * 64 + lane, r = slot / (cpm + 1), c = slot - r * (cpm + 1);
+                if (r < n && c < cpm) dma16(A.msum8 + (size_t)s_list[r] * (F / 8) + c * 4, mbuf + q * 256);
+            }
+        }
+        wait_vmem();
+        __syncthreads();
         const uint8_t *wr = wbuf + (size_t)(16 * wave + j) * rb;
-        for (int c0 = 0; c0 < n; c0 += 8) {
-            // 16 plane rows (8 tokens x {hi, lo}) of mid, swizzled
-            for (int q = wave; q * 64 < 16 * cpr; q += 4) {
-                const int C = q * 64 + lane, r = C / cpr, pos = C - r * cpr;
-                const int sl = s_list[min(c0 + (r >> 1), n - 1)];
-                dma16(A.midp + ((size_t)sl * 2 + (r & 1)) * F + (size_t)(pos ^ (r & 15)) * 8, abuf + (size_t)q * 1024);
-            }
-            wait_vmem();
-            __syncthreads();
-            int oslot[2];
+        int mrow[2];
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) oslot[t2] = s_list[min(c0 + 2 * kq + t2, n - 1)];
-            const qg_f4 y = shared ? dn_tile<SFMT>(wr, abuf, F, j, kq, A.msum8, oslot) : dn_tile<FMT>(wr, abuf, F, j, kq, A.msum8, oslot);
+        for (int t2 = 0; t2 < 2; t2++) mrow[t2] = min(2 * kq + t2, n - 1);
+        const qg_f4 y = shared ? dn_tile<SFMT>(wr, abuf, F, j, kq, mbuf, mrow) : dn_tile<FMT>(wr, abuf, F, j, kq, mbuf, mrow);
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) {
-                const int idx = c0 + 2 * kq + t2;
-                if (idx < n) {
-                    const int sl = oslot[t2];
-                    const float v = y[2 * t2] + y[2 * t2 + 1];
-                    A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * A.w[sl];
-                }
+        for (int t2 = 0; t2 < 2; t2++) {
+            const int idx = 2 * kq + t2;
+            if (idx < n) {
+                const int sl = s_list[idx];
+                const float v = y[2 * t2] + y[2 * t2 + 1];
+                A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * A.w[sl];
             }
-            __syncthreads();  // the stage is rewritten by the next tile
         }
-        __syncthreads();  // s_list, s_n and the slab are rewritten by the next item
+        __syncthreads();  // s_list, s_e, s_n, the slab and the stage are rewritten by the next item
     }
 }
 
 // ---------------- K4: router-rank combine + shared + residual ----------------
 struct CombArgs {
     int nt, D;
-    const int *ids; const TokRoute *tr;
+    const int *ids; const DecPlan *pl;
     const float *slots;
     const float *sh_logit; int ld; int has_shared;
     float *out, *resid;
@@ -638,7 +662,7 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
     if (d < A.D) {
         // every load is independent of the others (slot addresses do not depend
         // on the ids): one memory round trip; invalid selections are selected away
-        const int flag = A.tr->flag[t];
+        const int flag = A.pl->flag[t];
         int e[QG_TOP];
         float4 v[QG_TOP];
 #pragma unroll
@@ -681,23 +705,18 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
     if (A.stats && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
         // counters in token order (deterministic, unlike the reference's atomics)
         for (int u = 0; u < A.nt; u++) {
-            const int f = A.tr->flag[u];
+            const int f = A.pl->flag[u];
             if (f == 3) continue;
             A.stats->token_layers += 1;
-            A.stats->missing_selections += (uint64_t)A.tr->missing[u];
+            A.stats->missing_selections += (uint64_t)A.pl->missing[u];
             if (f == 1) {
-                A.stats->skipped_selections += (uint64_t)A.tr->missing[u];
+                A.stats->skipped_selections += (uint64_t)A.pl->missing[u];
                 A.stats->avoided_token_handoffs += 1;
-                A.stats->skipped_mass += A.tr->mass[u];
+                A.stats->skipped_mass += A.pl->mass[u];
             }
         }
     }
 }
-
-// Tokens per gate/up tile (MFMA rows = tokens x {hi, lo}); the staged planes
-// of 8 tokens take 8 x 2 x (D + D/32) x 2 bytes of shared memory (68 KB at
-// D = 2048; a workgroup may use 160 KB on gfx950).
-int gu_tile_tokens(int) { return 8; }
 
 bool fmt_down_ok(int t, int F) { return (t == QT_Q4_K && F % 256 == 0) || t == QT_IQ4_NL; }
 
@@ -723,7 +742,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const bool sh = L->sh_gate != nullptr;
     const DecLayout lay = dec_layout(D, F);
     hipStream_t s = qg_stream();
-    TokRoute *tr = (TokRoute *)(ws + lay.tok);
+    DecPlan *pl = (DecPlan *)(ws + lay.tok);
     float *logits = (float *)(ws + lay.logits);
     _Float16 *xp = (_Float16 *)(ws + lay.xp);
     _Float16 *xsp = (_Float16 *)(ws + lay.xsum);
@@ -740,41 +759,42 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     if (rc) return rc;
     const bool inl = nt <= INLINE_MAX;
     if (!inl) {
-        RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, tr};
-        dec_launch(1, dec_route_kernel, dim3((nt + 3) / 4), dim3(256), 0, s, RA);
+        RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, pl};
+        dec_launch(1, dec_route_kernel, dim3(1), dim3(64 * RT_WAVES), 0, s, RA);
         if ((rc = hipGetLastError())) return rc;
     }
     _Float16 *midp = (_Float16 *)(ws + lay.midp);
     float *msum8 = (float *)(ws + lay.msum);
-    GuArgs G2{nt, D, F, inl ? 1 : 0, logits, rows, L->resident, L->threshold, ids, weights, flags, tr,
+    GuArgs G2{nt, D, F, inl ? 1 : 0, logits, rows, L->resident, L->threshold, ids, weights, flags, pl,
               (const uint8_t *)L->gate, (const uint8_t *)L->up, sh ? (const uint8_t *)L->sh_gate : nullptr,
               sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D), xp, xsp, midp, msum8,
-              L->down_type, sh ? L->sh_down_type : L->down_type, gu_tile_tokens(D)};
-    // upper bound of the work items: every selection its own expert with one tile
-    const int rblocks = F / GU_WROWS;
-    const int TT = gu_tile_tokens(D);
-    const int items = ((sh ? (nt + TT - 1) / TT : 0) + (nt * QG_TOP < QG_EXPERTS ? nt * QG_TOP : QG_EXPERTS)) * rblocks;
+              L->down_type, sh ? L->sh_down_type : L->down_type};
+    // upper bound of the tiles: the shared expert's, and every selection its own tile
+    const int tiles = (sh ? (nt + TILE_TOK - 1) / TILE_TOK : 0) + nt * QG_TOP;
+    const int items = tiles * (F / GU_WROWS);
     const int nwg = items < GU_WGS ? items : GU_WGS;
-    // planes, the sum planes rounded up to whole 1 KB copies, 4 waves' headers
-    // (16 rows x NSB x 16 B, the last copy rounded up to 1 KB)
-    const size_t act_lds = (size_t)TT * 2 * D * 2 + (((size_t)TT * 2 * (D / 32) * 2 + 1023) & ~(size_t)1023) +
-                           4 * (((size_t)16 * (D / 256) * 16 + 1023) & ~(size_t)1023);
-    if (D == 2048) dec_launch(2, dec_gateup_kernel<8>, dim3(nwg), dim3(256), act_lds, s, G2);
-    else dec_launch(2, dec_gateup_kernel<10>, dim3(nwg), dim3(256), act_lds, s, G2);
+    const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
+    if (D == 2048) {
+        if (inl) dec_launch(2, dec_gateup_kernel<8, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        else dec_launch(2, dec_gateup_kernel<8, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+    } else {
+        if (inl) dec_launch(2, dec_gateup_kernel<10, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+    }
     if ((rc = hipGetLastError())) return rc;
     const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;
     float *slots = (float *)(ws + lay.slots);
-    DnArgs DA{nt, D, F, ids, weights, tr, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
+    DnArgs DA{nt, D, F, weights, pl, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
               midp, msum8, slots};
     const size_t rbmax = rb > srb ? rb : srb;
-    const size_t dn_lds = ((DN_ROWS * rbmax + 1023) & ~(size_t)1023) + (size_t)16 * F * 2;
+    // slab, 16 staged plane rows, 8 padded rows of 8-row sums (rounded up to whole 1 KB copies)
+    const size_t dn_lds = ((DN_ROWS * rbmax + 1023) & ~(size_t)1023) + (size_t)16 * F * 2 +
+                          (((size_t)8 * (F / 8 + 4) * 4 + 1023) & ~(size_t)1023);
     const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
-    // upper bound of the items: every selection its own expert, plus the shared expert
-    const int owners = (nt * QG_TOP < QG_EXPERTS ? nt * QG_TOP : QG_EXPERTS) + (sh ? 1 : 0);
-    const int dn_items = owners * (D / DN_ROWS);
+    const int dn_items = tiles * (D / DN_ROWS);
     launch_down(DA, fr, fs, dim3(dn_items < DN_WGS ? dn_items : DN_WGS), dn_lds, s);
     if ((rc = hipGetLastError())) return rc;
-    CombArgs CA{nt, D, ids, tr, slots, logits + QG_EXPERTS, rows, sh ? 1 : 0, out, resid,
+    CombArgs CA{nt, D, ids, pl, slots, logits + QG_EXPERTS, rows, sh ? 1 : 0, out, resid,
                 (L->resident && stats) ? stats : nullptr};
     dec_launch(4, dec_combine_kernel, dim3((D / 4 + 255) / 256, nt), dim3(256), 0, s, CA);
     return hipGetLastError();
