@@ -114,17 +114,6 @@ QG_DEV float qg_swiglu_fast(float g, float u) {
 }
 
 // ---- cross-lane helpers (wave64) ----
-// Pairwise tree over 32-lane halves with strides 16,8,4,2,1: lane 0 (and 32)
-// ends with ((a0+a16)+(a8+a24))+... exactly as cpu.c's reduction
-// (cpu_portable.h:333, gpu.cu:89-92).
-QG_DEV float qg_tree32(float v) {
-    v += __shfl_down(v, 16, 32);
-    v += __shfl_down(v, 8, 32);
-    v += __shfl_down(v, 4, 32);
-    v += __shfl_down(v, 2, 32);
-    v += __shfl_down(v, 1, 32);
-    return v;
-}
 // Sum over `width` consecutive lanes (power of two <= 64); result in every lane.
 template <int WIDTH>
 QG_DEV float qg_sum_lanes(float v) {
@@ -143,6 +132,19 @@ QG_DEV float qg_row_max(float v) {
     v = fmaxf(v, QG_DPP_F(v, 0x4E));
     v = fmaxf(v, QG_DPP_F(v, 0x141));
     v = fmaxf(v, QG_DPP_F(v, 0x140));
+    return v;
+}
+// Pairwise tree over 32-lane halves with strides 16,8,4,2,1: lane 0 (and 32)
+// ends with ((a0+a16)+(a8+a24))+... exactly as cpu.c's reduction
+// (cpu_portable.h:333, gpu.cu:89-92); only lanes 0 and 32 are meaningful.
+// Stride 16 is a swizzle (lane ^ 16), strides 8..1 rotate within 16-lane
+// rows, which gives lanes 0 and 32 the same partners as the strided tree.
+QG_DEV float qg_tree32(float v) {
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    v += QG_DPP_F(v, 0x128);
+    v += QG_DPP_F(v, 0x124);
+    v += QG_DPP_F(v, 0x122);
+    v += QG_DPP_F(v, 0x121);
     return v;
 }
 QG_DEV float qg_wave_max(float v) {

@@ -31,6 +31,7 @@
 #include "qg_internal.h"
 #include "qg_frag.h"
 #include <hip/hip_ext.h>
+#include <type_traits>
 
 namespace {
 
@@ -98,85 +99,110 @@ struct RouterArgs {
     float *logits;                  // [nt][rows]
     int norm; float eps; float *xn; // RMS-normalise the input; normalised rows to xn
     _Float16 *xp, *xsp;             // planes [nt][2][D] (Q4_K order); planes of 32-group sums [nt][2][D/32]
-    int row_pairs;                  // blockIdx.x < row_pairs: router rows; above: planes
+    int row_blocks;                 // blockIdx.x < row_blocks: router rows; above: planes
     const float *bias;              // F32 [512] added to the expert logits, or null
 };
 
-// Router: grid (row_pairs + ceil(nt/4)), 4 waves per block.  Router block x <
-// row_pairs: each 32-lane half owns row 2x+half, wave w the tokens w, w+4, ...,
-// w+4(TPW-1); lane j accumulates columns k = j (mod 32) in ascending k with
-// fma, then the 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal
-// the reference's qc_matmul bit for bit.  The router rows are read from HBM
-// once per block (the 4 waves share them through the L1); the loads of the
-// next chunk of k-steps are in flight while a chunk's fmas run.  Blocks x >=
-// row_pairs: one token per wave, its (optionally normalised) row as fp16
-// hi/lo planes in the Q4_K fragment order, plus hi/lo planes of the sums of
-// each 32-group.
-template <int TPW>
+
+// The exact-order dot product of one router row with one token row: lane j of
+// each 32-lane half accumulates columns k = j (mod 32) in ascending k with fma,
+// then the 16/8/4/2/1 tree (cpu.c:122-139).  Used by the plane blocks for the
+// shared-expert gate vector.
+template <int KS>
+QG_DEV float exact_row_dot(const float *w, const float *x, bool norm, float sc, int j) {
+    float wv[KS], xv[KS], acc = 0.0f;  // every load in flight at once
+#pragma unroll
+    for (int i = 0; i < KS; i++) { wv[i] = w[32 * i + j]; xv[i] = x[32 * i + j]; }
+#pragma unroll
+    for (int i = 0; i < KS; i++) acc = __builtin_fmaf(wv[i], norm ? xv[i] * sc : xv[i], acc);
+    return qg_tree32(acc);
+}
+
+// Router: grid (64 x token groups of up to 5 + ceil(nt/4) plane blocks), 4
+// waves per block.  Router block b covers expert rows 8(b % 64) .. +7 and the
+// token group b / 64 (TPB tokens), so the blocks sharing a row block sit on
+// one XCD and share its router rows through that L2.  Wave w owns rows
+// 8(b % 64) + 2w + h (32-lane half h), read into registers; the group's token
+// rows are staged in shared memory by direct global->shared copies, each
+// block starting at its own offset so the CUs do not read the same L2 lines
+// at once.  Lane j accumulates columns k = j (mod 32) in ascending k with fma,
+// then the 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal the
+// reference's qc_matmul bit for bit.  Blocks above 64 x groups: one token per
+// wave: the shared-expert gate logit (same order), and the (optionally
+// normalised) row as fp16 hi/lo planes in the Q4_K fragment order plus hi/lo
+// planes of the sums of each 32-group.
+constexpr int RT_ROWBLOCKS = QG_EXPERTS / 8;
+template <int TPB, int DW>
 __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
+    constexpr int KS = DW / 32;
+    extern __shared__ float s_rt[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
-    if (blockIdx.x >= A.row_pairs) {
-        const int t = (blockIdx.x - A.row_pairs) * 4 + wave;
-        if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
-        const float *xr = A.x + (size_t)t * A.D;
-        const float sc = A.norm ? row_rms_scale(xr, A.D, A.eps, lane) : 1.0f;
-        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
-        token_planes(xr, A.D, A.norm != 0, sc, lane, hi, hi + A.D, shi, shi + A.D / 32, A.xn ? A.xn + (size_t)t * A.D : nullptr);
+    const int nt = A.nt;
+    if (blockIdx.x >= A.row_blocks) {
+        const int t = (blockIdx.x - A.row_blocks) * 4 + wave;
+        if (t >= nt) return;  // whole wave; the plane blocks have no block barrier
+        const float *xr = A.x + (size_t)t * DW;
+        const float sc = A.norm ? row_rms_scale(xr, DW, A.eps, lane) : 1.0f;
+        if (A.sh_row) {
+            const float r = exact_row_dot<KS>(A.sh_row, xr, A.norm != 0, sc, j);
+            if (lane == 0) A.logits[(size_t)t * A.rows + QG_EXPERTS] = r;
+        }
+        _Float16 *hi = A.xp + (size_t)t * 2 * DW, *shi = A.xsp + (size_t)t * 2 * (DW / 32);
+        token_planes(xr, DW, A.norm != 0, sc, lane, hi, hi + DW, shi, shi + DW / 32, A.xn ? A.xn + (size_t)t * DW : nullptr);
         return;
     }
-    if (wave >= A.nt) return;  // whole wave
-    const int row = blockIdx.x * 2 + half;
-    const bool rok = row < A.rows;
-    const float *wr = !rok ? A.router : row == QG_EXPERTS ? A.sh_row : A.router + (size_t)row * A.D;
-    // the wave's tokens; past the batch they repeat the wave's first token and are not stored
-    const float *xr[TPW];
-    float sc[TPW], acc[TPW];
+    const int rb = blockIdx.x % RT_ROWBLOCKS, t0 = (blockIdx.x / RT_ROWBLOCKS) * TPB;
+    const int ntg = min(TPB, nt - t0);  // tokens of this group (>= 1)
+    const int row = rb * 8 + 2 * wave + half;
+    const float *wr = A.router + (size_t)row * DW;
+    // the group's token rows, 1 KB per copy, rotated start
+    constexpr int CPT = DW / 256;
+    const int ncp = ntg * CPT, rot = (int)((blockIdx.x * 37u) % (unsigned)ncp);
+    for (int q = wave; q < ncp; q += 4) {
+        int c = q + rot;
+        if (c >= ncp) c -= ncp;
+        dma16(A.x + (size_t)t0 * DW + c * 256 + lane * 4, s_rt + c * 256);
+    }
+    // the wave's router rows, in flight with the copies
+    float wv[KS];
 #pragma unroll
-    for (int u = 0; u < TPW; u++) {
-        const int t = wave + 4 * u < A.nt ? wave + 4 * u : wave;
-        xr[u] = A.x + (size_t)t * A.D;
-        sc[u] = A.norm ? row_rms_scale(xr[u], A.D, A.eps, lane) : 1.0f;
+    for (int i = 0; i < KS; i++) wv[i] = wr[32 * i + j];
+    wait_vmem();
+    __syncthreads();
+    // past the group the chains repeat its first token and are not stored
+    float sc[TPB], acc[TPB];
+    const float *xb[TPB];
+#pragma unroll
+    for (int u = 0; u < TPB; u++) {
+        const int uu = u < ntg ? u : 0;
+        xb[u] = s_rt + uu * DW + j;
+        sc[u] = A.norm ? lds_rms_scale(s_rt + uu * DW, DW, A.eps, lane) : 1.0f;
         acc[u] = 0.0f;
     }
-    // chunks of CH k-steps in a ring of NBUF register buffers: the loads of
-    // chunks c+1 .. c+NBUF-1 are in flight while chunk c's fmas run (one token:
-    // the whole row of a 2048-wide layer is requested at once)
-    constexpr int CH = TPW == 1 ? 16 : 8, NBUF = TPW == 1 ? 4 : 2;
-    const int nfull = A.D / (32 * CH);
-    float wv[NBUF][CH], xv[NBUF][TPW][CH];
-    auto load = [&](int b, int k0) {
+    // the TPB chains advance together, 4 k-steps per group: the compiler
+    // barriers between groups (memory, and every accumulator) keep it from
+    // running one chain ahead while the others' reads pile up in registers
+    auto chains = [&](auto scaled) {
 #pragma unroll
-        for (int i = 0; i < CH; i++) wv[b][i] = wr[k0 + 32 * i + j];
+        for (int i = 0; i < KS; i++) {
 #pragma unroll
-        for (int u = 0; u < TPW; u++)
+            for (int u = 0; u < TPB; u++) {
+                const float xv = xb[u][32 * i];
+                acc[u] = __builtin_fmaf(wv[i], decltype(scaled)::value ? xv * sc[u] : xv, acc[u]);
+            }
+            if ((i & 3) == 3) {
+                asm volatile("" ::: "memory");
 #pragma unroll
-            for (int i = 0; i < CH; i++) xv[b][u][i] = xr[u][k0 + 32 * i + j];
-    };
-#pragma unroll
-    for (int b = 0; b < NBUF - 1; b++)
-        if (b < nfull) load(b, b * 32 * CH);
-    for (int c = 0; c < nfull; c += NBUF) {
-#pragma unroll
-        for (int b = 0; b < NBUF; b++) {
-            if (c + b >= nfull) break;
-            if (c + b + NBUF - 1 < nfull) load((b + NBUF - 1) % NBUF, (c + b + NBUF - 1) * 32 * CH);
-#pragma unroll
-            for (int i = 0; i < CH; i++)
-#pragma unroll
-                for (int u = 0; u < TPW; u++)
-                    acc[u] = __builtin_fmaf(wv[b][i], A.norm ? xv[b][u][i] * sc[u] : xv[b][u][i], acc[u]);
+                for (int u = 0; u < TPB; u++) asm volatile("" : "+v"(acc[u]));
+            }
         }
-    }
-    for (int k0 = nfull * 32 * CH; k0 < A.D; k0 += 32) {  // D not a multiple of 32*CH
-        const float w1 = wr[k0 + j];
+    };
+    if (A.norm) chains(std::true_type{});
+    else chains(std::false_type{});
 #pragma unroll
-        for (int u = 0; u < TPW; u++) acc[u] = __builtin_fmaf(w1, A.norm ? xr[u][k0 + j] * sc[u] : xr[u][k0 + j], acc[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < TPW; u++) {
+    for (int u = 0; u < TPB; u++) {
         const float r = qg_tree32(acc[u]);
-        const int t = wave + 4 * u;
-        if (j == 0 && rok && t < A.nt) A.logits[(size_t)t * A.rows + row] = A.bias && row < QG_EXPERTS ? r + A.bias[row] : r;
+        if (j == 0 && u < ntg) A.logits[(size_t)(t0 + u) * A.rows + row] = A.bias ? r + A.bias[row] : r;
     }
 }
 
@@ -189,10 +215,11 @@ struct RouteArgs {
 
 constexpr int RT_WAVES = 16;
 
-// Wave w routes tokens w, w + 16; then the block builds the plan: each
-// expert's first eligible selection and eligible count (shared-memory
-// atomics), the experts in selection order with the prefix of their tile
-// counts (wave 0), and each expert's tiles (one wave per expert).
+// One block: wave w routes tokens w, w + 16 (a second block with a
+// device-scope release/acquire hand-off measured slower); then the block
+// builds the plan: each expert's first eligible selection and eligible count
+// (shared-memory atomics), the experts in selection order with the prefix of
+// their tile counts (wave 0), and each expert's tiles (one wave per expert).
 __global__ __launch_bounds__(1024) void dec_route_kernel(RouteArgs A) {
     __shared__ float s_rv[RT_WAVES][64];
     __shared__ int s_ri[RT_WAVES][64];
@@ -201,6 +228,7 @@ __global__ __launch_bounds__(1024) void dec_route_kernel(RouteArgs A) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ns = A.nt * QG_TOP;
     const unsigned long long below = (1ULL << lane) - 1ULL;
     for (int i = tid; i < QG_EXPERTS; i += 64 * RT_WAVES) { s_first[i] = 0x7fffffff; s_cnt[i] = 0; }
+    // wave w routes tokens w, w + 16
     for (int t = wave; t < A.nt; t += RT_WAVES) {
         int id, missing;
         float wv;
@@ -736,6 +764,17 @@ void launch_down(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStr
     else dec_launch(3, dec_down_kernel<QT_Q4_K, QT_Q4_K>, grid, block, lds, s, DA);
 }
 
+template <int DW>
+void router_launch(int TPB, dim3 grid, dim3 block, size_t lds, hipStream_t s, const RouterArgs &R) {
+    switch (TPB) {
+    case 1: dec_launch(0, dec_router_kernel<1, DW>, grid, block, lds, s, R); break;
+    case 2: dec_launch(0, dec_router_kernel<2, DW>, grid, block, lds, s, R); break;
+    case 3: dec_launch(0, dec_router_kernel<3, DW>, grid, block, lds, s, R); break;
+    case 4: dec_launch(0, dec_router_kernel<4, DW>, grid, block, lds, s, R); break;
+    default: dec_launch(0, dec_router_kernel<5, DW>, grid, block, lds, s, R); break;
+    }
+}
+
 int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                 const float *x, float *xn_out, int norm, int nt, const qg_moe_layer *L, uint8_t *ws) {
     const int D = L->width, F = L->ff;
@@ -747,14 +786,15 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     _Float16 *xp = (_Float16 *)(ws + lay.xp);
     _Float16 *xsp = (_Float16 *)(ws + lay.xsum);
     const int rows = QG_EXPERTS + (sh ? 1 : 0);
-    const int row_pairs = (rows + 1) / 2;
-    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_pairs,
+    // token groups of up to 5: 64 row blocks each
+    const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr;
+    const int row_blocks = RT_ROWBLOCKS * ngr;
+    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_blocks,
                  L->router_bias};
-    const dim3 rgrid(row_pairs + (nt + 3) / 4);
-    if (nt <= 4) dec_launch(0, dec_router_kernel<1>, rgrid, dim3(256), 0, s, R);
-    else if (nt <= 8) dec_launch(0, dec_router_kernel<2>, rgrid, dim3(256), 0, s, R);
-    else if (nt <= 12) dec_launch(0, dec_router_kernel<3>, rgrid, dim3(256), 0, s, R);
-    else dec_launch(0, dec_router_kernel<5>, rgrid, dim3(256), 0, s, R);
+    const dim3 rgrid(row_blocks + (nt + 3) / 4), rblock(256);
+    const size_t rlds = (size_t)TPB * D * 4;
+    if (D == 2048) router_launch<2048>(TPB, rgrid, rblock, rlds, s, R);
+    else router_launch<2560>(TPB, rgrid, rblock, rlds, s, R);
     int rc = hipGetLastError();
     if (rc) return rc;
     const bool inl = nt <= INLINE_MAX;

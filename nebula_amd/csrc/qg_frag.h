@@ -71,14 +71,25 @@ QG_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 // wave; every caller runs this same code, so all blocks agree bit for bit.
 QG_DEV float row_rms_scale(const float *xr, int D, float eps, int lane) {
     float ss = 0.0f;
+#pragma unroll 4
     for (int i = lane; i < D; i += 64) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    ss = qg_sum_lanes<64>(ss);
+    return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+}
+// The same scale from a row held in shared memory (same values, same order).
+QG_DEV float lds_rms_scale(const float *xl, int D, float eps, int lane) {
+    float ss = 0.0f;
+#pragma unroll 4
+    for (int i = lane; i < D; i += 64) ss = __builtin_fmaf(xl[i], xl[i], ss);
     ss = qg_sum_lanes<64>(ss);
     return 1.0f / __builtin_sqrtf(ss / (float)D + eps);
 }
 
 // The fp16 hi/lo planes of one token row (Q4_K fragment order) and the hi/lo
 // planes of its 32-group sums, optionally RMS-scaled by sc (written to xn);
-// lane g handles groups g, g+64, ... with 8 float4 loads each.
+// lane g handles groups g, g+64, ... with 8 float4 loads each.  In the Q4_K
+// order every 16-byte chunk holds 8 consecutive elements of one group (in
+// qg_perm8 order), so each group is written as 4 chunks per plane.
 QG_DEV void token_planes(const float *xr, int D, bool norm, float sc, int lane, _Float16 *hi, _Float16 *lo,
                          _Float16 *shi, _Float16 *slo, float *xn) {
     for (int g = lane; g < D / 32; g += 64) {
@@ -98,13 +109,25 @@ QG_DEV void token_planes(const float *xr, int D, bool norm, float sc, int lane, 
         const _Float16 sh = (_Float16)s;
         shi[g] = sh;
         slo[g] = (_Float16)(s - (float)sh);
+        if (norm && xn) {
+            float4 *dst = (float4 *)(xn + 32 * g);
 #pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const int e = 32 * g + l, p = plane_pos(QT_Q4_K, e);
-            const _Float16 h = (_Float16)v[l];
-            hi[p] = h;
-            lo[p] = (_Float16)(v[l] - (float)h);
-            if (norm && xn) xn[e] = v[l];
+            for (int i = 0; i < 8; i++) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            // elements 8q..8q+7 of the group form one chunk; pos_q4k of its first element
+            const int p0 = (g & ~7) * 32 + pos_q4k((g & 7) * 32 + 8 * q);
+            qg_half8 h8, l8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = v[8 * q + qg_perm8(i)];
+                const _Float16 h = (_Float16)x;
+                h8[i] = h;
+                l8[i] = (_Float16)(x - (float)h);
+            }
+            *(qg_half8 *)(hi + p0) = h8;
+            *(qg_half8 *)(lo + p0) = l8;
         }
     }
 }
