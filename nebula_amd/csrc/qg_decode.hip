@@ -343,8 +343,8 @@ static __host__ __device__ inline GuLds gu_lds(int D) {
 template <int NSB, bool INL>
 __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
-    __shared__ int s_item[2];        // expert (-1: shared), token count (-1: no more items)
-    __shared__ int s_list[MB];       // the item's selections (shared expert: MS + t)
+    __shared__ int s_item[2][2];     // per buffer: expert (-1: shared), token count (-1: no more items)
+    __shared__ int s_list[2][TILE_TOK];  // per buffer: the item's selections (shared expert: MS + t)
     __shared__ float s_rv[64];
     __shared__ int s_ri[64];
     __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
@@ -388,73 +388,94 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         __syncthreads();
     }
     const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
-    for (int item = blockIdx.x;; item += gridDim.x) {
-        const int T = item / rblocks, rb0 = item - T * rblocks;
-        if (wave == 0) {
-            int e = -1, n = -1;
-            if (T < sh_tiles) {
-                n = min(TILE_TOK, A.nt - TILE_TOK * T);
-                if (lane < n) s_list[lane] = MS + TILE_TOK * T + lane;
-            } else if (INL) {
-                const int k = T - sh_tiles;
-                if (k < s_nent) {
-                    e = s_rid[k];
-                    n = 1;
-                    if (lane == 0) s_list[0] = s_rank[k];
-                }
-            } else if (T - sh_tiles < MAX_TILES) {
-                // one round trip: the tile count and the tile are independent loads
-                const int k = T - sh_tiles;
-                const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
-                const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
-                if (k < ntl) {
-                    e = ek;
-                    n = nk;
-                    if (lane < nk) s_list[lane] = qk;
-                }
+    // item -> expert (-1: shared), token count (-1: past the plan) and list, by
+    // wave 0 into buffer b (its plan loads stay in flight until the next wait)
+    auto resolve = [&](int item, int b) {
+        if (wave != 0) return;
+        const int T = item / rblocks;
+        int e = -1, n = -1;
+        if (T < sh_tiles) {
+            n = min(TILE_TOK, A.nt - TILE_TOK * T);
+            if (lane < n) s_list[b][lane] = MS + TILE_TOK * T + lane;
+        } else if (INL) {
+            const int k = T - sh_tiles;
+            if (k < s_nent) {
+                e = s_rid[k];
+                n = 1;
+                if (lane == 0) s_list[b][0] = s_rank[k];
             }
-            if (lane == 0) { s_item[0] = e; s_item[1] = n; }
+        } else if (T - sh_tiles < MAX_TILES) {
+            // one round trip: the tile count and the tile are independent loads
+            const int k = T - sh_tiles;
+            const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
+            const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
+            if (k < ntl) {
+                e = ek;
+                n = nk;
+                if (lane < nk) s_list[b][lane] = qk;
+            }
         }
-        __syncthreads();
-        const int e = s_item[0], n = s_item[1];
-        if (n < 0) break;  // block-uniform; every later item is past the plan too
-        const bool shared = e < 0;
-        const uint8_t *gm = shared ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
-        const uint8_t *um = shared ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
-        const int wrow0 = rb0 * GU_WROWS + wave * GU_ROWS;
-        // weight rows of this wave into registers
-        const uint8_t *wrow = (j < 8 ? gm : um) + (size_t)(wrow0 + (j & 7)) * A.rb;
-        uint4 c0[NSB], c1[NSB];
+        if (lane == 0) { s_item[b][0] = e; s_item[b][1] = n; }
+    };
+    auto mats = [&](int e, const uint8_t *&gm, const uint8_t *&um) {
+        gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
+        um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
+    };
+    // this wave's 8 gate and 8 up rows of an item into registers
+    auto load_weights = [&](int e, int rb0, uint4 *w0, uint4 *w1) {
+        const uint8_t *gm, *um;
+        mats(e, gm, um);
+        const uint8_t *wrow = (j < 8 ? gm : um) + (size_t)(rb0 * GU_WROWS + wave * GU_ROWS + (j & 7)) * A.rb;
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
-            const uint8_t *p = wrow + sb * 144;
-            c0[sb] = qg_ld16(p + 16 + 16 * kq);
-            c1[sb] = qg_ld16(p + 16 + 16 * (kq + 4));
+            w0[sb] = qg_ld16(wrow + sb * 144 + 16 + 16 * kq);
+            w1[sb] = qg_ld16(wrow + sb * 144 + 16 + 16 * (kq + 4));
         }
-        // the wave's 16 x NSB superblock headers, straight into shared memory
+    };
+    // the wave's 16 x NSB superblock headers, and the tile's rows r < 2n (token
+    // r/2, plane r%2) with their sum rows, straight into shared memory
+    auto stage = [&](int e, int rb0, int n, const int *list) {
+        const uint8_t *gm, *um;
+        mats(e, gm, um);
+        const int wrow0 = rb0 * GU_WROWS + wave * GU_ROWS;
         for (int q = 0; q * 64 < 16 * HROW; q++) {
             const int slot = q * 64 + lane, rr = slot / HROW, sb = slot - rr * HROW;
             if (rr < 16 && sb < NSB)
                 dma16((rr < 8 ? gm : um) + (size_t)(wrow0 + (rr & 7)) * A.rb + sb * 144, hbuf + (size_t)q * 1024);
         }
-        const int fmt = shared ? A.sh_fmt : A.fmt;
-        const int pos = plane_pos(fmt, wrow0 + (j & 7));
-        // stage rows r < 2n (token r/2, plane r%2) and their sum rows, in flight
-        // with the weight loads
         for (int q = wave; q < 2 * n * bpr; q += 4) {
             const int r = q / bpr, b = q - r * bpr;
-            const int sl = s_list[r >> 1], tok = shared ? sl - MS : sl / QG_TOP;
+            const int sl = list[r >> 1], tok = e < 0 ? sl - MS : sl / QG_TOP;
             dma16(A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)(b * 64 + lane) * 8, act + (size_t)r * LY.arow + b * 512);
         }
         for (int q = wave; q * 64 < 2 * n * (cps + 1); q += 4) {
             const int slot = q * 64 + lane, r = slot / (cps + 1), c = slot - r * (cps + 1);
             if (r < 2 * n && c < cps) {
-                const int sl = s_list[r >> 1], tok = shared ? sl - MS : sl / QG_TOP;
+                const int sl = list[r >> 1], tok = e < 0 ? sl - MS : sl / QG_TOP;
                 dma16(A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)c * 8, acts + (size_t)q * 512);
             }
         }
+    };
+    // software pipeline over the workgroup's items: the next item's weight rows
+    // load into registers while the current item's products run
+    int item = blockIdx.x, buf = 0;
+    resolve(item, 0);
+    __syncthreads();
+    if (s_item[0][1] < 0) return;  // block-uniform
+    uint4 c0[NSB], c1[NSB], n0[NSB], n1[NSB];
+    load_weights(s_item[0][0], item % rblocks, c0, c1);
+    stage(s_item[0][0], item % rblocks, s_item[0][1], s_list[0]);
+    for (;;) {
+        const int next = item + gridDim.x;
+        resolve(next, buf ^ 1);
         wait_vmem();
         __syncthreads();
+        const int e = s_item[buf][0], n = s_item[buf][1], rb0 = item % rblocks;
+        const int e2 = s_item[buf ^ 1][0], n2 = s_item[buf ^ 1][1];
+        if (n2 >= 0) load_weights(e2, next % rblocks, n0, n1);
+        const bool shared = e < 0;
+        const int fmt = shared ? A.sh_fmt : A.fmt;
+        const int pos = plane_pos(fmt, rb0 * GU_WROWS + wave * GU_ROWS + (j & 7));
         const int r = 2 * min(j >> 1, n - 1) + (j & 1);
         // the min-term product takes its 8 group sums from lanes kq = 0; the
         // other lanes read zeros
@@ -476,6 +497,11 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
             mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(sp + sb * 8), q4k_min_frag(h), mm, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(h.d, p0[i] + p1[i], __builtin_fmaf(-h.dmin, mm[i], y[i]));
+            // one superblock at a time: its sums are taken and no later read is
+            // hoisted above it (the prefetched weight rows need the registers)
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < 4; i++) asm volatile("" : "+v"(y[i]));
         }
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++) {
@@ -489,7 +515,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
             s8 += __shfl_xor(s8, 4);
             const int idx = 2 * kq + t2;
             if (j < 8 && idx < n) {
-                const int sl = s_list[idx];
+                const int sl = s_list[buf][idx];
                 _Float16 *mp = A.midp + (size_t)sl * 2 * A.F;
                 const _Float16 hv = (_Float16)m;
                 mp[pos] = hv;
@@ -497,7 +523,13 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
                 if (j == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + rb0 * 4 + wave] = s8;
             }
         }
-        __syncthreads();  // the stage, the headers and the item are rewritten next
+        __syncthreads();  // the stage, the headers and this item's buffer are free
+        if (n2 < 0) break;  // block-uniform
+        stage(e2, next % rblocks, n2, s_list[buf ^ 1]);
+#pragma unroll
+        for (int sb = 0; sb < NSB; sb++) { c0[sb] = n0[sb]; c1[sb] = n1[sb]; }
+        item = next;
+        buf ^= 1;
     }
 }
 
