@@ -361,7 +361,7 @@ def bench_prefill(args, data: str) -> dict:
                    "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
         "roofline": {"bound": "mfma", "kernel": "gate_up_dense", "achieved": round(achieved, 1) if achieved else None,
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4) if achieved else None,
-                     "traffic": load_traffic(f"gate_up_dense_config3_B{nt}"), "algorithmic_ops": ops_gu(rows_dense)},
+                     **load_traffic(f"gate_up_dense_config3_B{nt}"), "algorithmic_ops": ops_gu(rows_dense)},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
@@ -379,7 +379,18 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy kernel over MIB MiB 5 times (qg_unary identity: MIB read, MIB "
+                         "written; the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src, dst = qg.Device(nbytes=n), qg.Device(nbytes=n)
+        for _ in range(5):
+            qg.call("unary", dst.p, src.p, n // 4, 2, qg.F(1.0))
+        qg.call("sync")
+        print(json.dumps({"calibration_copy_bytes": n, "copies": 5, "kernel": "unary_kernel (identity)"}), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the layer; --gpus {args.gpus} is not supported "
               "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
@@ -447,7 +458,7 @@ def main() -> int:
                    "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
         "roofline": {"bound": "hbm", "kernel": "gate_up", "achieved": round(achieved, 1) if achieved else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-                     "traffic": load_traffic(f"gate_up_config{args.config}_B{wl.nt}"),
+                     **load_traffic(f"gate_up_config{args.config}_B{wl.nt}"),
                      "algorithmic_bytes": int(gu_bytes)},
         "cpu_baseline": None,
     }
@@ -457,16 +468,23 @@ def main() -> int:
     return 0
 
 
-def load_traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
-    counters (profiles/traffic.json), or None when not measured."""
+def load_traffic(name: str) -> dict:
+    """HBM bytes per launch of the roofline kernel, measured with rocprofv3
+    FETCH_SIZE/WRITE_SIZE counters scaled by a copy kernel of known size
+    (profiles/traffic.json): {"traffic": bytes or None, "traffic_detail": ...}.
+    The counter runs profile the first two layers of the rotation, so the
+    detail carries their algorithmic bytes and the measured/algorithmic ratio."""
     p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get(name)
-        except (OSError, ValueError):
-            return None
-    return None
+    try:
+        rec = json.loads(p.read_text()).get(name) if p.exists() else None
+    except (OSError, ValueError):
+        rec = None
+    if not rec:
+        return {"traffic": None}
+    return {"traffic": rec["bytes"],
+            "traffic_detail": {"layers_profiled": [l["layer"] for l in rec.get("layers", [])],
+                               "algorithmic_bytes_profiled": rec["algorithmic_bytes"],
+                               "measured_over_algorithmic": rec["ratio"], "source": rec.get("profile")}}
 
 
 if __name__ == "__main__":
