@@ -12,16 +12,19 @@
 //                order, so logits, ids and weights are bit-exact.  Extra
 //                blocks write the fp16 hi/lo activation planes and per-32
 //                sums; optionally the input is RMS-normalised first.
-//   KR route   : B > 1 only; one wave per token: top-10, coverage/prune, flags.
-//   K2 gate/up : one workgroup per (selection, 32 rows of F).  A selection
-//                computes its expert only if it is the expert's first
-//                eligible selection (no dispatch list needed), for every token
-//                that chose the expert.  B = 1 routes inline.  Products on the
-//                matrix cores (v_mfma_f32_16x16x32_f16) with exact integer
-//                weights; SwiGLU; mid rows written as fp16 hi/lo planes.
-//   K3 down    : item = (owning expert, 64 output rows): weight slab and the
-//                tokens' mid planes staged in shared memory, products on the
-//                matrix cores, weighted results to per-selection slots.
+//   KR route   : B > 1 only; one block: a wave per token (top-10,
+//                coverage/prune, flags), then the plan: the experts in order
+//                of their first eligible selection, each cut into tiles of up
+//                to 8 selections in token order.
+//   K2 gate/up : persistent; item = (tile, 32 rows of F), the shared
+//                expert's tiles first.  B = 1 routes inline (every workgroup
+//                routes the token; workgroup 0 publishes the plan).  Products
+//                on the matrix cores (v_mfma_f32_16x16x32_f16) with exact
+//                integer weights; SwiGLU; mid rows written as fp16 hi/lo
+//                planes with their 8-row sums.
+//   K3 down    : persistent; item = (tile, 64 output rows): weight slab and
+//                the tile's mid planes staged in shared memory, products on
+//                the matrix cores, weighted results to per-selection slots.
 //   K4 combine : router-rank sum of the 10 slots, the sigmoid-gated shared
 //                expert and the optional residual add.
 //
@@ -616,10 +619,10 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
     return y;
 }
 
-// Persistent; item = (owner, 64 output rows): the shared expert first, then
-// each routed expert at its owning selection (its first eligible selection).
-// An item's 64-row weight slab (contiguous) and its tokens' mid planes (8 at a
-// time) are staged in shared memory by direct global->shared copies; each of
+// Persistent; item = (tile, 64 output rows): the shared expert's tiles first,
+// then the plan's routed tiles.  An item's 64-row weight slab (contiguous) and
+// the tile's mid planes (up to 8 tokens) are staged in shared memory by direct
+// global->shared copies; each of
 // the 4 waves takes 16 rows (MFMA columns).  Results go to the selection's
 // slot, weighted by its routing weight (shared rows unweighted); the combine
 // kernel sums the slots in router-rank order.
