@@ -287,6 +287,114 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     if (lane < QG_TOP) { id_out = lds_i[lane]; w_out = num / total; }
 }
 
+// Two tokens per wave, one per 32-lane half h: the routing of qg_route_fast
+// with 16 logits per lane (lane l of half h holds row_h[l], row_h[l+32], ...).
+// The threshold is the 10th largest of the half's 32 lane maxima (counting
+// equal values separately), so at least 10 logits reach it; the candidates
+// >= T are ranked exactly as there.  On return lane 32h + k (k < 10) holds the
+// rank-k id and weight of token h, other lanes -1/0.  A half with a
+// non-finite logit gets -1/0; a half with more than 32 candidates (heavy
+// ties) is not routed here: fb_h is set (wave-uniform) and the caller routes
+// that token with qg_route_lane.  lds_v/lds_i: 64 floats / 64 ints of
+// wave-private shared memory (32 per half).
+QG_DEV void qg_route_pair(const float *row, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i, bool &fb0,
+                          bool &fb1) {
+    const int h = lane >> 5, l = lane & 31;
+    const unsigned long long hm = h ? 0xFFFFFFFF00000000ull : 0x00000000FFFFFFFFull;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    float v[16];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 16; i++) { v[i] = row[l + 32 * i]; bad |= !__builtin_isfinite(v[i]); }
+    const unsigned long long bb = __ballot(bad);
+    const bool bad0 = (bb & 0xFFFFFFFFull) != 0, bad1 = (bb >> 32) != 0, mybad = h ? bad1 : bad0;
+    if (mybad) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.0f;  // a harmless routing whose result is discarded
+    }
+    float lm = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) lm = fmaxf(lm, v[i]);
+    // threshold per half: walk down the distinct lane maxima until 10 lanes are covered
+    float largest = 0.0f, T = 0.0f, cur = lm;
+    int remaining = QG_TOP;
+    bool done = false;
+    for (int r = 0; r < QG_TOP; r++) {
+        const float rm = qg_row_max(cur);
+        const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 0));
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16));
+        const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 32));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 48));
+        const float m = h ? fmaxf(r2, r3) : fmaxf(r0, r1);
+        if (r == 0) largest = m;
+        const int cnt = __popcll(__ballot(cur == m) & hm);
+        if (!done) {
+            T = m;
+            if (cnt >= remaining) done = true;
+            else remaining -= cnt;
+        }
+        if (__ballot(!done) == 0) break;
+        cur = (!done && cur == m) ? -__builtin_inff() : cur;
+    }
+    // candidates v >= T, compacted in lane order within the half
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) c += v[i] >= T;
+    int pos = 0, tc0 = 0, tc1 = 0;
+#pragma unroll
+    for (int bit = 0; bit < 5; bit++) {
+        const unsigned long long b = __ballot((c >> bit) & 1);
+        pos += __popcll(b & hm & below) << bit;
+        tc0 += __popcll(b & 0xFFFFFFFFull) << bit;
+        tc1 += __popcll(b >> 32) << bit;
+    }
+    fb0 = !bad0 && tc0 > 32;
+    fb1 = !bad1 && tc1 > 32;
+    const int total_c = h ? tc1 : tc0;
+    const bool ok = total_c <= 32;
+    float *hv = lds_v + 32 * h;
+    int *hi = lds_i + 32 * h;
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (v[i] >= T) { hv[pos] = v[i]; hi[pos] = l + 32 * i; pos++; }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rank of candidate l among the half's candidates
+    const bool mine = ok && l < total_c;
+    const float cv = mine ? hv[l] : 0.0f;
+    const int ci = mine ? hi[l] : 0;
+    const int qm = max(tc0 <= 32 ? tc0 : 0, tc1 <= 32 ? tc1 : 0);
+    int rank = 0;
+    for (int q = 0; q < qm; q++) {  // candidate q of each half from its lane's registers (wave-uniform q)
+        const float o0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), q));
+        const float o1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), 32 + q));
+        const int i0 = __builtin_amdgcn_readlane(ci, q), i1 = __builtin_amdgcn_readlane(ci, 32 + q);
+        const float ov = h ? o1 : o0;
+        const int oi = h ? i1 : i0;
+        if (q < total_c) rank += (ov > cv) | ((ov == cv) & (oi < ci));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (mine && rank < QG_TOP) { hv[rank] = cv; hi[rank] = ci; }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool win = ok && !mybad && l < QG_TOP;
+    const float num = win ? qg_expf(hv[l] - largest) : 0.0f;
+    float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) {
+        t0 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), k));
+        t1 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), 32 + k));
+    }
+    id_out = win ? hi[l] : -1;
+    w_out = win ? num / (h ? t1 : t0) : 0.0f;
+}
+
 // Routing of one token written to ids[0..9] / w[0..9] by lanes 0..9
 // (lds_v/lds_i as for qg_route_fast).
 QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane, float *lds_v, int *lds_i) {
@@ -294,6 +402,25 @@ QG_DEV void qg_route_wave(int *ids, float *w, const float *s, int lane, float *l
     float wv;
     qg_route_fast(s, lane, id, wv, lds_v, lds_i);
     if (lane < QG_TOP) { ids[lane] = id; w[lane] = wv; }
+}
+
+// Routing of tokens ta (lanes 0-31) and tb (lanes 32-63; tb == ta routes one
+// token) of a [nt][ld] logit matrix, written to rows ta/tb of ids and w; a
+// half with heavy ties is routed again by the whole wave.
+QG_DEV void qg_route_wave2(int *ids, float *w, const float *logits, int ld, int ta, int tb, int lane, float *lds_v,
+                           int *lds_i) {
+    int id;
+    float wv;
+    bool fb0, fb1;
+    const int h = lane >> 5, k = lane & 31, t = h ? tb : ta;
+    qg_route_pair(logits + (size_t)t * ld, lane, id, wv, lds_v, lds_i, fb0, fb1);
+    if (k < QG_TOP && !(h ? fb1 : fb0) && (h == 0 || tb != ta)) {
+        ids[(size_t)t * QG_TOP + k] = id;
+        w[(size_t)t * QG_TOP + k] = wv;
+    }
+    if (fb0) qg_route_wave(ids + (size_t)ta * QG_TOP, w + (size_t)ta * QG_TOP, logits + (size_t)ta * ld, lane, lds_v, lds_i);
+    if (fb1 && tb != ta)
+        qg_route_wave(ids + (size_t)tb * QG_TOP, w + (size_t)tb * QG_TOP, logits + (size_t)tb * ld, lane, lds_v, lds_i);
 }
 
 // Coverage of one routed token (gpu.cu:467-483 with the 0.10 rule of
@@ -315,6 +442,32 @@ QG_DEV int qg_route_cover(int &id, float &wv, const uint8_t *resident, double th
 #pragma unroll
     for (int k = 0; k < QG_TOP; k++)
         if ((nb >> k) & 1) mass += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), k));
+    const int flag = bad ? 3 : !missing ? 0 : (thr > 0 && mass < thr) ? 1 : 2;
+    if (flag == 1 && nonres) { id = -id - 2; wv = 0.0f; }
+    return flag;
+}
+
+// qg_route_cover for the two tokens of qg_route_pair: lane 32h + k (k < 10)
+// holds rank k of token h; each half gets its own flag, missing and mass
+// (same rank-order double sum).
+QG_DEV int qg_route_cover_half(int &id, float &wv, const uint8_t *resident, double thr, int &missing, double &mass) {
+    const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int h = lane >> 5;
+    const bool mine = (lane & 31) < QG_TOP, valid = id >= 0 && id < QG_EXPERTS;
+    const bool nonres = mine && valid && resident && !resident[id];
+    const unsigned long long nb = __ballot(nonres), vb = __ballot(mine && !valid);
+    const uint32_t nb0 = (uint32_t)nb, nb1 = (uint32_t)(nb >> 32);
+    const bool bad = (h ? (uint32_t)(vb >> 32) : (uint32_t)vb) != 0u;
+    missing = __popc(h ? nb1 : nb0);
+    double m0 = 0.0, m1 = 0.0;
+#pragma unroll
+    for (int k = 0; k < QG_TOP; k++) {
+        const double a = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), k));
+        const double b = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), 32 + k));
+        if ((nb0 >> k) & 1) m0 += a;
+        if ((nb1 >> k) & 1) m1 += b;
+    }
+    mass = h ? m1 : m0;
     const int flag = bad ? 3 : !missing ? 0 : (thr > 0 && mass < thr) ? 1 : 2;
     if (flag == 1 && nonres) { id = -id - 2; wv = 0.0f; }
     return flag;

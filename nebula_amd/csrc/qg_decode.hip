@@ -43,6 +43,7 @@ constexpr int MS = MB * QG_TOP;           // 170 selections
 constexpr int ME = MS + MB;               // selection rows + shared-expert rows
 constexpr int INLINE_MAX = 1;             // tokens routed inside the gate/up kernel
 constexpr int GU_WGS = 512;               // gate/up grid cap (workgroups)
+constexpr int GU_NI = 8;                  // items per gate/up workgroup at most
 constexpr int DN_WGS = 1024;              // down grid cap (workgroups)
 
 // Routing results of the batch and its tile plan, written once per layer by
@@ -209,94 +210,34 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     }
 }
 
-// ---------------- KR: routing and the expert plan (B > 1), one block ----------------
+// ---------------- KR: routing (B > 1), one block per token ----------------
 struct RouteArgs {
     int nt; const float *logits; int ld;
     const uint8_t *resident; double thr;
     int *ids; float *w; uint8_t *flags_out; DecPlan *pl;
 };
 
-constexpr int RT_WAVES = 16;
-
-// One block: wave w routes tokens w, w + 16 (a second block with a
-// device-scope release/acquire hand-off measured slower); then the block
-// builds the plan: each expert's first eligible selection and eligible count
-// (shared-memory atomics), the experts in selection order with the prefix of
-// their tile counts (wave 0), and each expert's tiles (one wave per expert).
-__global__ __launch_bounds__(1024) void dec_route_kernel(RouteArgs A) {
-    __shared__ float s_rv[RT_WAVES][64];
-    __shared__ int s_ri[RT_WAVES][64];
-    __shared__ int s_ids[MS], s_flag[MB], s_first[QG_EXPERTS], s_cnt[QG_EXPERTS], s_own[MS], s_tbase[MS];
-    __shared__ int s_nown;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ns = A.nt * QG_TOP;
-    const unsigned long long below = (1ULL << lane) - 1ULL;
-    for (int i = tid; i < QG_EXPERTS; i += 64 * RT_WAVES) { s_first[i] = 0x7fffffff; s_cnt[i] = 0; }
-    // wave w routes tokens w, w + 16
-    for (int t = wave; t < A.nt; t += RT_WAVES) {
-        int id, missing;
-        float wv;
-        double mass;
-        qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv[wave], s_ri[wave]);
-        const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
-        if (lane < QG_TOP) {
-            A.ids[t * QG_TOP + lane] = id;
-            A.w[t * QG_TOP + lane] = wv;
-            s_ids[t * QG_TOP + lane] = id;
-        }
-        if (lane == 0) {
-            A.pl->flag[t] = flag;
-            A.pl->missing[t] = missing;
-            A.pl->mass[t] = mass;
-            s_flag[t] = flag;
-            if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
-        }
+// Block t routes token t with one wave (top-10, coverage/prune, flags); the
+// tokens run on separate CUs.  The expert plan is built from these results by
+// every gate/up workgroup (dec_gateup_kernel).
+__global__ __launch_bounds__(64) void dec_route_kernel(RouteArgs A) {
+    __shared__ float s_rv[64];
+    __shared__ int s_ri[64];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    int id, missing;
+    float wv;
+    double mass;
+    qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv, s_ri);
+    const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+    if (lane < QG_TOP) {
+        A.ids[t * QG_TOP + lane] = id;
+        A.w[t * QG_TOP + lane] = wv;
     }
-    __syncthreads();
-    for (int q = tid; q < ns; q += 64 * RT_WAVES) {
-        const int e = s_ids[q];
-        if (e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2) {
-            atomicMin(&s_first[e], q);
-            atomicAdd(&s_cnt[e], 1);
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
-        // experts in order of their first eligible selection, and the prefix of their tile counts
-        int n = 0, tiles = 0;
-        for (int c0 = 0; c0 < ns; c0 += 64) {
-            const int q = c0 + lane;
-            const int e = q < ns ? s_ids[q] : -1;
-            const bool own = e >= 0 && e < QG_EXPERTS && s_flag[q / QG_TOP] < 2 && s_first[e] == q;
-            const int nt8 = own ? (min(s_cnt[e], MB) + TILE_TOK - 1) / TILE_TOK : 0;  // 0..3
-            const unsigned long long b = __ballot(own), b0 = __ballot(nt8 & 1), b1 = __ballot(nt8 & 2);
-            if (own) {
-                const int k = n + __popcll(b & below);
-                s_own[k] = q;
-                s_tbase[k] = tiles + __popcll(b0 & below) + 2 * __popcll(b1 & below);
-            }
-            n += __popcll(b);
-            tiles += __popcll(b0) + 2 * __popcll(b1);
-        }
-        if (lane == 0) { s_nown = n; A.pl->n_tiles = tiles; }
-    }
-    __syncthreads();
-    // one wave per expert: its eligible selections in token order, 8 per tile
-    for (int k = wave; k < s_nown; k += RT_WAVES) {
-        const int e = s_ids[s_own[k]], tb = s_tbase[k];
-        int n = 0;
-        for (int c0 = 0; c0 < ns; c0 += 64) {
-            const int q = c0 + lane;
-            const bool m = q < ns && s_ids[q] == e && s_flag[q / QG_TOP] < 2;
-            const unsigned long long b = __ballot(m);
-            const int pos = n + __popcll(b & below);
-            if (m && pos < MB) A.pl->tile[tb + pos / TILE_TOK].q[pos % TILE_TOK] = q;
-            n += __popcll(b);
-        }
-        n = min(n, MB);
-        if (lane < (n + TILE_TOK - 1) / TILE_TOK) {
-            A.pl->tile[tb + lane].e = e;
-            A.pl->tile[tb + lane].n = min(TILE_TOK, n - TILE_TOK * lane);
-        }
+    if (lane == 0) {
+        A.pl->flag[t] = flag;
+        A.pl->missing[t] = missing;
+        A.pl->mass[t] = mass;
+        if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
     }
 }
 
@@ -346,8 +287,9 @@ static __host__ __device__ inline GuLds gu_lds(int D) {
 template <int NSB, bool INL>
 __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
-    __shared__ int s_item[2][2];     // per buffer: expert (-1: shared), token count (-1: no more items)
-    __shared__ int s_list[2][TILE_TOK];  // per buffer: the item's selections (shared expert: MS + t)
+    __shared__ int s_item[GU_NI][2];     // per item: expert (-1: shared), token count (-1: past the plan)
+    __shared__ int s_list[GU_NI][TILE_TOK];  // per item: its selections (shared expert: MS + t)
+    __shared__ int s_nitems;
     __shared__ float s_rv[64];
     __shared__ int s_ri[64];
     __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
@@ -390,36 +332,92 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         }
         __syncthreads();
     }
+    // B > 1: the plan from the routing kernel's ids and flags, built the same
+    // way in every workgroup (scratch in the stage area, free until the first
+    // stage): an expert's eligible selections form tiles of up to 8 in token
+    // order; experts in order of their first eligible selection.  A
+    // selection is eligible when its id is an expert and its token is
+    // computed here (flag 0 or 1; pruned selections carry -id-2).
+    uint32_t *p_mask = (uint32_t *)s_dyn;                 // [512] tokens choosing each expert
+    int *p_ids = (int *)(p_mask + QG_EXPERTS);            // [MS] eligible id or -1
+    int *p_tile = p_ids + MS;                             // [MAX_TILES] expert | tile-in-expert << 16
+    int *p_ntiles = p_tile + MAX_TILES;
+    if (!INL) {
+        const int ns = A.nt * QG_TOP;
+        for (int i = tid; i < QG_EXPERTS; i += 256) p_mask[i] = 0u;
+        int eq = -1;
+        if (tid < ns) {
+            const int id = A.ids[tid], fl = A.pl->flag[tid / QG_TOP];
+            eq = id >= 0 && id < QG_EXPERTS && fl < 2 ? id : -1;
+            p_ids[tid] = eq;
+        }
+        __syncthreads();
+        if (eq >= 0) atomicOr(&p_mask[eq], 1u << (tid / QG_TOP));
+        __syncthreads();
+        if (wave == 0) {
+            const unsigned long long below = (1ULL << lane) - 1ULL;
+            int tiles = 0;
+            for (int c0 = 0; c0 < ns; c0 += 64) {
+                const int q = c0 + lane, e = q < ns ? p_ids[q] : -1;
+                const uint32_t m = e >= 0 ? p_mask[e] : 0u;
+                // the expert's first eligible selection: its lowest token
+                const bool own = e >= 0 && (m & ((1u << (q / QG_TOP)) - 1u)) == 0u;
+                const int nt8 = own ? (__popc(m) + TILE_TOK - 1) / TILE_TOK : 0;  // 0..3
+                const unsigned long long b0 = __ballot(nt8 & 1), b1 = __ballot(nt8 & 2);
+                const int base = tiles + __popcll(b0 & below) + 2 * __popcll(b1 & below);
+                for (int x = 0; x < nt8; x++) p_tile[base + x] = e | (x << 16);
+                tiles += __popcll(b0) + 2 * __popcll(b1);
+            }
+            if (lane == 0) *p_ntiles = tiles;
+        }
+        __syncthreads();
+    }
     const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
-    // item -> expert (-1: shared), token count (-1: past the plan) and list, by
-    // wave 0 into buffer b (its plan loads stay in flight until the next wait)
-    auto resolve = [&](int item, int b) {
-        if (wave != 0) return;
-        const int T = item / rblocks;
+    // the workgroup's items (blockIdx.x + i * gridDim.x, i < GU_NI) -> expert
+    // (-1: shared), token count (-1: past the plan) and selection list, by
+    // wave 0: lane l takes item l / 8, list slot l % 8.  The workgroup with an
+    // item in a tile's first row block publishes the tile for the down kernel.
+    if (wave == 0) {
+        const int i = lane >> 3, slot = lane & 7, item = blockIdx.x + i * gridDim.x, T = item / rblocks;
         int e = -1, n = -1;
         if (T < sh_tiles) {
             n = min(TILE_TOK, A.nt - TILE_TOK * T);
-            if (lane < n) s_list[b][lane] = MS + TILE_TOK * T + lane;
+            if (slot < n) s_list[i][slot] = MS + TILE_TOK * T + slot;
         } else if (INL) {
             const int k = T - sh_tiles;
             if (k < s_nent) {
                 e = s_rid[k];
                 n = 1;
-                if (lane == 0) s_list[b][0] = s_rank[k];
+                if (slot == 0) s_list[i][0] = s_rank[k];
             }
-        } else if (T - sh_tiles < MAX_TILES) {
-            // one round trip: the tile count and the tile are independent loads
-            const int k = T - sh_tiles;
-            const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
-            const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
-            if (k < ntl) {
-                e = ek;
-                n = nk;
-                if (lane < nk) s_list[b][lane] = qk;
+        } else if (T - sh_tiles < *p_ntiles) {
+            const int k = T - sh_tiles, te = p_tile[k], jt = te >> 16;
+            e = te & 0xffff;
+            const uint32_t m = p_mask[e];
+            n = min(TILE_TOK, __popc(m) - TILE_TOK * jt);
+            int q = -1;
+            if (slot < n) {
+                // the (8 jt + slot)-th token choosing e, and the rank it gave e
+                uint32_t mm = m;
+                for (int x = TILE_TOK * jt + slot; x > 0; x--) mm &= mm - 1u;
+                const int t = __builtin_ctz(mm);
+                int r = 0;
+#pragma unroll
+                for (int rr = 0; rr < QG_TOP; rr++) r = p_ids[t * QG_TOP + rr] == e ? rr : r;
+                q = t * QG_TOP + r;
+                s_list[i][slot] = q;
+            }
+            if (item % rblocks == 0) {
+                if (slot < n) A.pl->tile[k].q[slot] = q;
+                if (slot == 0) { A.pl->tile[k].e = e; A.pl->tile[k].n = n; }
             }
         }
-        if (lane == 0) { s_item[b][0] = e; s_item[b][1] = n; }
-    };
+        if (!INL && blockIdx.x == 0 && lane == 0) A.pl->n_tiles = *p_ntiles;
+        if (slot == 0) { s_item[i][0] = e; s_item[i][1] = n; }
+        // items ascend in tile order, so the valid ones are a prefix
+        const unsigned long long v = __ballot(slot == 0 && n >= 0);
+        if (lane == 0) s_nitems = __popcll(v);
+    }
     auto mats = [&](int e, const uint8_t *&gm, const uint8_t *&um) {
         gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
         um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
@@ -444,38 +442,45 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         for (int q = 0; q * 64 < 16 * HROW; q++) {
             const int slot = q * 64 + lane, rr = slot / HROW, sb = slot - rr * HROW;
             if (rr < 16 && sb < NSB)
-                dma16((rr < 8 ? gm : um) + (size_t)(wrow0 + (rr & 7)) * A.rb + sb * 144, hbuf + (size_t)q * 1024);
+                dma16_ordered((rr < 8 ? gm : um) + (size_t)(wrow0 + (rr & 7)) * A.rb + sb * 144, hbuf + (size_t)q * 1024);
         }
         for (int q = wave; q < 2 * n * bpr; q += 4) {
             const int r = q / bpr, b = q - r * bpr;
             const int sl = list[r >> 1], tok = e < 0 ? sl - MS : sl / QG_TOP;
-            dma16(A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)(b * 64 + lane) * 8, act + (size_t)r * LY.arow + b * 512);
+            dma16_ordered(A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)(b * 64 + lane) * 8, act + (size_t)r * LY.arow + b * 512);
         }
         for (int q = wave; q * 64 < 2 * n * (cps + 1); q += 4) {
             const int slot = q * 64 + lane, r = slot / (cps + 1), c = slot - r * (cps + 1);
             if (r < 2 * n && c < cps) {
                 const int sl = list[r >> 1], tok = e < 0 ? sl - MS : sl / QG_TOP;
-                dma16(A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)c * 8, acts + (size_t)q * 512);
+                dma16_ordered(A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)c * 8, acts + (size_t)q * 512);
             }
         }
     };
     // software pipeline over the workgroup's items: the next item's weight rows
-    // load into registers while the current item's products run
-    int item = blockIdx.x, buf = 0;
-    resolve(item, 0);
+    // load into registers while the current item's products run.  The first
+    // item's stage is issued before its weight rows, so the products start
+    // once the stage has landed and each superblock's rows wait only for
+    // themselves (loads complete in issue order).
     __syncthreads();
-    if (s_item[0][1] < 0) return;  // block-uniform
+    const int nit = s_nitems;
+    if (nit == 0) return;  // block-uniform
     uint4 c0[NSB], c1[NSB], n0[NSB], n1[NSB];
-    load_weights(s_item[0][0], item % rblocks, c0, c1);
-    stage(s_item[0][0], item % rblocks, s_item[0][1], s_list[0]);
-    for (;;) {
-        const int next = item + gridDim.x;
-        resolve(next, buf ^ 1);
-        wait_vmem();
+    stage(s_item[0][0], blockIdx.x % rblocks, s_item[0][1], s_list[0]);
+    asm volatile("" ::: "memory");
+    load_weights(s_item[0][0], blockIdx.x % rblocks, c0, c1);
+    // one item; the first is peeled (FIRST) so that the compiler's wait
+    // before its shared-memory reads counts only the stage, not the weight
+    // rows issued after it
+    auto process = [&](int it, auto first) -> bool {
+        constexpr bool FIRST = decltype(first)::value;
+        const int item = blockIdx.x + it * gridDim.x;
+        if (FIRST) wait_vmem_but<2 * NSB>();
+        else wait_vmem();
         __syncthreads();
-        const int e = s_item[buf][0], n = s_item[buf][1], rb0 = item % rblocks;
-        const int e2 = s_item[buf ^ 1][0], n2 = s_item[buf ^ 1][1];
-        if (n2 >= 0) load_weights(e2, next % rblocks, n0, n1);
+        const int e = s_item[it][0], n = s_item[it][1], rb0 = item % rblocks;
+        const bool more = it + 1 < nit;
+        if (more) load_weights(s_item[it + 1][0], (item + gridDim.x) % rblocks, n0, n1);
         const bool shared = e < 0;
         const int fmt = shared ? A.sh_fmt : A.fmt;
         const int pos = plane_pos(fmt, rb0 * GU_WROWS + wave * GU_ROWS + (j & 7));
@@ -518,7 +523,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
             s8 += __shfl_xor(s8, 4);
             const int idx = 2 * kq + t2;
             if (j < 8 && idx < n) {
-                const int sl = s_list[buf][idx];
+                const int sl = s_list[it][idx];
                 _Float16 *mp = A.midp + (size_t)sl * 2 * A.F;
                 const _Float16 hv = (_Float16)m;
                 mp[pos] = hv;
@@ -526,13 +531,15 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
                 if (j == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + rb0 * 4 + wave] = s8;
             }
         }
-        __syncthreads();  // the stage, the headers and this item's buffer are free
-        if (n2 < 0) break;  // block-uniform
-        stage(e2, next % rblocks, n2, s_list[buf ^ 1]);
+        __syncthreads();  // the stage and the headers are free
+        if (!more) return false;  // block-uniform
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) { c0[sb] = n0[sb]; c1[sb] = n1[sb]; }
-        item = next;
-        buf ^= 1;
+        stage(s_item[it + 1][0], (item + gridDim.x) % rblocks, s_item[it + 1][1], s_list[it + 1]);
+        return true;
+    };
+    if (!process(0, std::true_type{})) return;
+    for (int it = 1; process(it, std::false_type{}); it++) {
     }
 }
 
@@ -835,7 +842,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const bool inl = nt <= INLINE_MAX;
     if (!inl) {
         RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, pl};
-        dec_launch(1, dec_route_kernel, dim3(1), dim3(64 * RT_WAVES), 0, s, RA);
+        dec_launch(1, dec_route_kernel, dim3(nt), dim3(64), 0, s, RA);
         if ((rc = hipGetLastError())) return rc;
     }
     _Float16 *midp = (_Float16 *)(ws + lay.midp);
@@ -847,7 +854,8 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     // upper bound of the tiles: the shared expert's, and every selection its own tile
     const int tiles = (sh ? (nt + TILE_TOK - 1) / TILE_TOK : 0) + nt * QG_TOP;
     const int items = tiles * (F / GU_WROWS);
-    const int nwg = items < GU_WGS ? items : GU_WGS;
+    int nwg = items < GU_WGS ? items : GU_WGS;
+    if (nwg * GU_NI < items) nwg = (items + GU_NI - 1) / GU_NI;  // each workgroup resolves GU_NI items at most
     const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
     if (D == 2048) {
         if (inl) dec_launch(2, dec_gateup_kernel<8, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);

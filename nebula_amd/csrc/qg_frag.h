@@ -68,7 +68,28 @@ typedef __attribute__((address_space(3))) void qg_lds_void;
 QG_DEV void dma16(const void *g, void *lds_base) {
     __builtin_amdgcn_global_load_lds(g, (qg_lds_void *)lds_base, 16, 0, 0);
 }
+// The same copy issued from inline assembly: it stays in program order with
+// the surrounding memory operations and the compiler does not track it, so
+// it adds no waits of its own before later shared-memory reads; the caller
+// waits for it with wait_vmem or wait_vmem_but before the data is read (and
+// makes it visible to the other waves with a barrier).  M0, which holds the
+// shared-memory base of the copy, is restored afterwards.
+QG_DEV void dma16_ordered(const void *g, void *lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(qg_lds_void *)lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(base)
+                 : "memory");
+}
 QG_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order), leaving the other counters alone.
+template <int N>
+QG_DEV void wait_vmem_but() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 // 1/sqrt(mean(x^2) + eps) of one row, summed lane-strided then across the
 // wave; every caller runs this same code, so all blocks agree bit for bit.

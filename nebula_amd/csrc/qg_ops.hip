@@ -152,16 +152,16 @@ __global__ void binary_kernel(float *o, const float *a, const float *b, int n, i
 }
 
 // ------------------------------------------------------------------------
-// Routing (gpu.cu:456-465).  One wave per token (qg_route_fast): the 10
-// winners by value with the lowest index among equal values (the reference's
-// strict-greater scan from index 0), numerators exp(s - max) summed in rank
-// order, then divided by the sum.
+// Routing (gpu.cu:456-465).  One wave per pair of tokens (qg_route_pair, a
+// 32-lane half per token): the 10 winners by value with the lowest index
+// among equal values (the reference's strict-greater scan from index 0),
+// numerators exp(s - max) summed in rank order, then divided by the sum.
 // ------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void route_kernel(int *ids, float *weights, const float *logits, int nt, int ld) {
     __shared__ float s_v[64];
     __shared__ int s_i[64];
-    const int t = blockIdx.x;
-    qg_route_wave(ids + (size_t)t * QG_TOP, weights + (size_t)t * QG_TOP, logits + (size_t)t * ld, threadIdx.x, s_v, s_i);
+    const int ta = 2 * blockIdx.x, tb = min(ta + 1, nt - 1);
+    qg_route_wave2(ids, weights, logits, ld, ta, tb, threadIdx.x, s_v, s_i);
 }
 
 // Pruning (gpu.cu:467-483), one thread per token, device atomics for the
@@ -310,7 +310,7 @@ int qg_binary(float *o, const float *a, const float *b, int n, int op) {  // gpu
 
 int qg_route(int *ids, float *w, const float *logits, int nt) {  // gpu.cu:466
     if (nt < 1 || nt > QG_MAX_TOKENS || !ids || !w || !logits) return hipErrorInvalidValue;
-    route_kernel<<<nt, 64, 0, qg_stream()>>>(ids, w, logits, nt, QG_EXPERTS);
+    route_kernel<<<(nt + 1) / 2, 64, 0, qg_stream()>>>(ids, w, logits, nt, QG_EXPERTS);
     return hipGetLastError();
 }
 

@@ -96,13 +96,18 @@ def test_route_matches_oracle_and_kat(qgl):
     logits = (rng.normal(size=(300, 512))).astype(np.float32)
     logits[0] = 0
     logits[1, 100:120] = logits[1, 5]  # ties
+    # heavy ties (more candidates than a 32-lane half ranks) in either half of a token pair
+    logits[2, 3:200:3] = logits[2].max() + 1.0
+    logits[9, 40:90] = logits[9].max() + 0.5
+    logits[10, :] = 0.25
     dl = Device(logits)
     ids, w = Device(shape=(300, 10), dtype=np.int32), Device(shape=(300, 10), dtype=np.float32)
-    say("route 300 tokens")
-    call("route", ids.p, w.p, dl.p, 300)
     oi, ow = O.route(logits)
-    np.testing.assert_array_equal(ids.get(), oi)
-    np.testing.assert_array_equal(w.get().view('u4'), ow.view('u4'))
+    for nt in (300, 299, 1):
+        say(f"route {nt} tokens")
+        call("route", ids.p, w.p, dl.p, nt)
+        np.testing.assert_array_equal(ids.get()[:nt], oi[:nt])
+        np.testing.assert_array_equal(w.get()[:nt].view('u4'), ow[:nt].view('u4'))
     np.testing.assert_array_equal(ids.get()[:, :10], np.argsort(-logits, axis=1, kind='stable')[:, :10])
     logits[5, 7] = np.nan
     logits[6, 511] = -np.inf
@@ -405,6 +410,35 @@ def test_layer_partial_residency_mixed_flags(layer1, nt):
         say(f"  flags {counts}, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
     finally:
         L.desc = saved
+
+
+@pytest.mark.parametrize("nt,ties", [(5, 40), (17, 40), (17, 70)])
+def test_layer_router_heavy_ties(layer1, nt, ties):
+    """`ties` identical router rows that beat every other logit of every
+    token: more tied candidates than a 32-lane half ranks (40) or than a whole
+    wave ranks (70), so the routing kernel's whole-wave paths run.  Ids,
+    weights and flags stay exact; every token picks experts 0..9, so each
+    expert carries the whole batch (several tiles)."""
+    L, H = layer1
+    x = synth.inputs(91, nt, 2048, correlated=True)
+    u = x.mean(axis=0)
+    u /= np.linalg.norm(u)
+    proj = x @ u
+    assert proj.min() > 1.0
+    natural = (x @ H.router.reshape(512, 2048).T).max()
+    router = H.router.copy()
+    router.reshape(512, 2048)[:ties] = ((natural + 1.0) / proj.min() * u).astype(np.float32)
+    rdev = Device(router)
+    desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    desc.router = rdev.p
+    saved_desc, saved_router = L.desc, H.router
+    L.desc, H.router = desc, router
+    try:
+        _, oids, _, _, _, _ = H.forward(x)
+        np.testing.assert_array_equal(oids, np.tile(np.arange(10), (nt, 1)))
+        _check_layer(L, H, x, f"heavy ties {ties} B={nt}")
+    finally:
+        L.desc, H.router = saved_desc, saved_router
 
 
 @pytest.mark.parametrize("nt", [2, 8])
