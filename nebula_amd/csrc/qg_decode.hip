@@ -255,31 +255,318 @@ struct GuArgs {
 constexpr int GU_ROWS = 8;           // F rows of gate and of up per wave
 constexpr int GU_WROWS = 4 * GU_ROWS; // F rows per workgroup (4 waves)
 
+// ---- pieces shared by the gate/up kernels ----
+
+// Warm this XCD's L2 with the batch's activation and sum planes while the
+// plan is built (workgroups b, b + 8, ... share an XCD; each takes 4 KB); the
+// returned word is consumed once the loads are needed to have landed.
+QG_DEV uint32_t gu_warm(const GuArgs &A, int tid) {
+    uint32_t warm = 0;
+    const size_t pb = (size_t)A.nt * 2 * A.D * 2, tb = pb + (size_t)A.nt * 2 * (A.D / 32) * 2;
+    const size_t step = (size_t)((gridDim.x + 7) / 8) * 4096;
+    for (size_t off = (size_t)(blockIdx.x / 8) * 4096 + (size_t)tid * 16; off < tb; off += step) {
+        const uint4 v = off < pb ? *(const uint4 *)((const uint8_t *)A.xp + off)
+                                 : *(const uint4 *)((const uint8_t *)A.xsp + (off - pb));
+        warm ^= v.x;
+    }
+    return warm;
+}
+
+// One token (wave 0 of every workgroup): its routing; entry k = k-th eligible
+// rank (s_rank, s_rid, *s_nent).  Workgroup 0 publishes ids, weights, flags
+// and the plan.
+QG_DEV void gu_route_inline(const GuArgs &A, int lane, float *s_rv, int *s_ri, int *s_rank, int *s_rid, int *s_nent) {
+    int id, missing;
+    float wv;
+    double mass;
+    qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri);
+    const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+    const bool el = lane < QG_TOP && flag < 2 && id >= 0 && id < QG_EXPERTS;
+    const unsigned long long b = __ballot(el);
+    const int k = __popcll(b & ((1ULL << lane) - 1ULL));
+    if (el) { s_rank[k] = lane; s_rid[k] = id; }
+    if (lane == 0) *s_nent = __popcll(b);
+    if (blockIdx.x == 0) {
+        if (lane < QG_TOP) { A.ids[lane] = id; A.w[lane] = wv; }
+        if (el) { A.pl->tile[k].e = id; A.pl->tile[k].n = 1; A.pl->tile[k].q[0] = lane; }
+        if (lane == 0) {
+            A.pl->flag[0] = flag;
+            A.pl->missing[0] = missing;
+            A.pl->mass[0] = mass;
+            A.pl->n_tiles = __popcll(b);
+            if (A.flags_out) A.flags_out[0] = (uint8_t)flag;
+        }
+    }
+}
+
+// B > 1: the plan from the routing kernel's ids and flags, built the same way
+// in every workgroup (256 threads; scratch in shared memory): an expert's
+// eligible selections form tiles of up to 8 in token order, experts in order
+// of their first eligible selection.  A selection is eligible when its id is
+// an expert and its token is computed here (flag 0 or 1; pruned selections
+// carry -id-2).  p_mask[512]: tokens choosing each expert; p_ids[MS]:
+// eligible id or -1; p_tile[MAX_TILES]: expert | tile-in-expert << 16.
+struct GuPlan { uint32_t *mask; int *ids, *tile, *ntiles; };
+QG_DEV GuPlan gu_plan_at(void *base) {
+    GuPlan P;
+    P.mask = (uint32_t *)base;
+    P.ids = (int *)(P.mask + QG_EXPERTS);
+    P.tile = P.ids + MS;
+    P.ntiles = P.tile + MAX_TILES;
+    return P;
+}
+constexpr int GU_PLAN_BYTES = (QG_EXPERTS + MS + MAX_TILES + 1) * 4;
+QG_DEV void gu_build_plan(const GuArgs &A, int tid, const GuPlan &P) {
+    const int wave = tid >> 6, lane = tid & 63, ns = A.nt * QG_TOP;
+    for (int i = tid; i < QG_EXPERTS; i += 256) P.mask[i] = 0u;
+    int eq = -1;
+    if (tid < ns) {
+        const int id = A.ids[tid], fl = A.pl->flag[tid / QG_TOP];
+        eq = id >= 0 && id < QG_EXPERTS && fl < 2 ? id : -1;
+        P.ids[tid] = eq;
+    }
+    __syncthreads();
+    if (eq >= 0) atomicOr(&P.mask[eq], 1u << (tid / QG_TOP));
+    __syncthreads();
+    if (wave == 0) {
+        const unsigned long long below = (1ULL << lane) - 1ULL;
+        int tiles = 0;
+        for (int c0 = 0; c0 < ns; c0 += 64) {
+            const int q = c0 + lane, e = q < ns ? P.ids[q] : -1;
+            const uint32_t m = e >= 0 ? P.mask[e] : 0u;
+            // the expert's first eligible selection: its lowest token
+            const bool own = e >= 0 && (m & ((1u << (q / QG_TOP)) - 1u)) == 0u;
+            const int nt8 = own ? (__popc(m) + TILE_TOK - 1) / TILE_TOK : 0;  // 0..3
+            const unsigned long long b0 = __ballot(nt8 & 1), b1 = __ballot(nt8 & 2);
+            const int base = tiles + __popcll(b0 & below) + 2 * __popcll(b1 & below);
+            for (int x = 0; x < nt8; x++) P.tile[base + x] = e | (x << 16);
+            tiles += __popcll(b0) + 2 * __popcll(b1);
+        }
+        if (lane == 0) *P.ntiles = tiles;
+    }
+    __syncthreads();
+}
+
+// Tile T of the layer (the shared expert's tiles first): expert e (-1:
+// shared), token count n (-1: past the plan) and, for list slot < n, its
+// selection q (shared expert: MS + token).  With `publish`, the routed tile is
+// written to the plan for the down kernel.
+template <bool INL>
+QG_DEV void gu_tile(const GuArgs &A, int T, int sh_tiles, int slot, const int *s_rank, const int *s_rid, int nent,
+                    const GuPlan &P, bool publish, int &e, int &n, int &q) {
+    e = -1;
+    n = -1;
+    q = -1;
+    if (T < sh_tiles) {
+        n = min(TILE_TOK, A.nt - TILE_TOK * T);
+        if (slot < n) q = MS + TILE_TOK * T + slot;
+    } else if (INL) {
+        const int k = T - sh_tiles;
+        if (k < nent) {
+            e = s_rid[k];
+            n = 1;
+            if (slot == 0) q = s_rank[k];
+        }
+    } else if (T - sh_tiles < *P.ntiles) {
+        const int k = T - sh_tiles, te = P.tile[k], jt = te >> 16;
+        e = te & 0xffff;
+        const uint32_t m = P.mask[e];
+        n = min(TILE_TOK, __popc(m) - TILE_TOK * jt);
+        if (slot < n) {
+            // the (8 jt + slot)-th token choosing e, and the rank it gave e
+            uint32_t mm = m;
+            for (int x = TILE_TOK * jt + slot; x > 0; x--) mm &= mm - 1u;
+            const int t = __builtin_ctz(mm);
+            int r = 0;
+#pragma unroll
+            for (int rr = 0; rr < QG_TOP; rr++) r = P.ids[t * QG_TOP + rr] == e ? rr : r;
+            q = t * QG_TOP + r;
+        }
+        if (publish) {
+            if (slot < n) A.pl->tile[k].q[slot] = q;
+            if (slot == 0) { A.pl->tile[k].e = e; A.pl->tile[k].n = n; }
+        }
+    }
+}
+
+// ---- K2 at D = 2048: pipelined K split ----
+constexpr int GU2_ROWS = 16;                  // F rows per item (16 gate + 16 up weight rows)
+constexpr int GU2_SL = 32 * 18;              // 16-byte slots per item and wave: 32 rows x 2 superblocks of 144 bytes
+constexpr int GU2_NT = 4;                     // tiles a workgroup's item range may touch
+constexpr size_t GU2_LDS = (size_t)4 * 2 * GU2_SL * 16;  // 4 waves x 2 buffers
+
+// Persistent: the layer's items (tile, 16 F rows) in tile order, split into
+// contiguous ranges, one per workgroup, so a workgroup keeps a tile's
+// activation fragments in registers across its row blocks.  Wave w takes
+// superblocks 2w, 2w + 1 (the K split) of the item's 32 weight rows (column
+// block 0: gate rows, 1: up rows): their bytes come by direct global->shared
+// copies into the wave's own double buffer (each row's 288 bytes one
+// contiguous run, rotated by row group to spread the fragment reads), the next
+// item's copies in flight while this item's products run; partial sums meet
+// in shared memory and wave 0 applies SwiGLU.
+template <bool INL>
+__global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    __shared__ int s_te[GU2_NT][2];          // per tile of the range: expert, token count
+    __shared__ int s_tl[GU2_NT][TILE_TOK];   // and its selections
+    __shared__ float s_rv[64];
+    __shared__ int s_ri[64];
+    __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
+    __shared__ int s_nent;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    const int D = A.D, D32 = D / 32, RBK = A.F / GU2_ROWS;
+    const uint32_t warm = gu_warm(A, tid);
+    const GuPlan P = gu_plan_at(s_dyn);
+    if (INL) {
+        if (wave == 0) gu_route_inline(A, lane, s_rv, s_ri, s_rank, s_rid, &s_nent);
+        __syncthreads();
+    } else {
+        gu_build_plan(A, tid, P);
+    }
+    const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    const int ntl = sh_tiles + (INL ? s_nent : *P.ntiles), N = ntl * RBK;
+    const int i0 = (int)((long long)N * blockIdx.x / gridDim.x), i1 = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    const int T0 = i0 / RBK;
+    if (wave == 0) {
+        // the range's tiles (lane l: tile T0 + l / 8, list slot l % 8); the
+        // workgroup holding a tile's first row block publishes it
+        const int ti = lane >> 3, slot = lane & 7, T = T0 + ti;
+        if (ti < GU2_NT && i1 > i0 && T * RBK < i1) {
+            int e, n, q;
+            const bool pub = T * RBK >= i0;
+            gu_tile<INL>(A, T, sh_tiles, slot, s_rank, s_rid, INL ? s_nent : 0, P, pub, e, n, q);
+            if (slot < n) s_tl[ti][slot] = q;
+            if (slot == 0) { s_te[ti][0] = e; s_te[ti][1] = n; }
+        }
+        if (!INL && blockIdx.x == 0 && lane == 0) A.pl->n_tiles = *P.ntiles;
+    }
+    __syncthreads();
+    asm volatile("" ::"v"(warm));  // the warming loads have landed
+    if (i1 <= i0) return;  // block-uniform
+    uint4 *wl = s_dyn + (size_t)wave * 2 * GU2_SL;  // this wave's two buffers
+    // item -> the wave's copies into buffer b
+    auto copy_item = [&](int item, int b) {
+        const int ti = item / RBK - T0, rb = item % RBK, e = s_te[ti][0];
+        const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
+        const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
+#pragma unroll
+        for (int i = 0; i < GU2_SL / 64; i++) {
+            // slot sl = 18 row + position; the row's 288 bytes (its two
+            // superblocks, headers included) are one contiguous run, rotated
+            // by 2 (row / 8) positions so the 16 rows of a fragment read
+            // spread over the banks
+            const int sl = i * 64 + lane, row = sl / 18, pc = sl - 18 * row;
+            const int c = pc - 2 * (row >> 3) + (pc < 2 * (row >> 3) ? 18 : 0);
+            dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 288 + 16 * c,
+                          wl + (size_t)b * GU2_SL + i * 64);
+        }
+    };
+    copy_item(i0, 0);
+    int cur = -1;
+    qg_half8 af[2][8], sf[2];
+    const int gA = 2 * (kq >> 1), gB = gA + 4;
+    for (int k = 0; i0 + k < i1; k++) {
+        const int item = i0 + k, ti = item / RBK - T0, rb = item % RBK, b = k & 1;
+        const int e = s_te[ti][0], n = s_te[ti][1];
+        if (ti != cur) {
+            // the tile's activation fragments for this wave's superblocks:
+            // plane row r = (token r/2, plane r%2)
+            const int r = 2 * min(j >> 1, n - 1) + (j & 1), sl0 = s_tl[ti][r >> 1];
+            const int tok = e < 0 ? sl0 - MS : sl0 / QG_TOP;
+            const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 512 + kq * 8;
+            const _Float16 *xs = A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)wave * 16;
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++) {
+#pragma unroll
+                for (int m = 0; m < 8; m++) af[sb][m] = ld_frag(xr + sb * 256 + m * 32);
+                sf[sb] = kq ? qg_half8{} : ld_frag(xs + sb * 8);
+            }
+            cur = ti;
+        }
+        wait_vmem();  // this item's copies (and fragments) have landed
+        if (i0 + k + 1 < i1) copy_item(item + 1, b ^ 1);
+        const uint4 *wb = wl + (size_t)b * GU2_SL;
+        qg_f4 y[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+            y[cb] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int row = cb * 16 + j, rot = 2 * (row >> 3);
+            // piece c of the row (0: header 0, 1..8: nibbles 0, 9: header 1, 10..17: nibbles 1)
+            auto piece = [&](int c) { const int x = c + rot; return wb[18 * row + (x >= 18 ? x - 18 : x)]; };
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++) {
+                const Q4kHeader h = q4k_header(piece(9 * sb));
+                const uint4 ch0 = piece(9 * sb + 1 + kq), ch1 = piece(9 * sb + 5 + kq);
+                qg_f4 p0 = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, p1 = p0, mm = p0;
+#pragma unroll
+                for (int f = 0; f < 4; f++) {
+                    p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][f], q4k_chunk_frag(ch0, f, q4k_sh(h, gA + (f >> 1))), p0, 0, 0, 0);
+                    p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][4 + f], q4k_chunk_frag(ch1, f, q4k_sh(h, gB + (f >> 1))), p1, 0, 0, 0);
+                }
+                mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf[sb], q4k_min_frag(h), mm, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[cb][i] = __builtin_fmaf(h.d, p0[i] + p1[i], __builtin_fmaf(-h.dmin, mm[i], y[cb][i]));
+            }
+        }
+        // partial sums into this wave's buffer b (its reads are done)
+        float4 *pw = (float4 *)(wl + (size_t)b * GU2_SL);
+        pw[lane] = make_float4(y[0][0], y[0][1], y[0][2], y[0][3]);
+        pw[64 + lane] = make_float4(y[1][0], y[1][1], y[1][2], y[1][3]);
+        __syncthreads();
+        if (wave == 0) {
+            // the 4 partials in wave order; F row rb 16 + j
+            float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float4 *pr = (const float4 *)(s_dyn + (size_t)w * 2 * GU2_SL + (size_t)b * GU2_SL);
+                const float4 ga = pr[lane], ua = pr[64 + lane];
+                g[0] += ga.x; g[1] += ga.y; g[2] += ga.z; g[3] += ga.w;
+                u[0] += ua.x; u[1] += ua.y; u[2] += ua.z; u[3] += ua.w;
+            }
+            const int fmt = e < 0 ? A.sh_fmt : A.fmt, frow = rb * GU2_ROWS + j, pos = plane_pos(fmt, frow);
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
+                const float m = qg_swiglu_fast(g[2 * t2] + g[2 * t2 + 1], u[2 * t2] + u[2 * t2 + 1]);
+                float s8 = m;  // sum over the 8 rows of this lane's group
+                s8 += __shfl_xor(s8, 1);
+                s8 += __shfl_xor(s8, 2);
+                s8 += __shfl_xor(s8, 4);
+                const int idx = 2 * kq + t2;
+                if (idx < n) {
+                    const int sl = s_tl[ti][idx];
+                    _Float16 *mp = A.midp + (size_t)sl * 2 * A.F;
+                    const _Float16 hv = (_Float16)m;
+                    mp[pos] = hv;
+                    mp[A.F + pos] = (_Float16)(m - (float)hv);
+                    if ((j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
+                }
+            }
+        }
+        __syncthreads();  // buffer b is free for the item after next
+    }
+}
+
 // Shared-memory layout of the gate/up kernel (fp16 units): 16 staged plane
-// rows (8 tokens x {hi, lo}) of D values each padded by 8, 16 rows of D/32
-// group sums each padded by 8, then per wave 16 rows of NSB Q4_K headers (16
-// bytes each) padded by one header.  The padding puts the 16 rows of every
+// rows (8 tokens x {hi, lo}) of D values each padded by 8, then 16 rows of
+// D/32 group sums each padded by 8.  The padding puts the 16 rows of every
 // fragment read in distinct banks while each read keeps a constant offset.
 // Copies into it are direct global->shared with the lanes of padding slots
-// masked off.
-struct GuLds { int arow, srow, hrow, sums, hdr, hdr_wave, total; };  // strides and offsets in fp16 units
+// masked off.  Before the first stage the area holds the plan scratch.
+struct GuLds { int arow, srow, sums, total; };  // strides and offsets in fp16 units
 static __host__ __device__ inline GuLds gu_lds(int D) {
     GuLds L;
     L.arow = D + 8;
     L.srow = D / 32 + 8;
-    L.hrow = 8 * (D / 256 + 1);
     L.sums = 16 * L.arow;
-    L.hdr = L.sums + 16 * L.srow;
-    L.hdr_wave = 16 * L.hrow;
-    L.total = L.hdr + 4 * L.hdr_wave;
+    L.total = L.sums + 16 * L.srow;
     return L;
 }
 
 // Persistent; item = (tile, 32 F rows): the shared expert's tiles first (no
 // routing needed), then the plan's routed tiles.  The item's weight rows go to
-// registers (8 gate and the same 8 up rows per wave) and their headers to
-// shared memory, while the tile's activation planes and sum planes are staged
-// by direct global->shared copies; then the products on the matrix cores.  In
+// registers (8 gate and the same 8 up rows per wave, headers included), while
+// the tile's activation planes and sum planes are staged by direct
+// global->shared copies; then the products on the matrix cores.  In
 // a wave, MFMA columns 0..7 are the gate rows and 8..15 the up rows, so lanes
 // l and l^8 hold gate and up of one (row, token) pair.  Tiles of one expert
 // and row block are items rblocks apart, on workgroups of one XCD, so their
@@ -298,79 +585,17 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int D = A.D, D32 = D / 32, cps = D / 256, bpr = D / 512;
     if (tid < NSB) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first barrier
-    const int rblocks = A.F / GU_WROWS, sh = A.sh_gate ? 1 : 0;
-    constexpr int HROW = NSB + 1;    // header slots per padded row
+    const int rblocks = A.F / GU_WROWS;
     const GuLds LY = gu_lds(D);
     _Float16 *act = (_Float16 *)s_dyn;
     _Float16 *acts = act + LY.sums;
-    uint8_t *hbuf = (uint8_t *)(act + LY.hdr + wave * LY.hdr_wave);
+    const uint32_t warm = gu_warm(A, tid);
+    const GuPlan P = gu_plan_at(s_dyn);  // scratch in the stage area, free until the first stage
     if (INL) {
-        // one token: every workgroup routes it (wave 0); workgroup 0 publishes
-        // the results and the plan (entry k = k-th eligible rank)
-        if (wave == 0) {
-            int id, missing;
-            float wv;
-            double mass;
-            qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri);
-            const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
-            const bool el = lane < QG_TOP && flag < 2 && id >= 0 && id < QG_EXPERTS;
-            const unsigned long long b = __ballot(el);
-            const int k = __popcll(b & ((1ULL << lane) - 1ULL));
-            if (el) { s_rank[k] = lane; s_rid[k] = id; }
-            if (lane == 0) s_nent = __popcll(b);
-            if (blockIdx.x == 0) {
-                if (lane < QG_TOP) { A.ids[lane] = id; A.w[lane] = wv; }
-                if (el) { A.pl->tile[k].e = id; A.pl->tile[k].n = 1; A.pl->tile[k].q[0] = lane; }
-                if (lane == 0) {
-                    A.pl->flag[0] = flag;
-                    A.pl->missing[0] = missing;
-                    A.pl->mass[0] = mass;
-                    A.pl->n_tiles = __popcll(b);
-                    if (A.flags_out) A.flags_out[0] = (uint8_t)flag;
-                }
-            }
-        }
+        if (wave == 0) gu_route_inline(A, lane, s_rv, s_ri, s_rank, s_rid, &s_nent);
         __syncthreads();
-    }
-    // B > 1: the plan from the routing kernel's ids and flags, built the same
-    // way in every workgroup (scratch in the stage area, free until the first
-    // stage): an expert's eligible selections form tiles of up to 8 in token
-    // order; experts in order of their first eligible selection.  A
-    // selection is eligible when its id is an expert and its token is
-    // computed here (flag 0 or 1; pruned selections carry -id-2).
-    uint32_t *p_mask = (uint32_t *)s_dyn;                 // [512] tokens choosing each expert
-    int *p_ids = (int *)(p_mask + QG_EXPERTS);            // [MS] eligible id or -1
-    int *p_tile = p_ids + MS;                             // [MAX_TILES] expert | tile-in-expert << 16
-    int *p_ntiles = p_tile + MAX_TILES;
-    if (!INL) {
-        const int ns = A.nt * QG_TOP;
-        for (int i = tid; i < QG_EXPERTS; i += 256) p_mask[i] = 0u;
-        int eq = -1;
-        if (tid < ns) {
-            const int id = A.ids[tid], fl = A.pl->flag[tid / QG_TOP];
-            eq = id >= 0 && id < QG_EXPERTS && fl < 2 ? id : -1;
-            p_ids[tid] = eq;
-        }
-        __syncthreads();
-        if (eq >= 0) atomicOr(&p_mask[eq], 1u << (tid / QG_TOP));
-        __syncthreads();
-        if (wave == 0) {
-            const unsigned long long below = (1ULL << lane) - 1ULL;
-            int tiles = 0;
-            for (int c0 = 0; c0 < ns; c0 += 64) {
-                const int q = c0 + lane, e = q < ns ? p_ids[q] : -1;
-                const uint32_t m = e >= 0 ? p_mask[e] : 0u;
-                // the expert's first eligible selection: its lowest token
-                const bool own = e >= 0 && (m & ((1u << (q / QG_TOP)) - 1u)) == 0u;
-                const int nt8 = own ? (__popc(m) + TILE_TOK - 1) / TILE_TOK : 0;  // 0..3
-                const unsigned long long b0 = __ballot(nt8 & 1), b1 = __ballot(nt8 & 2);
-                const int base = tiles + __popcll(b0 & below) + 2 * __popcll(b1 & below);
-                for (int x = 0; x < nt8; x++) p_tile[base + x] = e | (x << 16);
-                tiles += __popcll(b0) + 2 * __popcll(b1);
-            }
-            if (lane == 0) *p_ntiles = tiles;
-        }
-        __syncthreads();
+    } else {
+        gu_build_plan(A, tid, P);
     }
     const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     // the workgroup's items (blockIdx.x + i * gridDim.x, i < GU_NI) -> expert
@@ -379,40 +604,10 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     // item in a tile's first row block publishes the tile for the down kernel.
     if (wave == 0) {
         const int i = lane >> 3, slot = lane & 7, item = blockIdx.x + i * gridDim.x, T = item / rblocks;
-        int e = -1, n = -1;
-        if (T < sh_tiles) {
-            n = min(TILE_TOK, A.nt - TILE_TOK * T);
-            if (slot < n) s_list[i][slot] = MS + TILE_TOK * T + slot;
-        } else if (INL) {
-            const int k = T - sh_tiles;
-            if (k < s_nent) {
-                e = s_rid[k];
-                n = 1;
-                if (slot == 0) s_list[i][0] = s_rank[k];
-            }
-        } else if (T - sh_tiles < *p_ntiles) {
-            const int k = T - sh_tiles, te = p_tile[k], jt = te >> 16;
-            e = te & 0xffff;
-            const uint32_t m = p_mask[e];
-            n = min(TILE_TOK, __popc(m) - TILE_TOK * jt);
-            int q = -1;
-            if (slot < n) {
-                // the (8 jt + slot)-th token choosing e, and the rank it gave e
-                uint32_t mm = m;
-                for (int x = TILE_TOK * jt + slot; x > 0; x--) mm &= mm - 1u;
-                const int t = __builtin_ctz(mm);
-                int r = 0;
-#pragma unroll
-                for (int rr = 0; rr < QG_TOP; rr++) r = p_ids[t * QG_TOP + rr] == e ? rr : r;
-                q = t * QG_TOP + r;
-                s_list[i][slot] = q;
-            }
-            if (item % rblocks == 0) {
-                if (slot < n) A.pl->tile[k].q[slot] = q;
-                if (slot == 0) { A.pl->tile[k].e = e; A.pl->tile[k].n = n; }
-            }
-        }
-        if (!INL && blockIdx.x == 0 && lane == 0) A.pl->n_tiles = *p_ntiles;
+        int e, n, q;
+        gu_tile<INL>(A, T, sh_tiles, slot, s_rank, s_rid, INL ? s_nent : 0, P, item % rblocks == 0, e, n, q);
+        if (slot < n) s_list[i][slot] = q;
+        if (!INL && blockIdx.x == 0 && lane == 0) A.pl->n_tiles = *P.ntiles;
         if (slot == 0) { s_item[i][0] = e; s_item[i][1] = n; }
         // items ascend in tile order, so the valid ones are a prefix
         const unsigned long long v = __ballot(slot == 0 && n >= 0);
@@ -422,28 +617,24 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
         um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
     };
-    // this wave's 8 gate and 8 up rows of an item into registers
-    auto load_weights = [&](int e, int rb0, uint4 *w0, uint4 *w1) {
+    // this wave's 8 gate and 8 up rows of an item into registers, superblock
+    // by superblock: the header (every lane of a row loads the same 16 bytes,
+    // one memory request) and the lane's two 16-byte chunks of nibbles
+    auto load_weights = [&](int e, int rb0, uint4 *hd, uint4 *w0, uint4 *w1) {
         const uint8_t *gm, *um;
         mats(e, gm, um);
         const uint8_t *wrow = (j < 8 ? gm : um) + (size_t)(rb0 * GU_WROWS + wave * GU_ROWS + (j & 7)) * A.rb;
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
+            hd[sb] = qg_ld16(wrow + sb * 144);
             w0[sb] = qg_ld16(wrow + sb * 144 + 16 + 16 * kq);
             w1[sb] = qg_ld16(wrow + sb * 144 + 16 + 16 * (kq + 4));
+            asm volatile("" ::: "memory");  // issue in superblock order
         }
     };
-    // the wave's 16 x NSB superblock headers, and the tile's rows r < 2n (token
-    // r/2, plane r%2) with their sum rows, straight into shared memory
-    auto stage = [&](int e, int rb0, int n, const int *list) {
-        const uint8_t *gm, *um;
-        mats(e, gm, um);
-        const int wrow0 = rb0 * GU_WROWS + wave * GU_ROWS;
-        for (int q = 0; q * 64 < 16 * HROW; q++) {
-            const int slot = q * 64 + lane, rr = slot / HROW, sb = slot - rr * HROW;
-            if (rr < 16 && sb < NSB)
-                dma16_ordered((rr < 8 ? gm : um) + (size_t)(wrow0 + (rr & 7)) * A.rb + sb * 144, hbuf + (size_t)q * 1024);
-        }
+    // the tile's rows r < 2n (token r/2, plane r%2) with their sum rows,
+    // straight into shared memory
+    auto stage = [&](int e, int n, const int *list) {
         for (int q = wave; q < 2 * n * bpr; q += 4) {
             const int r = q / bpr, b = q - r * bpr;
             const int sl = list[r >> 1], tok = e < 0 ? sl - MS : sl / QG_TOP;
@@ -457,30 +648,24 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
             }
         }
     };
-    // software pipeline over the workgroup's items: the next item's weight rows
-    // load into registers while the current item's products run.  The first
-    // item's stage is issued before its weight rows, so the products start
-    // once the stage has landed and each superblock's rows wait only for
-    // themselves (loads complete in issue order).
+    // Per item: the stage (untracked copies), then the weight rows; a wait for
+    // the stage alone (the 3 NSB weight loads behind it may still be in
+    // flight) and a barrier; then the products, each superblock waiting only
+    // for its own rows (loads complete in issue order), so they run while the
+    // later superblocks stream in.
     __syncthreads();
+    asm volatile("" ::"v"(warm));  // the warming loads have landed
     const int nit = s_nitems;
     if (nit == 0) return;  // block-uniform
-    uint4 c0[NSB], c1[NSB], n0[NSB], n1[NSB];
-    stage(s_item[0][0], blockIdx.x % rblocks, s_item[0][1], s_list[0]);
+    uint4 hd[NSB], c0[NSB], c1[NSB];
+    stage(s_item[0][0], s_item[0][1], s_list[0]);
     asm volatile("" ::: "memory");
-    load_weights(s_item[0][0], blockIdx.x % rblocks, c0, c1);
-    // one item; the first is peeled (FIRST) so that the compiler's wait
-    // before its shared-memory reads counts only the stage, not the weight
-    // rows issued after it
-    auto process = [&](int it, auto first) -> bool {
-        constexpr bool FIRST = decltype(first)::value;
+    load_weights(s_item[0][0], blockIdx.x % rblocks, hd, c0, c1);
+    for (int it = 0;; it++) {
         const int item = blockIdx.x + it * gridDim.x;
-        if (FIRST) wait_vmem_but<2 * NSB>();
-        else wait_vmem();
+        wait_vmem_but<3 * NSB>();
         __syncthreads();
         const int e = s_item[it][0], n = s_item[it][1], rb0 = item % rblocks;
-        const bool more = it + 1 < nit;
-        if (more) load_weights(s_item[it + 1][0], (item + gridDim.x) % rblocks, n0, n1);
         const bool shared = e < 0;
         const int fmt = shared ? A.sh_fmt : A.fmt;
         const int pos = plane_pos(fmt, rb0 * GU_WROWS + wave * GU_ROWS + (j & 7));
@@ -488,12 +673,11 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         // the min-term product takes its 8 group sums from lanes kq = 0; the
         // other lanes read zeros
         const _Float16 *ap = act + (size_t)r * LY.arow + kq * 8, *sp = kq ? (const _Float16 *)s_zero : acts + (size_t)r * LY.srow;
-        const uint8_t *hp = hbuf + (size_t)j * HROW * 16;
         const int gA = 2 * (kq >> 1), gB = gA + 4;
         qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
-            const Q4kHeader h = q4k_header(*(const uint4 *)(hp + sb * 16));
+            const Q4kHeader h = q4k_header(hd[sb]);
             qg_f4 p0 = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, p1 = p0, mm = p0;
 #pragma unroll
             for (int f = 0; f < 4; f++) {
@@ -506,7 +690,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
 #pragma unroll
             for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(h.d, p0[i] + p1[i], __builtin_fmaf(-h.dmin, mm[i], y[i]));
             // one superblock at a time: its sums are taken and no later read is
-            // hoisted above it (the prefetched weight rows need the registers)
+            // hoisted above it
             asm volatile("" ::: "memory");
 #pragma unroll
             for (int i = 0; i < 4; i++) asm volatile("" : "+v"(y[i]));
@@ -531,15 +715,11 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
                 if (j == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + rb0 * 4 + wave] = s8;
             }
         }
-        __syncthreads();  // the stage and the headers are free
-        if (!more) return false;  // block-uniform
-#pragma unroll
-        for (int sb = 0; sb < NSB; sb++) { c0[sb] = n0[sb]; c1[sb] = n1[sb]; }
-        stage(s_item[it + 1][0], (item + gridDim.x) % rblocks, s_item[it + 1][1], s_list[it + 1]);
-        return true;
-    };
-    if (!process(0, std::true_type{})) return;
-    for (int it = 1; process(it, std::false_type{}); it++) {
+        __syncthreads();  // the stage is free
+        if (it + 1 == nit) break;  // block-uniform
+        stage(s_item[it + 1][0], s_item[it + 1][1], s_list[it + 1]);
+        asm volatile("" ::: "memory");
+        load_weights(s_item[it + 1][0], (item + gridDim.x) % rblocks, hd, c0, c1);
     }
 }
 
@@ -856,13 +1036,22 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const int items = tiles * (F / GU_WROWS);
     int nwg = items < GU_WGS ? items : GU_WGS;
     if (nwg * GU_NI < items) nwg = (items + GU_NI - 1) / GU_NI;  // each workgroup resolves GU_NI items at most
-    const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
-    if (D == 2048) {
-        if (inl) dec_launch(2, dec_gateup_kernel<8, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-        else dec_launch(2, dec_gateup_kernel<8, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+    // the pipelined kernel: contiguous ranges of 16-row items, at most GU2_NT tiles each
+    const int items2 = tiles * (F / GU2_ROWS), per2 = (GU2_NT - 1) * (F / GU2_ROWS);
+    int nwg2 = items2 < GU_WGS ? items2 : GU_WGS;
+    if ((long long)nwg2 * per2 < items2) nwg2 = (items2 + per2 - 1) / per2;
+    if (D == 2048 && F % GU2_ROWS == 0) {
+        if (inl) dec_launch(2, dec_gateup2_kernel<true>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
+        else dec_launch(2, dec_gateup2_kernel<false>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
     } else {
-        if (inl) dec_launch(2, dec_gateup_kernel<10, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-        else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
+        if (D == 2048) {
+            if (inl) dec_launch(2, dec_gateup_kernel<8, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+            else dec_launch(2, dec_gateup_kernel<8, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        } else {
+            if (inl) dec_launch(2, dec_gateup_kernel<10, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+            else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        }
     }
     if ((rc = hipGetLastError())) return rc;
     const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;
