@@ -968,6 +968,155 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
     }
 }
 
+// ---------------- K3+K4 at one token: down and combine in one kernel ----------------
+struct Dn1Args {
+    int D, F;
+    const float *w; const DecPlan *pl;
+    const uint8_t *down, *sh_down; size_t rb, sh_rb;
+    const _Float16 *midp; const float *msum8;
+    const float *sh_logit;               // the shared-gate logit (with a shared expert)
+    float *out, *resid;
+    qg_prune_stats *stats;
+};
+constexpr int DN1_ROWS = 16;             // output rows per workgroup
+constexpr int DN1_SL = DN1_ROWS * 288 / 16;  // 16-byte slots of 16 rows of 288 bytes
+constexpr int DN1_W = 8;                 // waves per workgroup
+constexpr int DN1_EPW = 2;               // entries per wave (10 routed + 1 shared over 8 waves)
+// weight rows per wave and entry, then every entry's mid planes (F = 512) and 8-row sums
+constexpr size_t DN1_LDS = (size_t)DN1_W * DN1_EPW * DN1_SL * 16 + (size_t)(QG_TOP + 1) * 2 * 512 * 2 + (size_t)(QG_TOP + 1) * 64 * 4;
+
+// One token (the plan's entries k = eligible ranks in order, then the shared
+// expert): workgroup b owns output rows 16b .. 16b + 15; wave w (of 8) computes
+// the entries k = w, w + 8 (their 16 weight rows, the entries' mid planes
+// and 8-row sums all copied into shared memory by direct global->shared
+// copies at once), each weighted by its routing weight; wave 0 then sums them in
+// rank order, adds sigmoid(logit) times the shared expert's row and the
+// optional residual, as the combine kernel does.  F = 512 (288-byte rows).
+template <int FMT, int SFMT>
+__global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
+    extern __shared__ uint4 s_dyn[];
+    __shared__ float s_v[QG_TOP + 1][DN1_ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    const int F = A.F, d0 = blockIdx.x * DN1_ROWS, sh = A.sh_down ? 1 : 0;
+    const int nent = A.pl->n_tiles, flag = A.pl->flag[0], E = nent + sh;
+    uint4 *wl = s_dyn + (size_t)wave * DN1_EPW * DN1_SL;
+    _Float16 *mids = (_Float16 *)(s_dyn + (size_t)DN1_W * DN1_EPW * DN1_SL);  // [E][2][F] mid planes
+    float *msl = (float *)(mids + (size_t)(QG_TOP + 1) * 2 * F);          // [E][F/8] 8-row sums
+    int ee[DN1_EPW], qq[DN1_EPW];
+#pragma unroll
+    for (int x = 0; x < DN1_EPW; x++) {
+        const int k = wave + DN1_W * x;
+        ee[x] = k < nent ? A.pl->tile[k].e : -1;
+        qq[x] = k < nent ? A.pl->tile[k].q[0] : MS;
+    }
+    // every copy at once: this wave's entries' weight rows, and (spread over the
+    // waves) each entry's two mid plane rows and its 8-row sums
+#pragma unroll
+    for (int x = 0; x < DN1_EPW; x++) {
+        const int k = wave + DN1_W * x;
+        if (k < E) {
+            const uint8_t *W = (ee[x] < 0 ? A.sh_down : A.down + (size_t)ee[x] * A.D * A.rb) + (size_t)d0 * 288;
+#pragma unroll
+            for (int i = 0; i < (DN1_SL + 63) / 64; i++) {
+                const int sl = i * 64 + lane;
+                if (sl < DN1_SL) dma16_ordered(W + 16 * (size_t)sl, wl + (size_t)x * DN1_SL + i * 64);
+            }
+            // the entry's mid planes (2 x 1 KB) and sums (256 bytes)
+            const int q = qq[x];
+            const _Float16 *mg = A.midp + (size_t)q * 2 * F;
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++) dma16_ordered(mg + (size_t)pl * F + lane * 8, mids + ((size_t)k * 2 + pl) * F);
+            if (lane < F / 32) dma16_ordered(A.msum8 + (size_t)q * (F / 8) + lane * 4, msl + (size_t)k * (F / 8));
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < DN1_EPW; x++) {
+        const int k = wave + DN1_W * x;
+        if (k < E) {
+            const bool shared = ee[x] < 0, q4k = (shared ? SFMT : FMT) == QT_Q4_K;
+            const int q = qq[x];
+            // A rows: 0 = hi plane, 1 = lo plane of the token's mid (others repeat them)
+            const _Float16 *mr = mids + ((size_t)k * 2 + (j & 1)) * F + kq * 8;
+            qg_half8 af[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) af[i] = ld_frag(mr + i * 32);
+            float xg[16];
+            if (q4k) {
+#pragma unroll
+                for (int g = 0; g < 16; g++) {
+                    const float4 m4 = *(const float4 *)(msl + (size_t)k * (F / 8) + 4 * g);
+                    xg[g] = (m4.x + m4.y) + (m4.z + m4.w);
+                }
+            }
+            const uint8_t *wb = (const uint8_t *)(wl + (size_t)x * DN1_SL) + (size_t)j * 288;
+            qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (q4k) {
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++) {
+                    const uint8_t *p = wb + sb * 144;
+                    const Q4kHeader h = q4k_header(*(const uint4 *)p);
+                    const uint4 ca = *(const uint4 *)(p + 16 + 16 * kq), cb = *(const uint4 *)(p + 16 + 16 * (kq + 4));
+                    const int gA = 2 * (kq >> 1), gB = gA + 4;
+                    qg_f4 acc = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int f = 0; f < 4; f++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + f], q4k_chunk_frag(ca, f, (_Float16)q4k_s(h, gA + (f >> 1))), acc, 0, 0, 0);
+#pragma unroll
+                    for (int f = 0; f < 4; f++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + 4 + f], q4k_chunk_frag(cb, f, (_Float16)q4k_s(h, gB + (f >> 1))), acc, 0, 0, 0);
+                    float M = 0.0f;
+#pragma unroll
+                    for (int g = 0; g < 8; g++) M = __builtin_fmaf((float)q4k_m(h, g), xg[sb * 8 + g], M);
+                    y[0] = __builtin_fmaf(h.d, acc[0], __builtin_fmaf(-h.dmin, M, y[0]));
+                    y[1] = __builtin_fmaf(h.d, acc[1], y[1]);
+                }
+            } else {
+#pragma unroll
+                for (int b0 = 0; b0 < 16; b0 += 8) {
+                    qg_f4 acc[8];
+                    float d[8];
+#pragma unroll
+                    for (int bb = 0; bb < 8; bb++) {
+                        const uint16_t *p16 = (const uint16_t *)(wb + 18 * (b0 + bb));  // 2-byte aligned
+                        d[bb] = qg_half_u16(p16[0]);
+                        const uint32_t qv = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
+                        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[b0 + bb], iq4_frag4(qv), qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int bb = 0; bb < 8; bb++) {
+                        y[0] = __builtin_fmaf(d[bb], acc[bb][0], y[0]);
+                        y[1] = __builtin_fmaf(d[bb], acc[bb][1], y[1]);
+                    }
+                }
+            }
+            // lanes kq = 0 hold rows 0 (hi) and 1 (lo) of weight row j
+            const float v = y[0] + y[1];
+            if (kq == 0) s_v[k][j] = shared ? v : v * A.w[q];
+        }
+    }
+    __syncthreads();
+    if (tid < DN1_ROWS) {
+        float acc = 0.0f;
+        if (flag < 2) {
+            for (int k = 0; k < nent; k++) acc += s_v[k][tid];
+            if (sh) acc = __builtin_fmaf(s_v[nent][tid], qg_sig(A.sh_logit[0]), acc);
+        }
+        if (A.out) A.out[d0 + tid] = acc;
+        if (A.resid) A.resid[d0 + tid] += acc;
+    }
+    if (A.stats && blockIdx.x == 0 && tid == 0 && flag != 3) {
+        A.stats->token_layers += 1;
+        A.stats->missing_selections += (uint64_t)A.pl->missing[0];
+        if (flag == 1) {
+            A.stats->skipped_selections += (uint64_t)A.pl->missing[0];
+            A.stats->avoided_token_handoffs += 1;
+            A.stats->skipped_mass += A.pl->mass[0];
+        }
+    }
+}
+
 bool fmt_down_ok(int t, int F) { return (t == QT_Q4_K && F % 256 == 0) || t == QT_IQ4_NL; }
 
 bool dec_ok(const qg_moe_layer *L) {
@@ -1063,6 +1212,17 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const size_t dn_lds = ((DN_ROWS * rbmax + 1023) & ~(size_t)1023) + (size_t)16 * F * 2 +
                           (((size_t)8 * (F / 8 + 4) * 4 + 1023) & ~(size_t)1023);
     const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
+    if (inl && F == 512 && rb == 288 && (!sh || srb == 288) && D % DN1_ROWS == 0) {
+        // one token: down and the combine in one kernel
+        Dn1Args D1{D, F, weights, pl, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
+                   midp, msum8, logits + QG_EXPERTS, out, resid, (L->resident && stats) ? stats : nullptr};
+        const dim3 g1(D / DN1_ROWS), b1(64 * DN1_W);
+        if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) dec_launch(3, dec_down1_kernel<QT_IQ4_NL, QT_IQ4_NL>, g1, b1, DN1_LDS, s, D1);
+        else if (fr == QT_IQ4_NL) dec_launch(3, dec_down1_kernel<QT_IQ4_NL, QT_Q4_K>, g1, b1, DN1_LDS, s, D1);
+        else if (fs == QT_IQ4_NL) dec_launch(3, dec_down1_kernel<QT_Q4_K, QT_IQ4_NL>, g1, b1, DN1_LDS, s, D1);
+        else dec_launch(3, dec_down1_kernel<QT_Q4_K, QT_Q4_K>, g1, b1, DN1_LDS, s, D1);
+        return hipGetLastError();
+    }
     const int dn_items = tiles * (D / DN_ROWS);
     launch_down(DA, fr, fs, dim3(dn_items < DN_WGS ? dn_items : DN_WGS), dn_lds, s);
     if ((rc = hipGetLastError())) return rc;

@@ -337,7 +337,7 @@ def test_layer_config0_multitoken_no_shared(layer0):
     _check_layer(L, H, synth.inputs(9, 5, 2048), "config0 B=5")
 
 
-@pytest.mark.parametrize("nt", [4, 17])
+@pytest.mark.parametrize("nt", [1, 4, 17])
 def test_layer_partial_residency_flags(layer1, nt):
     """Config 4: 128 resident experts chosen by routed-weight mass over 4096
     synthetic tokens; flags and pruning exact, unflagged rows in tolerance
