@@ -36,6 +36,26 @@ int nm_stack_forward(nm_stack *s, int tokens, int use_graph);
 int nm_stack_record(nm_stack *s, int layer, const float **x, const int **ids, const float **weights, const float **out);
 const char *nm_last_error(void);
 
+/* CPU handoff of one layer's flag-2 tokens (the hybrid path of
+ * qwen.c:658-678, narrowed from the whole batch to the flagged tokens).
+ * cpu_moe computes the routed part (qc_moe of cpu.c:235-261, through
+ * qwen.c:615-617) of `tokens` packed rows: out [tokens][D] from x
+ * [tokens][D], ids/weights [tokens][10]; it returns 0 on success. */
+typedef int (*nm_cpu_moe_fn)(void *ctx, float *out, const float *x, const int *ids, const float *weights, int tokens);
+/* Device scratch bytes nm_moe_handoff needs for up to `tokens` tokens. */
+size_t nm_handoff_scratch_bytes(int width, int tokens);
+/* After qg_moe_forward(_residual) with flags: packs the flag-2 tokens on the
+ * device, reads their count (4 bytes, synchronous) and then only their
+ * input rows, ids and weights, calls cpu_moe, writes its rows back and adds
+ * them to out (and to out2 when not NULL: the residual stream h) at the
+ * tokens' rows, where the device left the shared expert's part.  x is the
+ * layer input the forward used (xn_out for the residual form).  Synchronous
+ * (not capturable), like the reference's handoff.  *handed_off (may be NULL)
+ * = number of tokens sent to the host. */
+int nm_moe_handoff(float *out, float *out2, const unsigned char *flags, const float *x, const int *ids,
+                   const float *weights, int tokens, int width, void *scratch, size_t scratch_bytes,
+                   nm_cpu_moe_fn cpu_moe, void *ctx, int *handed_off);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,8 +117,11 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
 /* out [tokens, D]; ids/weights [tokens, 10] (after pruning); flags [tokens]
  * or NULL: 0 all selections resident, 1 pruned (omitted mass < threshold),
  * 2 handoff (coverage below 1-threshold), 3 invalid router distribution;
- * stats may be NULL.  With flags==2 the token's output row is not computed
- * here (it belongs to the host handoff, qwen.c:658-678) and is written as 0.
+ * stats may be NULL.  With flags==2 the token's routed part is not computed
+ * here (it belongs to the host handoff, qwen.c:658-678): its row holds only
+ * the sigmoid-gated shared expert (which stays on the device, qwen.c:661-663),
+ * or 0 without one; qg_moe_handoff_pack/merge move the routed part through
+ * the host.  flags==3 rows are 0.
  * tokens 1..8192: up to 17 the decode kernels (any format qg_matmul takes);
  * above, the prefill grouped GEMMs, which need Q4_K gate/up, Q4_K or IQ4_NL
  * down, D a multiple of 256 and F a multiple of 128 (else an error). */
@@ -133,6 +136,20 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
 int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                             float *xn_out, float *out, int tokens, const qg_moe_layer *layer,
                             void *workspace, size_t workspace_bytes);
+
+/* CPU handoff of the flag-2 tokens (replaces the whole-batch reads of
+ * qwen.c:665-666 and the write of qwen.c:672).  Device arrays; async on the
+ * calling thread's stream.  pack: count[0] = number of tokens with
+ * flags[t] == 2, rows[i] = the i-th of them (ascending), and row i of x_pack
+ * [tokens, width], ids_pack / w_pack [tokens, 10] = that token's input row,
+ * ids and weights (only the first count[0] rows are written).  merge:
+ * out[rows[i]] += y_pack[i] for i < count[0], y_pack [tokens, width] being
+ * the host's routed rows (qc_moe, cpu.c:235-261, of the packed tokens).
+ * tokens 1..8192. */
+int qg_moe_handoff_pack(int *count, int *rows, float *x_pack, int *ids_pack, float *w_pack,
+                        const unsigned char *flags, const float *x, const int *ids, const float *weights,
+                        int tokens, int width);
+int qg_moe_handoff_merge(float *out, const float *y_pack, const int *count, const int *rows, int tokens, int width);
 
 /* Benchmark support: events[2i] and events[2i+1] (qg_event_create handles)
  * are recorded at the start and end of kernel i of this thread's

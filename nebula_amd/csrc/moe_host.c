@@ -2,6 +2,7 @@
  * include/nebula_moe.h).  Calls only the qg_* C ABI of libqwen_gpu.so. */
 #include "nebula_moe.h"
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -104,4 +105,63 @@ int nm_stack_record(nm_stack *s, int layer, const float **x, const int **ids, co
     if (ids) *ids = s->rec_ids + b * layer;
     if (weights) *weights = s->rec_w + b * layer;
     return 0;
+}
+
+/* ---- CPU handoff of flag-2 tokens (qwen.c:658-678) ---- */
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+/* scratch: count | rows [T] | x_pack [T][D] | ids [T][10] | weights [T][10] | y [T][D] */
+typedef struct { int *count, *rows, *ids; float *x, *w, *y; size_t bytes; } handoff_layout;
+static handoff_layout handoff_at(uintptr_t base, int D, int T) {
+    handoff_layout L;
+    size_t o = 0;
+    L.count = (int *)(base + o); o += 256;
+    L.rows = (int *)(base + o); o += align256((size_t)T * 4);
+    L.x = (float *)(base + o); o += align256((size_t)T * D * 4);
+    L.ids = (int *)(base + o); o += align256((size_t)T * NM_TOP * 4);
+    L.w = (float *)(base + o); o += align256((size_t)T * NM_TOP * 4);
+    L.y = (float *)(base + o); o += align256((size_t)T * D * 4);
+    L.bytes = o;
+    return L;
+}
+
+size_t nm_handoff_scratch_bytes(int width, int tokens) {
+    if (width < 1 || tokens < 1 || tokens > 8192) return 0;
+    return handoff_at(0, width, tokens).bytes;
+}
+
+int nm_moe_handoff(float *out, float *out2, const unsigned char *flags, const float *x, const int *ids,
+                   const float *weights, int nt, int D, void *scratch, size_t scratch_bytes,
+                   nm_cpu_moe_fn cpu_moe, void *ctx, int *handed_off) {
+    if (handed_off) *handed_off = 0;
+    if (!out || !flags || !x || !ids || !weights || !scratch || !cpu_moe || nt < 1 || nt > 8192 || D < 1)
+        return fail("invalid handoff arguments");
+    const handoff_layout L = handoff_at((uintptr_t)scratch, D, nt);
+    if (scratch_bytes < L.bytes) return fail("handoff scratch of %zu bytes, %zu needed", scratch_bytes, L.bytes);
+    int rc = qg_moe_handoff_pack(L.count, L.rows, L.x, L.ids, L.w, flags, x, ids, weights, nt, D);
+    int n = 0;
+    if (!rc) rc = qg_read(&n, L.count, sizeof n);
+    if (rc) return fail("handoff pack: %s", qg_error(rc));
+    if (n < 0 || n > nt) return fail("handoff count %d out of range", n);
+    if (!n) return 0;
+    const size_t xb = (size_t)n * D * sizeof(float), sb = (size_t)n * NM_TOP * 4;
+    float *hx = malloc(xb), *hy = malloc(xb), *hw = malloc(sb);
+    int *hi = malloc(sb);
+    int ret = -1;
+    if (!hx || !hy || !hw || !hi) { fail("host allocation"); goto done; }
+    if ((rc = qg_read(hx, L.x, xb)) || (rc = qg_read(hi, L.ids, sb)) || (rc = qg_read(hw, L.w, sb))) {
+        fail("handoff read: %s", qg_error(rc));
+        goto done;
+    }
+    if (cpu_moe(ctx, hy, hx, hi, hw, n)) { fail("CPU MoE of %d handed-off tokens failed", n); goto done; }
+    if ((rc = qg_write(L.y, hy, xb)) || (rc = qg_moe_handoff_merge(out, L.y, L.count, L.rows, nt, D)) ||
+        (out2 && (rc = qg_moe_handoff_merge(out2, L.y, L.count, L.rows, nt, D)))) {
+        fail("handoff merge: %s", qg_error(rc));
+        goto done;
+    }
+    if (handed_off) *handed_off = n;
+    ret = 0;
+done:
+    free(hx); free(hy); free(hw); free(hi);
+    return ret;
 }

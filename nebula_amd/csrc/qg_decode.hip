@@ -905,8 +905,9 @@ struct CombArgs {
 };
 
 // out[t] = sum over ranks k of the weighted slots (cpu.c:257-259 order), then
-// + y_sh * sigmoid(logit) (gpu.cu:552-553), then the optional residual add;
-// flag >= 2 rows are 0.
+// + y_sh * sigmoid(logit) (gpu.cu:552-553), then the optional residual add.
+// Flag 2 rows (host handoff, qwen.c:658-678) get the shared part only, flag 3
+// rows 0.
 __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
     const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d < A.D) {
@@ -936,13 +937,13 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
                 acc.z += ok ? v[k].z : 0.0f;
                 acc.w += ok ? v[k].w : 0.0f;
             }
-            if (A.has_shared) {
-                const float sg = qg_sig(lg);
-                acc.x = __builtin_fmaf(vs.x, sg, acc.x);
-                acc.y = __builtin_fmaf(vs.y, sg, acc.y);
-                acc.z = __builtin_fmaf(vs.z, sg, acc.z);
-                acc.w = __builtin_fmaf(vs.w, sg, acc.w);
-            }
+        }
+        if (A.has_shared && flag != 3) {
+            const float sg = qg_sig(lg);
+            acc.x = __builtin_fmaf(vs.x, sg, acc.x);
+            acc.y = __builtin_fmaf(vs.y, sg, acc.y);
+            acc.z = __builtin_fmaf(vs.z, sg, acc.z);
+            acc.w = __builtin_fmaf(vs.w, sg, acc.w);
         }
         const size_t o = (size_t)t * A.D + d;
         if (A.out) *(float4 *)(A.out + o) = acc;
@@ -1099,10 +1100,10 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
     __syncthreads();
     if (tid < DN1_ROWS) {
         float acc = 0.0f;
-        if (flag < 2) {
+        if (flag < 2)
             for (int k = 0; k < nent; k++) acc += s_v[k][tid];
-            if (sh) acc = __builtin_fmaf(s_v[nent][tid], qg_sig(A.sh_logit[0]), acc);
-        }
+        // a handed-off token (flag 2, no routed entries) keeps the shared part
+        if (sh && flag != 3) acc = __builtin_fmaf(s_v[nent][tid], qg_sig(A.sh_logit[0]), acc);
         if (A.out) A.out[d0 + tid] = acc;
         if (A.resid) A.resid[d0 + tid] += acc;
     }

@@ -562,8 +562,8 @@ __global__ __launch_bounds__(256) void down_kernel(DownArgs A) {
 // ---------------- kernel 5: router-rank combine + shared expert ----------------
 // out[t,d] = sum over k=0..9 of the weighted slots from 0.0f in router-rank
 // order (gpu.cu:521-527, cpu.c:227-230; pruned ranks add +0), then the
-// sigmoid-gated shared expert added with one fma (gpu.cu:552).  Tokens
-// flagged handoff/invalid get a zero row.
+// sigmoid-gated shared expert added with one fma (gpu.cu:552).  Handoff
+// tokens (flag 2) get the shared part only, invalid ones (flag 3) a zero row.
 __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *slots, const Disp *ds, const float *sh_logit,
                                                       int ld, int nt, int D) {
     const int i = blockIdx.x * 256 + threadIdx.x, q = D / 4;
@@ -586,10 +586,10 @@ __global__ __launch_bounds__(256) void combine_kernel(float *out, const float *s
             const bool ok = se[k] >= 0;
             acc.x += ok ? v[k].x : 0.0f; acc.y += ok ? v[k].y : 0.0f; acc.z += ok ? v[k].z : 0.0f; acc.w += ok ? v[k].w : 0.0f;
         }
-        if (has_shared) {
-            acc.x = __builtin_fmaf(s.x, g, acc.x); acc.y = __builtin_fmaf(s.y, g, acc.y);
-            acc.z = __builtin_fmaf(s.z, g, acc.z); acc.w = __builtin_fmaf(s.w, g, acc.w);
-        }
+    }
+    if (has_shared && flag != 3) {
+        acc.x = __builtin_fmaf(s.x, g, acc.x); acc.y = __builtin_fmaf(s.y, g, acc.y);
+        acc.z = __builtin_fmaf(s.z, g, acc.z); acc.w = __builtin_fmaf(s.w, g, acc.w);
     }
     *(float4 *)(out + (size_t)t * D + d4) = acc;
 }

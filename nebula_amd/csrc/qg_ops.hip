@@ -242,6 +242,61 @@ __global__ void shared_add_kernel(float *o, const float *x, const float *g, int 
 
 unsigned blocks_for(size_t n, unsigned threads) { return (unsigned)((n + threads - 1) / threads); }
 
+// ---- CPU handoff of flagged tokens (qwen.c:658-678) ----
+// rows[i] = the i-th token, ascending, whose flag is 2 (coverage below
+// 1 - threshold); count[0] = their number.  One block of 1024 threads.
+__global__ __launch_bounds__(1024) void handoff_rows_kernel(int *count, int *rows, const uint8_t *flags, int nt) {
+    __shared__ int s_wave[16];
+    __shared__ int s_base;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_base = 0;
+    __syncthreads();
+    for (int c0 = 0; c0 < nt; c0 += 1024) {
+        const int t = c0 + tid;
+        const bool h = t < nt && flags[t] == 2;
+        const unsigned long long b = __ballot(h);
+        if (lane == 0) s_wave[wave] = __popcll(b);
+        __syncthreads();
+        int off = s_base;
+        for (int w = 0; w < wave; w++) off += s_wave[w];
+        if (h) rows[off + __popcll(b & ((1ULL << lane) - 1ULL))] = t;
+        __syncthreads();
+        if (tid == 0) {
+            int n = 0;
+            for (int w = 0; w < 16; w++) n += s_wave[w];
+            s_base += n;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) count[0] = s_base;
+}
+
+// Block i < count: row i of the packed arrays = token rows[i]'s input row,
+// ids and weights (blocks past the count exit).
+__global__ __launch_bounds__(256) void handoff_pack_kernel(float *xp, int *idp, float *wp, const int *count, const int *rows,
+                                                           const float *x, const int *ids, const float *w, int width) {
+    const int i = blockIdx.x;
+    if (i >= count[0]) return;
+    const int t = rows[i];
+    const float *src = x + (size_t)t * width;
+    float *dst = xp + (size_t)i * width;
+    for (int d = threadIdx.x; d < width; d += 256) dst[d] = src[d];
+    if (threadIdx.x < QG_TOP) {
+        idp[(size_t)i * QG_TOP + threadIdx.x] = ids[(size_t)t * QG_TOP + threadIdx.x];
+        wp[(size_t)i * QG_TOP + threadIdx.x] = w[(size_t)t * QG_TOP + threadIdx.x];
+    }
+}
+
+// Block i < count: out[rows[i]] += y[i] (the host's routed rows onto the
+// device rows, which hold the shared expert's part).
+__global__ __launch_bounds__(256) void handoff_merge_kernel(float *out, const float *y, const int *count, const int *rows, int width) {
+    const int i = blockIdx.x;
+    if (i >= count[0]) return;
+    float *o = out + (size_t)rows[i] * width;
+    const float *src = y + (size_t)i * width;
+    for (int d = threadIdx.x; d < width; d += 256) o[d] += src[d];
+}
+
 }  // namespace
 
 int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt,
@@ -347,6 +402,26 @@ int qg_moe_reduce(float *out, const float *slots, int nt) {  // gpu.cu:525-527
 int qg_shared_add(float *o, const float *x, const float *g, int nt) {  // gpu.cu:553
     if (nt < 1) return hipErrorInvalidValue;
     shared_add_kernel<<<blocks_for((size_t)nt * g_width, 256), 256, 0, qg_stream()>>>(o, x, g, nt, g_width);
+    return hipGetLastError();
+}
+
+// qwen.c:665-666 read every token's input and weights to the host when a
+// selection is missing; here only the flag-2 tokens are packed for it.
+int qg_moe_handoff_pack(int *count, int *rows, float *x_pack, int *ids_pack, float *w_pack, const unsigned char *flags,
+                        const float *x, const int *ids, const float *weights, int nt, int width) {
+    if (nt < 1 || nt > QG_MAX_TOKENS || width < 1 || !count || !rows || !x_pack || !ids_pack || !w_pack || !flags || !x ||
+        !ids || !weights)
+        return hipErrorInvalidValue;
+    handoff_rows_kernel<<<1, 1024, 0, qg_stream()>>>(count, rows, flags, nt);
+    handoff_pack_kernel<<<nt, 256, 0, qg_stream()>>>(x_pack, ids_pack, w_pack, count, rows, x, ids, weights, width);
+    return hipGetLastError();
+}
+
+// qwen.c:672 writes the host's rows over the layer output; here they are
+// added to the device rows of the packed tokens (the shared expert's part).
+int qg_moe_handoff_merge(float *out, const float *y_pack, const int *count, const int *rows, int nt, int width) {
+    if (nt < 1 || nt > QG_MAX_TOKENS || width < 1 || !out || !y_pack || !count || !rows) return hipErrorInvalidValue;
+    handoff_merge_kernel<<<nt, 256, 0, qg_stream()>>>(out, y_pack, count, rows, width);
     return hipGetLastError();
 }
 

@@ -804,7 +804,8 @@ struct CombArgs {
 
 // out[t] = sum_k (w[t,k] * y[t,k]) in rank order (each product rounded, as
 // the slot products of cpu.c:253-259), then + y_sh * sigmoid(logit)
-// (gpu.cu:552-553); flag >= 2 rows are 0.
+// (gpu.cu:552-553).  Flag 2 rows (host handoff) get the shared part only,
+// flag 3 rows 0.
 __global__ __launch_bounds__(256) void pf_combine_kernel(CombArgs A) {
     const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d >= A.D) return;
@@ -821,14 +822,14 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(CombArgs A) {
             acc.z += __fmul_rn(v.z, wk);
             acc.w += __fmul_rn(v.w, wk);
         }
-        if (A.sh_logit) {
-            const float sg = qg_sig(A.sh_logit[(size_t)t * A.ld]);
-            const float4 v = *(const float4 *)(A.slots + ((size_t)A.nt * QG_TOP + t) * A.D + d);
-            acc.x = __builtin_fmaf(v.x, sg, acc.x);
-            acc.y = __builtin_fmaf(v.y, sg, acc.y);
-            acc.z = __builtin_fmaf(v.z, sg, acc.z);
-            acc.w = __builtin_fmaf(v.w, sg, acc.w);
-        }
+    }
+    if (A.sh_logit && A.flag[t] != 3) {
+        const float sg = qg_sig(A.sh_logit[(size_t)t * A.ld]);
+        const float4 v = *(const float4 *)(A.slots + ((size_t)A.nt * QG_TOP + t) * A.D + d);
+        acc.x = __builtin_fmaf(v.x, sg, acc.x);
+        acc.y = __builtin_fmaf(v.y, sg, acc.y);
+        acc.z = __builtin_fmaf(v.z, sg, acc.z);
+        acc.w = __builtin_fmaf(v.w, sg, acc.w);
     }
     const size_t o = (size_t)t * A.D + d;
     if (A.out) *(float4 *)(A.out + o) = acc;

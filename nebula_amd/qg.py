@@ -38,11 +38,17 @@ SIGNATURES = {
     "event_create": ([], P), "event_destroy": ([P], None), "event_record": ([P], I), "event_elapsed": ([P, P, P], I),
     "device_info": ([P, Z, P, P, P, P], I),
     "synth_matrix": ([P, I, U64, U64, I, I, F], I),
+    "moe_handoff_pack": ([P, P, P, P, P, P, P, P, P, I, I], I), "moe_handoff_merge": ([P, P, P, P, I, I], I),
 }
+
+# nm_cpu_moe_fn of include/nebula_moe.h: (ctx, out, x, ids, weights, tokens) -> 0 on success
+CPU_MOE_FN = C.CFUNCTYPE(I, P, P, P, P, P, I)
 
 HOST_SIGNATURES = {
     "stack_create": ([P, I, I, I], P), "stack_destroy": ([P], None), "stack_hidden": ([P], P),
     "stack_forward": ([P, I, I], I), "stack_record": ([P, I, P, P, P, P], I), "last_error": ([], C.c_char_p),
+    "handoff_scratch_bytes": ([I, I], Z),
+    "moe_handoff": ([P, P, P, P, P, P, I, I, P, Z, CPU_MOE_FN, P, P], I),
 }
 
 

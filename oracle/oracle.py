@@ -217,3 +217,28 @@ class HostLayer:
                              x.ctypes.data, nt, res.ctypes.data if res is not None else None, threshold, C.byref(st))
         assert rc == 0
         return out, oids, ow, logits, flags, st
+
+    def routed(self, x, ids, w, fetch=None):
+        """The routed part alone (qc_moe, cpu.c:235-261) of the rows of x with
+        the given routing: what the host computes for handed-off tokens
+        (qwen.c:658-678)."""
+        x = np.ascontiguousarray(x, np.float32)
+        ids, w = np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(w, np.float32)
+        self.ensure(ids, fetch)
+        out = np.empty((x.shape[0], self.D), np.float32)
+        rc = lib().nbo_moe(out.ctypes.data, x.ctypes.data, ids.ctypes.data, w.ctypes.data, x.shape[0], self.D, self.F,
+                           self.gate.ctypes.data, self.gt, self.up.ctypes.data, self.ut, self.down.ctypes.data, self.dt)
+        assert rc == 0
+        return out
+
+    def shared_part(self, x):
+        """The sigmoid-gated shared expert alone (qwen.c:708-713, added to a zero
+        row): a handed-off token's device row.  Zero without a shared expert."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros((x.shape[0], self.D), np.float32)
+        if self.shared:
+            sg, su, sd = self.sh_types
+            rc = lib().nbo_shared(out.ctypes.data, x.ctypes.data, x.shape[0], self.D, self.F, self.sh_gate.ctypes.data, sg,
+                                  self.sh_up.ctypes.data, su, self.sh_down.ctypes.data, sd, self.sh_inp.ctypes.data)
+            assert rc == 0
+        return out

@@ -35,6 +35,19 @@ def assert_close(got, want, what=""):
     return maxabs, rel
 
 
+def check_flagged_rows(got, H, x, flags, what):
+    """Handoff rows (flag 2) hold the sigmoid-gated shared expert alone (its
+    routed part is the host's, qwen.c:658-678; the shared expert stays on the
+    device, qwen.c:661-663), or 0 without one; invalid rows (flag 3) are 0."""
+    h = flags == 2
+    if h.any():
+        if H.shared:
+            assert_close(got[h], H.shared_part(x[h]), f"{what}: handoff rows (shared part)")
+        else:
+            assert np.all(got[h] == 0), f"{what}: handoff rows"
+    assert np.all(got[flags == 3] == 0), f"{what}: invalid rows"
+
+
 def legal_blocks(rng, typ, rows, cols):
     from test_oracle_cpu import legal_blocks as lb
     return np.ascontiguousarray(lb(rng, typ, rows, cols))
@@ -315,7 +328,7 @@ def _check_layer(L, H, x, what, resident=None):
     np.testing.assert_array_equal(gf, flags, err_msg=f"{what}: flags")
     keep = gf < 2
     maxabs, rel = assert_close(fw.out.get()[:nt][keep], out[keep], what)
-    assert np.all(fw.out.get()[:nt][~keep] == 0)
+    check_flagged_rows(fw.out.get()[:nt], H, x, gf, what)
     say(f"  {what}: unique experts {len(np.unique(ids[ids >= 0]))}, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
     return fw, st
 
@@ -402,7 +415,7 @@ def test_layer_partial_residency_mixed_flags(layer1, nt):
         np.testing.assert_array_equal(fw.flags.get()[:nt], flags)
         keep = flags < 2
         maxabs, rel = assert_close(fw.out.get()[:nt][keep], out[keep], f"mixed residency B={nt}")
-        assert np.all(fw.out.get()[:nt][~keep] == 0)
+        check_flagged_rows(fw.out.get()[:nt], H, x, flags, f"mixed residency B={nt}")
         gst = qg.PruneStats.from_buffer_copy(fw.stats.get())
         assert (gst.token_layers, gst.missing_selections, gst.skipped_selections, gst.avoided_token_handoffs) == \
                (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs)
@@ -410,6 +423,140 @@ def test_layer_partial_residency_mixed_flags(layer1, nt):
         say(f"  flags {counts}, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
     finally:
         L.desc = saved
+
+
+def _mass_resident(H, x, top):
+    """The `top` experts of largest routed mass over the batch itself."""
+    ids, w = O.route(H.logits(x))
+    score = np.zeros(512)
+    np.add.at(score, ids.ravel(), w.ravel().astype(np.float64))
+    resident = np.zeros(512, np.uint8)
+    resident[np.lexsort((np.arange(512), -score))[:top]] = 1
+    return resident
+
+
+def _cpu_moe_callback(H, calls, D=2048):
+    """nm_cpu_moe_fn running the oracle's routed part (the stand-in for the
+    reference's qc_moe, cpu.c:235-261) on the packed rows."""
+    def fn(ctx, out, xp, idp, wp, n):
+        try:
+            xs = np.ctypeslib.as_array((C.c_float * (n * D)).from_address(xp)).reshape(n, D).copy()
+            ids = np.ctypeslib.as_array((C.c_int * (n * 10)).from_address(idp)).reshape(n, 10).copy()
+            w = np.ctypeslib.as_array((C.c_float * (n * 10)).from_address(wp)).reshape(n, 10).copy()
+            y = np.ascontiguousarray(H.routed(xs, ids, w), np.float32)
+            C.memmove(out, y.ctypes.data, y.nbytes)
+            calls.append((xs, ids, w, y))
+            return 0
+        except Exception as exc:  # noqa: BLE001 - reported through the return code
+            say(f"  callback failed: {exc!r}")
+            return 1
+    return qg.CPU_MOE_FN(fn)
+
+
+@pytest.mark.parametrize("nt", [1, 4, 17])
+def test_handoff_round_trip(layer1, nt):
+    """CPU handoff of the flag-2 tokens (qwen.c:658-678): the device packs
+    exactly those tokens' input rows, ids and weights (bit-exact), the host
+    computes their routed part (oracle) through nm_moe_handoff's callback, and
+    after the merge every row matches the oracle's full layer (routed +
+    shared) within tolerance; a second accumulator gets the host rows exactly."""
+    L, H = layer1
+    x = synth.inputs(77, nt, 2048, correlated=True)
+    if nt == 1:
+        # the token's three largest selections not resident: coverage below 90 %
+        resident = np.ones(512, np.uint8)
+        resident[O.route(H.logits(x))[0][0, :3]] = 0
+    else:
+        resident = _mass_resident(H, x, 16)
+    desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    rdev = Device(resident)
+    desc.resident, desc.threshold = rdev.p, 0.10
+    saved = L.desc
+    L.desc = desc
+    try:
+        fw = synth.Forward(2048, 512, nt)
+        fw.x.set(np.concatenate([x, np.zeros((fw.tokens - nt, 2048), np.float32)]) if nt < fw.tokens else x)
+        say(f"handoff forward nt={nt}")
+        fw.run(L, nt)
+        qg.call("sync")
+    finally:
+        L.desc = saved
+    out, oids, ow, _, flags, _ = H.forward(x, resident)
+    np.testing.assert_array_equal(fw.flags.get()[:nt], flags)
+    want = np.nonzero(flags == 2)[0]
+    assert len(want) > 0 and (nt == 1 or len(want) < nt), flags
+    check_flagged_rows(fw.out.get()[:nt], H, x, flags, f"handoff B={nt}")
+    # the pack alone
+    cnt, rows = Device(shape=(1,), dtype=np.int32), Device(shape=(nt,), dtype=np.int32)
+    xp, ip, wp = Device(shape=(nt, 2048), dtype=np.float32), Device(shape=(nt, 10), dtype=np.int32), Device(shape=(nt, 10), dtype=np.float32)
+    say(f"handoff pack nt={nt}")
+    call("moe_handoff_pack", cnt.p, rows.p, xp.p, ip.p, wp.p, fw.flags.p, fw.x.p, fw.ids.p, fw.w.p, nt, 2048)
+    n = int(cnt.get()[0])
+    assert n == len(want)
+    np.testing.assert_array_equal(rows.get()[:n], want)
+    np.testing.assert_array_equal(xp.get()[:n].view('u4'), x[want].view('u4'))
+    np.testing.assert_array_equal(ip.get()[:n], oids[want])
+    np.testing.assert_array_equal(wp.get()[:n].view('u4'), ow[want].view('u4'))
+    # the round trip through the host driver
+    h = qg.host()
+    sb = h.nm_handoff_scratch_bytes(2048, nt)
+    scratch, acc2 = Device(nbytes=sb), Device(np.zeros((nt, 2048), np.float32))
+    calls = []
+    cb = _cpu_moe_callback(H, calls)
+    handed = C.c_int(-1)
+    say(f"handoff round trip nt={nt}, {n} tokens to the host")
+    assert h.nm_moe_handoff(fw.out.p, acc2.p, fw.flags.p, fw.x.p, fw.ids.p, fw.w.p, nt, 2048, scratch.p, sb, cb, None,
+                            C.byref(handed)) == 0, h.nm_last_error()
+    assert handed.value == n and len(calls) == 1
+    _, cids, _, y = calls[0]
+    np.testing.assert_array_equal(cids, oids[want])
+    got = fw.out.get()[:nt]
+    ok = flags < 3
+    maxabs, rel = assert_close(got[ok], out[ok], f"handoff round trip B={nt}")
+    a2 = acc2.get()
+    np.testing.assert_array_equal(a2[want].view('u4'), y.view('u4'))
+    assert np.all(np.delete(a2, want, axis=0) == 0)
+    say(f"  {n} of {nt} tokens handed off, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
+    # no flagged token: nothing read, no callback
+    zf = Device(np.zeros(nt, np.uint8))
+    calls.clear()
+    assert h.nm_moe_handoff(fw.out.p, None, zf.p, fw.x.p, fw.ids.p, fw.w.p, nt, 2048, scratch.p, sb, cb, None,
+                            C.byref(handed)) == 0, h.nm_last_error()
+    assert handed.value == 0 and not calls
+    np.testing.assert_array_equal(fw.out.get()[:nt].view('u4'), got.view('u4'))
+
+
+def test_handoff_pack_merge_large():
+    """Pack and merge at 3000 tokens (three 1024-token scan chunks) with
+    seeded flags 0..3: rows ascending, packed rows bit-exact, merge adds the
+    host rows at exactly the flagged rows."""
+    rng = np.random.default_rng(5)
+    nt, D = 3000, 256
+    flags = rng.integers(0, 4, nt).astype(np.uint8)
+    x = rng.standard_normal((nt, D)).astype(np.float32)
+    ids = rng.integers(0, 512, (nt, 10)).astype(np.int32)
+    w = rng.random((nt, 10)).astype(np.float32)
+    dflags, dx, dids, dw = Device(flags), Device(x), Device(ids), Device(w)
+    cnt, rows = Device(shape=(1,), dtype=np.int32), Device(shape=(nt,), dtype=np.int32)
+    xp, ip, wp = Device(shape=(nt, D), dtype=np.float32), Device(shape=(nt, 10), dtype=np.int32), Device(shape=(nt, 10), dtype=np.float32)
+    say(f"handoff pack nt={nt}")
+    call("moe_handoff_pack", cnt.p, rows.p, xp.p, ip.p, wp.p, dflags.p, dx.p, dids.p, dw.p, nt, D)
+    want = np.nonzero(flags == 2)[0]
+    n = int(cnt.get()[0])
+    assert n == len(want)
+    np.testing.assert_array_equal(rows.get()[:n], want)
+    np.testing.assert_array_equal(xp.get()[:n].view('u4'), x[want].view('u4'))
+    np.testing.assert_array_equal(ip.get()[:n], ids[want])
+    np.testing.assert_array_equal(wp.get()[:n].view('u4'), w[want].view('u4'))
+    base = rng.standard_normal((nt, D)).astype(np.float32)
+    y = np.zeros((nt, D), np.float32)
+    y[:n] = rng.standard_normal((n, D)).astype(np.float32)
+    dout, dy = Device(base), Device(y)
+    say(f"handoff merge nt={nt}")
+    call("moe_handoff_merge", dout.p, dy.p, cnt.p, rows.p, nt, D)
+    expect = base.copy()
+    expect[want] += y[:n]
+    np.testing.assert_array_equal(dout.get().view('u4'), expect.view('u4'))
 
 
 @pytest.mark.parametrize("nt,ties", [(5, 40), (17, 40), (17, 70)])

@@ -101,7 +101,8 @@ def check_outputs(fw, L, H, x, rows, what, resident=None):
     got = fw.out.get()[rows]
     keep = oflags < 2
     maxabs, rel = assert_close(got[keep], out[keep], what)
-    assert np.all(got[~keep] == 0)
+    from test_gpu_parity import check_flagged_rows
+    check_flagged_rows(got, H, x[rows], oflags, what)
     say(f"  {what}: {len(rows)} rows, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
 
 
@@ -162,8 +163,8 @@ def test_prefill_shared_expert_mixed_formats(layer1):
 
 
 def test_prefill_partial_residency(layer1):
-    """Config-4 semantics at a prefill size: 128 resident experts, coverage
-    flags and pruning bit-exact, counters equal, flagged rows zero."""
+    """Config-4 semantics at a prefill size: coverage flags and pruning
+    bit-exact, counters equal, handoff rows holding the shared part alone."""
     L, H = layer1
     nt = 200
     # correlated rows, ranked on their own routing, so that the batch mixes

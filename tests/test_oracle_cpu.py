@@ -398,6 +398,30 @@ def test_libraries_export_every_declared_symbol():
     C.CDLL(str(host))
 
 
+def test_handoff_host_checks_without_gpu():
+    """nm_moe_handoff's scratch size (count, rows, packed rows, ids, weights,
+    host rows; 256-byte aligned pieces) and its argument checks, which reject
+    before any device call."""
+    gpu = ROOT / "nebula_amd" / "lib" / "libqwen_gpu.so"
+    host = ROOT / "nebula_amd" / "lib" / "libnebula_moe.so"
+    if not gpu.exists() or not host.exists():
+        pytest.skip("native libraries not built")
+    from nebula_amd import qg
+    h = qg.host()
+    a = lambda n: (n + 255) // 256 * 256
+    for D, T in ((2048, 17), (2048, 1), (2560, 8192), (256, 3)):
+        assert h.nm_handoff_scratch_bytes(D, T) == 256 + a(4 * T) + 2 * a(4 * T * D) + 2 * a(40 * T)
+    assert h.nm_handoff_scratch_bytes(2048, 0) == 0 and h.nm_handoff_scratch_bytes(2048, 8193) == 0
+    cb = qg.CPU_MOE_FN(lambda *args: 0)
+    handed = C.c_int(7)
+    assert h.nm_moe_handoff(None, None, None, None, None, None, 4, 2048, None, 0, cb, None, C.byref(handed)) != 0
+    assert handed.value == 0 and b"invalid handoff arguments" in h.nm_last_error()
+    buf = (C.c_char * 64)()
+    p = C.addressof(buf)
+    assert h.nm_moe_handoff(p, None, p, p, p, p, 4, 2048, p, 64, cb, None, None) != 0
+    assert b"scratch" in h.nm_last_error()
+
+
 def test_reference_signatures_bind():
     """Every qg_* name the reference's ctypes caller binds for the MoE path
     (qwen/test_gpu.py:14-33) exists with the same arity in the header."""
