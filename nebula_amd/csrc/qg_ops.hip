@@ -3,6 +3,7 @@
 // list, validation and semantics (gpu.cu lines cited per function); the
 // kernels are written for CDNA4 wave64.
 #include "qg_internal.h"
+#include "qg_frag.h"
 
 static int g_width = 2560, g_ff = 640;  // gpu.cu:508-553 hard-code these
 int qg_cfg_width(void) { return g_width; }
@@ -99,9 +100,135 @@ __global__ __launch_bounds__(64) void mm_exact_kernel(float *__restrict__ out, c
     }
 }
 
+// qg_matmul for Q4_K and IQ4_NL rows with cols a multiple of 256, up to TT
+// tokens per block: the arithmetic of mm_exact_kernel (the same weight value
+// per element, lane j's chain over k = j (mod 32) in ascending k, the same
+// tree), 8 rows per block (one per 32-lane half).  Per chunk of KC columns:
+// the 8 rows' weight bytes and the tile's x rows arrive by direct
+// global->shared copies, all in flight at once; then each group's d*s and
+// -(dmin*m) (Q4_K) or each block's d (IQ4_NL) is formed once into shared
+// memory, and the rows' chains run from shared memory.
+template <int TT> struct MmTile;
+template <> struct MmTile<1> { static constexpr int KC = 4096; };
+template <> struct MmTile<4> { static constexpr int KC = 2048; };
+template <> struct MmTile<8> { static constexpr int KC = 1024; };
+template <> struct MmTile<16> { static constexpr int KC = 512; };
+template <> struct MmTile<20> { static constexpr int KC = 512; };
+
+template <int TYPE, int TT>
+__global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, const uint8_t *__restrict__ w, int rows,
+                                                     int cols, const float *__restrict__ x, int nt, size_t stride) {
+    constexpr int KC = MmTile<TT>::KC, WB = KC / 256 * 144;  // chunk columns; chunk bytes of a row
+    constexpr int NS = TYPE == QT_Q4_K ? 8 * (KC / 256) * 8 : 8 * (KC / 32);  // scale entries per chunk
+    __shared__ __attribute__((aligned(16))) float xs[TT * KC];   // [token][k], row stride kc
+    __shared__ __attribute__((aligned(16))) uint8_t ws[8 * WB];  // [row][bytes]
+    __shared__ __attribute__((aligned(16))) float2 s_sc[TYPE == QT_Q4_K ? NS : 1];
+    __shared__ float s_d[TYPE == QT_Q4_K ? 1 : NS];
+    __shared__ float s_lut[16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hw = tid >> 5, j = tid & 31;
+    const int r0 = blockIdx.x * 8, row = r0 + hw;
+    const int t0 = blockIdx.y * TT, n = min(nt - t0, TT);
+    if (TYPE == QT_IQ4_NL && tid < 16) s_lut[tid] = (float)qg_iq4nl_lut[tid];
+    Acc<TT> a;
+#pragma unroll
+    for (int t = 0; t < TT; t++) a.v[t] = 0.0f;
+    for (int c0 = 0; c0 < cols; c0 += KC) {
+        const int kc = min(KC, cols - c0), rb = kc / 256 * 144;  // this chunk's columns, bytes per row
+        // the 8 rows' bytes, contiguous per row (rows past the end repeat the last)
+        const int wp = rb / 16;
+        for (int base = wave * 64; base < 8 * wp; base += 256) {
+            const int i = base + lane, r = i / wp, pc = i - r * wp;
+            if (i < 8 * wp) dma16(w + (size_t)min(r0 + r, rows - 1) * stride + (size_t)c0 / 256 * 144 + 16 * pc, ws + 16 * base);
+        }
+        // the tile's n token rows of the chunk: piece i lands at 16 i bytes, so
+        // token t starts at t * kc floats
+        const int xp = kc / 4;
+        for (int base = wave * 64; base < n * xp; base += 256) {
+            const int i = base + lane, t = i / xp, pc = i - t * xp;
+            if (i < n * xp) dma16(x + (size_t)(t0 + t) * cols + c0 + 4 * pc, xs + 4 * base);
+        }
+        wait_vmem();
+        __syncthreads();
+        // per-group (Q4_K) or per-block (IQ4_NL) scales of the chunk, once
+        if (TYPE == QT_Q4_K) {
+            const int nsb = kc / 256;
+            for (int e = tid; e < 8 * nsb * 8; e += 256) {
+                const int r = e / (nsb * 8), sb = (e >> 3) - r * nsb, g = e & 7;
+                const uint8_t *p = ws + r * rb + sb * 144, *sc = p + 4;
+                const float d = qg_half(p), dmin = qg_half(p + 2);
+                const int sv = g < 4 ? (sc[g] & 63) : ((sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4));
+                const int mv = g < 4 ? (sc[g + 4] & 63) : ((sc[g + 4] >> 4) | ((sc[g] >> 6) << 4));
+                s_sc[e] = make_float2(d * (float)sv, -(dmin * (float)mv));
+            }
+        } else {
+            const int nb = kc / 32;
+            for (int e = tid; e < 8 * nb; e += 256) {
+                const int r = e / nb, b = e - r * nb;
+                s_d[e] = qg_half(ws + r * rb + b * 18);
+            }
+        }
+        __syncthreads();
+        if (row < rows) {
+            const uint8_t *wr = ws + hw * rb;
+            // tokens past the tile's n re-read its last row (their sums are not stored)
+            auto chains = [&](float wv, int k) {
+#pragma unroll
+                for (int t = 0; t < TT; t++) a.v[t] = __builtin_fmaf(wv, xs[min(t, n - 1) * kc + k], a.v[t]);
+            };
+            if (TYPE == QT_Q4_K) {
+                const int nsb = kc / 256;
+                for (int sb = 0; sb < nsb; sb++) {
+                    const uint8_t *p = wr + sb * 144;
+                    const float2 *c = s_sc + (hw * nsb + sb) * 8;
+#pragma unroll
+                    for (int gp = 0; gp < 4; gp++) {
+                        const int byte = p[16 + gp * 32 + j];
+#pragma unroll
+                        for (int hi = 0; hi < 2; hi++) {
+                            const float2 ds = c[2 * gp + hi];
+                            chains(__builtin_fmaf(ds.x, (float)((byte >> (hi * 4)) & 15), ds.y), sb * 256 + (2 * gp + hi) * 32 + j);
+                        }
+                    }
+                }
+            } else {
+                const int nb = kc / 32;
+                for (int b = 0; b < nb; b++) {
+                    const int q = (wr[b * 18 + 2 + (j & 15)] >> ((j >> 4) * 4)) & 15;
+                    chains(s_d[hw * nb + b] * s_lut[q], b * 32 + j);
+                }
+            }
+        }
+        __syncthreads();  // the chunk's buffers are rewritten next
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            if (t < n) {
+                const float s = qg_tree32(a.v[t]);
+                if (j == 0) out[(size_t)(t0 + t) * rows + row] = s;
+            }
+        }
+    }
+}
+
+template <int TYPE, int TT>
+void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const float *x, int nt, size_t stride, hipStream_t s) {
+    mm_tile_kernel<TYPE, TT><<<dim3((rows + 7) / 8, (nt + TT - 1) / TT), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+}
+
 template <int TYPE>
 void launch_mm_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt, size_t stride,
                      const uint8_t *extra, hipStream_t s) {
+    if constexpr (TYPE == QT_Q4_K || TYPE == QT_IQ4_NL) {
+        if (!extra && cols % 256 == 0) {
+        if (nt == 1) launch_mm_tile<TYPE, 1>(out, w, rows, cols, x, nt, stride, s);
+        else if (nt <= 4) launch_mm_tile<TYPE, 4>(out, w, rows, cols, x, nt, stride, s);
+        else if (nt <= 8) launch_mm_tile<TYPE, 8>(out, w, rows, cols, x, nt, stride, s);
+        else if (nt <= 16) launch_mm_tile<TYPE, 16>(out, w, rows, cols, x, nt, stride, s);
+        else launch_mm_tile<TYPE, 20>(out, w, rows, cols, x, nt, stride, s);
+        return;
+        }
+    }
     dim3 grid((rows + 1) / 2, 1);
     if (nt == 1) { mm_exact_kernel<TYPE, 1><<<grid, 64, 0, s>>>(out, w, type, rows, cols, x, nt, stride, extra); return; }
     if (nt <= 64) {

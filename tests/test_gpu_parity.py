@@ -84,6 +84,25 @@ def test_matmul_bitexact_all_formats(qgl):
                                               err_msg=f"type {typ} cols {cols} nt {nt}")
 
 
+def test_matmul_tiled_shapes_bitexact(qgl):
+    """The tiled Q4_K / IQ4_NL path of qg_matmul (widths a multiple of 256)
+    at dense-projection widths: several K chunks per block, every token-tile
+    size (1, 4, 8, 16, 20 and tails past them), rows not a multiple of 8;
+    bit for bit against the oracle."""
+    rng = np.random.default_rng(91011)
+    for typ in (12, 20):
+        for rows, cols in ((37, 2560), (9, 6144), (8, 256)):
+            w = legal_blocks(rng, typ, rows, cols)
+            dw = Device(w)
+            for nt in (1, 2, 5, 8, 9, 17, 20, 21):
+                say(f"matmul tiled type={typ} {rows}x{cols} nt={nt}")
+                x = rng.normal(0, .5, (nt, cols)).astype(np.float32)
+                dx, out = Device(x), Device(shape=(nt, rows), dtype=np.float32)
+                call("matmul", out.p, dw.p, typ, rows, cols, dx.p, nt)
+                np.testing.assert_array_equal(out.get().view('u4'), O.matmul(w, typ, rows, cols, x).view('u4'),
+                                              err_msg=f"type {typ} {rows}x{cols} nt {nt}")
+
+
 def test_matmul_router_shape_and_errors(qgl):
     rng = np.random.default_rng(1)
     w = rng.normal(0, .02, (512, 2048)).astype(np.float32)
