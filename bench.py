@@ -18,6 +18,9 @@ before the timed region.
             IQ4_NL down): value = tokens/s of the layer; roofline = the
             matrix-core utilisation of the dense pass (experts with >= 256
             rows) of the grouped gate/up GEMM against the int8 peak.
+--matmul:   qg_matmul (exact reference order) on the D = 2560 dense
+            projections in Q4_K at --batch tokens (default 1): value = weight
+            GB/s; cpu_baseline = the reference's qc_matmul.
 
 Printed: one JSON line.  value = tokens/s (batch / step time), the step being
 one replay of the layer's captured graph; roofline = the gate/up kernel's
@@ -369,6 +372,86 @@ def bench_prefill(args, data: str) -> dict:
     return line
 
 
+MM_SHAPES = (("qkv", 10240, 2560), ("z", 6144, 2560), ("out", 2560, 6144))
+
+
+def bench_matmul(args, data) -> dict:
+    """qg_matmul on the reference's dense projections at D = 2560 (the gated
+    DeltaNet qkv, z and out matrices of qwen.c:533-543) in Q4_K, `batch`
+    tokens (default 1): each shape's weights rotate over enough seeded copies
+    (> 512 MB) that every launch streams from HBM.  value = weight bytes of the
+    three projections / their summed time; roofline on the largest (qkv)."""
+    nt = args.batch if args.batch is not None else 1
+    rng = np.random.default_rng(5)
+    per, total_bytes, total_us, cpu = {}, 0, 0.0, None
+    for name, rows, cols in MM_SHAPES:
+        nbytes = rows * qg.row_bytes(12, cols)
+        copies = max(4, (512 << 20) // nbytes + 1)
+        w = qg.Device(nbytes=nbytes * copies)
+        for c in range(copies):
+            qg.call("synth_matrix", w.p + c * nbytes, 12, 77, (9 << 32) | c, rows, cols, qg.F(0.02))
+        x = qg.Device(rng.standard_normal((nt, cols)).astype(np.float32))
+        out = qg.Device(shape=(nt, rows), dtype=np.float32)
+        for i in range(args.warmup):
+            qg.call("matmul", out.p, w.p + (i % copies) * nbytes, 12, rows, cols, x.p, nt)
+        b, e = qg.Event(), qg.Event()
+        qg.call("sync")
+        b.record()
+        for i in range(args.steps):
+            qg.call("matmul", out.p, w.p + (i % copies) * nbytes, 12, rows, cols, x.p, nt)
+        e.record()
+        qg.call("sync")
+        us = qg.elapsed_ms(b, e) * 1e3 / args.steps
+        per[name] = {"rows": rows, "cols": cols, "us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1)}
+        total_bytes += nbytes
+        total_us += us
+        if name == "qkv" and not args.no_cpu:
+            cpu = cpu_matmul(w, rows, cols, x, nt, args.cpu_budget)
+        w.free()
+    q = per["qkv"]
+    achieved = q["GBps"]
+    return {"metric": "qg_matmul dense-projection weight streaming (Q4_K GEMV/GEMM, qkv+z+out)",
+            "value": round(total_bytes / total_us / 1e3, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(total_us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": data,
+            "config": {"workload": f"qg_matmul, Q4_K, D=2560 dense projections (qkv 10240x2560, z 6144x2560, out 2560x6144), "
+                                   f"{nt} tokens, exact reference order", "batch_tokens": nt, "per_shape": per},
+            "roofline": {"bound": "hbm", "kernel": "mm_tile_kernel (qkv)", "achieved": achieved, "peak": 8000.0, "unit": "GB/s",
+                         "frac": round(achieved / 8000.0, 4), "traffic": None},
+            "cpu_baseline": cpu}
+
+
+def cpu_matmul(w, rows, cols, x, nt, budget_s) -> dict | None:
+    """The reference's qc_matmul (cpu.c:119-148) on the same Q4_K matrix and tokens."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    try:
+        import oracle as O
+    except Exception:
+        return None
+    ref = O.ref_lib(2048)
+    if ref is None:
+        return None
+    nbytes = rows * qg.row_bytes(12, cols)
+    hw = np.empty(nbytes, np.uint8)
+    qg.call("read", hw.ctypes.data, w.p, nbytes)
+    hx = x.get()
+    out = np.empty((nt, rows), np.float32)
+    cores = len(os.sched_getaffinity(0))
+    threads = max(1, min(28, cores))
+    run = lambda: ref.qc_matmul(out.ctypes.data, hw.ctypes.data, 12, rows, cols, hx.ctypes.data, nt, threads)
+    for _ in range(3):
+        assert run() == 0
+    times, t_end = [], time.time() + budget_s
+    while len(times) < 20 or (time.time() < t_end and len(times) < 2000):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"cpu.c qc_matmul, Q4_K {rows}x{cols}, {nt} tokens, isa={ref.qc_backend_name().decode()}; "
+                      f"median of {len(times)} runs after 3 warm-ups (one host-resident matrix)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -379,6 +462,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--matmul", action="store_true",
+                    help="measure qg_matmul on the dense projections instead of the MoE layer (--batch tokens, default 1)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy kernel over MIB MiB 5 times (qg_unary identity: MIB read, MIB "
                          "written; the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes) and exit")
@@ -396,6 +481,13 @@ def main() -> int:
               "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
         return 2
     data = "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)"
+    if args.matmul:
+        if args.batch is not None and not 1 <= args.batch <= 8192:
+            print("matmul batch must be 1..8192", file=sys.stderr)
+            return 2
+        print(json.dumps(bench_matmul(args, "synthetic (seeded N(0,0.02) weights quantised to Q4_K on the device; "
+                                                "seeded N(0,1) inputs)")), flush=True)
+        return 0
     if args.config == 3:
         if args.batch is not None and not 18 <= args.batch <= 8192:
             print("prefill batch must be 18..8192", file=sys.stderr)
