@@ -103,11 +103,12 @@ __global__ __launch_bounds__(64) void mm_exact_kernel(float *__restrict__ out, c
 // qg_matmul for Q4_K and IQ4_NL rows with cols a multiple of 256, up to TT
 // tokens per block: the arithmetic of mm_exact_kernel (the same weight value
 // per element, lane j's chain over k = j (mod 32) in ascending k, the same
-// tree), 8 rows per block (one per 32-lane half).  Per chunk of KC columns:
-// the 8 rows' weight bytes and the tile's x rows arrive by direct
-// global->shared copies, all in flight at once; then each group's d*s and
-// -(dmin*m) (Q4_K) or each block's d (IQ4_NL) is formed once into shared
-// memory, and the rows' chains run from shared memory.
+// tree).  A block holds 8 RPL rows: 32-lane half h runs rows h, h + 8, ...
+// (RPL of them, sharing every x read).  Per chunk of KC columns: the rows'
+// weight bytes and the tile's x rows arrive by direct global->shared copies,
+// all in flight at once; then each group's d*s and -(dmin*m) (Q4_K) or each
+// block's d (IQ4_NL) is formed once into shared memory, and the rows' chains
+// run from shared memory.
 template <int TT> struct MmTile;
 template <> struct MmTile<1> { static constexpr int KC = 4096; };
 template <> struct MmTile<4> { static constexpr int KC = 2048; };
@@ -115,30 +116,33 @@ template <> struct MmTile<8> { static constexpr int KC = 1024; };
 template <> struct MmTile<16> { static constexpr int KC = 512; };
 template <> struct MmTile<20> { static constexpr int KC = 512; };
 
-template <int TYPE, int TT>
+template <int TYPE, int TT, int RPL>
 __global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, const uint8_t *__restrict__ w, int rows,
                                                      int cols, const float *__restrict__ x, int nt, size_t stride) {
-    constexpr int KC = MmTile<TT>::KC, WB = KC / 256 * 144;  // chunk columns; chunk bytes of a row
-    constexpr int NS = TYPE == QT_Q4_K ? 8 * (KC / 256) * 8 : 8 * (KC / 32);  // scale entries per chunk
-    __shared__ __attribute__((aligned(16))) float xs[TT * KC];   // [token][k], row stride kc
-    __shared__ __attribute__((aligned(16))) uint8_t ws[8 * WB];  // [row][bytes]
+    constexpr int KC = MmTile<TT>::KC, RB = 8 * RPL;  // chunk columns; rows per block
+    constexpr int WB = KC / 256 * 144;                                       // chunk bytes of a row
+    constexpr int NS = TYPE == QT_Q4_K ? RB * (KC / 256) * 8 : RB * (KC / 32);  // scale entries per chunk
+    __shared__ __attribute__((aligned(16))) float xs[TT * KC];    // [token][k], row stride kc
+    __shared__ __attribute__((aligned(16))) uint8_t ws[RB * WB];  // [row][bytes]
     __shared__ __attribute__((aligned(16))) float2 s_sc[TYPE == QT_Q4_K ? NS : 1];
     __shared__ float s_d[TYPE == QT_Q4_K ? 1 : NS];
     __shared__ float s_lut[16];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hw = tid >> 5, j = tid & 31;
-    const int r0 = blockIdx.x * 8, row = r0 + hw;
+    const int r0 = blockIdx.x * RB;
     const int t0 = blockIdx.y * TT, n = min(nt - t0, TT);
     if (TYPE == QT_IQ4_NL && tid < 16) s_lut[tid] = (float)qg_iq4nl_lut[tid];
-    Acc<TT> a;
+    Acc<TT> a[RPL];
 #pragma unroll
-    for (int t = 0; t < TT; t++) a.v[t] = 0.0f;
+    for (int q = 0; q < RPL; q++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) a[q].v[t] = 0.0f;
     for (int c0 = 0; c0 < cols; c0 += KC) {
         const int kc = min(KC, cols - c0), rb = kc / 256 * 144;  // this chunk's columns, bytes per row
-        // the 8 rows' bytes, contiguous per row (rows past the end repeat the last)
+        // the block's rows' bytes, contiguous per row (rows past the end repeat the last)
         const int wp = rb / 16;
-        for (int base = wave * 64; base < 8 * wp; base += 256) {
+        for (int base = wave * 64; base < RB * wp; base += 256) {
             const int i = base + lane, r = i / wp, pc = i - r * wp;
-            if (i < 8 * wp) dma16(w + (size_t)min(r0 + r, rows - 1) * stride + (size_t)c0 / 256 * 144 + 16 * pc, ws + 16 * base);
+            if (i < RB * wp) dma16(w + (size_t)min(r0 + r, rows - 1) * stride + (size_t)c0 / 256 * 144 + 16 * pc, ws + 16 * base);
         }
         // the tile's n token rows of the chunk: piece i lands at 16 i bytes, so
         // token t starts at t * kc floats
@@ -152,7 +156,7 @@ __global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, c
         // per-group (Q4_K) or per-block (IQ4_NL) scales of the chunk, once
         if (TYPE == QT_Q4_K) {
             const int nsb = kc / 256;
-            for (int e = tid; e < 8 * nsb * 8; e += 256) {
+            for (int e = tid; e < RB * nsb * 8; e += 256) {
                 const int r = e / (nsb * 8), sb = (e >> 3) - r * nsb, g = e & 7;
                 const uint8_t *p = ws + r * rb + sb * 144, *sc = p + 4;
                 const float d = qg_half(p), dmin = qg_half(p + 2);
@@ -162,58 +166,77 @@ __global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, c
             }
         } else {
             const int nb = kc / 32;
-            for (int e = tid; e < 8 * nb; e += 256) {
+            for (int e = tid; e < RB * nb; e += 256) {
                 const int r = e / nb, b = e - r * nb;
                 s_d[e] = qg_half(ws + r * rb + b * 18);
             }
         }
         __syncthreads();
-        if (row < rows) {
-            const uint8_t *wr = ws + hw * rb;
-            // tokens past the tile's n re-read its last row (their sums are not stored)
-            auto chains = [&](float wv, int k) {
+        // tokens past the tile's n re-read its last row, rows past the end the
+        // last row (their sums are not stored)
+        auto chains = [&](const float *wv, int k) {
 #pragma unroll
-                for (int t = 0; t < TT; t++) a.v[t] = __builtin_fmaf(wv, xs[min(t, n - 1) * kc + k], a.v[t]);
-            };
-            if (TYPE == QT_Q4_K) {
-                const int nsb = kc / 256;
-                for (int sb = 0; sb < nsb; sb++) {
-                    const uint8_t *p = wr + sb * 144;
-                    const float2 *c = s_sc + (hw * nsb + sb) * 8;
+            for (int t = 0; t < TT; t++) {
+                const float xv = xs[min(t, n - 1) * kc + k];
 #pragma unroll
-                    for (int gp = 0; gp < 4; gp++) {
-                        const int byte = p[16 + gp * 32 + j];
+                for (int q = 0; q < RPL; q++) a[q].v[t] = __builtin_fmaf(wv[q], xv, a[q].v[t]);
+            }
+        };
+        if (TYPE == QT_Q4_K) {
+            const int nsb = kc / 256;
+            for (int sb = 0; sb < nsb; sb++) {
 #pragma unroll
-                        for (int hi = 0; hi < 2; hi++) {
-                            const float2 ds = c[2 * gp + hi];
-                            chains(__builtin_fmaf(ds.x, (float)((byte >> (hi * 4)) & 15), ds.y), sb * 256 + (2 * gp + hi) * 32 + j);
+                for (int gp = 0; gp < 4; gp++) {
+                    int byte[RPL];
+#pragma unroll
+                    for (int q = 0; q < RPL; q++) byte[q] = ws[(hw + 8 * q) * rb + sb * 144 + 16 + gp * 32 + j];
+#pragma unroll
+                    for (int hi = 0; hi < 2; hi++) {
+                        float wv[RPL];
+#pragma unroll
+                        for (int q = 0; q < RPL; q++) {
+                            const float2 ds = s_sc[((hw + 8 * q) * nsb + sb) * 8 + 2 * gp + hi];
+                            wv[q] = __builtin_fmaf(ds.x, (float)((byte[q] >> (hi * 4)) & 15), ds.y);
                         }
+                        chains(wv, sb * 256 + (2 * gp + hi) * 32 + j);
                     }
                 }
-            } else {
-                const int nb = kc / 32;
-                for (int b = 0; b < nb; b++) {
-                    const int q = (wr[b * 18 + 2 + (j & 15)] >> ((j >> 4) * 4)) & 15;
-                    chains(s_d[hw * nb + b] * s_lut[q], b * 32 + j);
+            }
+        } else {
+            const int nb = kc / 32;
+            for (int b = 0; b < nb; b++) {
+                float wv[RPL];
+#pragma unroll
+                for (int q = 0; q < RPL; q++) {
+                    const int r = hw + 8 * q;
+                    const int qq = (ws[r * rb + b * 18 + 2 + (j & 15)] >> ((j >> 4) * 4)) & 15;
+                    wv[q] = s_d[r * nb + b] * s_lut[qq];
                 }
+                chains(wv, b * 32 + j);
             }
         }
         __syncthreads();  // the chunk's buffers are rewritten next
     }
-    if (row < rows) {
+#pragma unroll
+    for (int q = 0; q < RPL; q++) {
+        const int row = r0 + hw + 8 * q;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            if (t < n) {
-                const float s = qg_tree32(a.v[t]);
-                if (j == 0) out[(size_t)(t0 + t) * rows + row] = s;
-            }
+            const float s = qg_tree32(a[q].v[t]);
+            if (j == 0 && t < n && row < rows) out[(size_t)(t0 + t) * rows + row] = s;
         }
     }
 }
 
+// Two rows per lane halve the shared-memory reads per product (they pay off
+// for the long token tiles), when the matrix still fills 512 blocks.
 template <int TYPE, int TT>
 void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const float *x, int nt, size_t stride, hipStream_t s) {
-    mm_tile_kernel<TYPE, TT><<<dim3((rows + 7) / 8, (nt + TT - 1) / TT), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    const int ty = (nt + TT - 1) / TT;
+    if (TT >= 16 && ((rows + 15) / 16) * ty >= 512)
+        mm_tile_kernel<TYPE, TT, 2><<<dim3((rows + 15) / 16, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    else
+        mm_tile_kernel<TYPE, TT, 1><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
 }
 
 template <int TYPE>

@@ -87,11 +87,12 @@ def test_matmul_bitexact_all_formats(qgl):
 def test_matmul_tiled_shapes_bitexact(qgl):
     """The tiled Q4_K / IQ4_NL path of qg_matmul (widths a multiple of 256)
     at dense-projection widths: several K chunks per block, every token-tile
-    size (1, 4, 8, 16, 20 and tails past them), rows not a multiple of 8;
+    size (1, 4, 8, 16, 20 and tails past them), rows not a multiple of 8, and a
+    matrix tall enough for two rows per lane;
     bit for bit against the oracle."""
     rng = np.random.default_rng(91011)
     for typ in (12, 20):
-        for rows, cols in ((37, 2560), (9, 6144), (8, 256)):
+        for rows, cols in ((37, 2560), (9, 6144), (8, 256), (8203, 256)):
             w = legal_blocks(rng, typ, rows, cols)
             dw = Device(w)
             for nt in (1, 2, 5, 8, 9, 17, 20, 21):
