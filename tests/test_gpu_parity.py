@@ -455,15 +455,16 @@ def _mass_resident(H, x, top):
     return resident
 
 
-def _cpu_moe_callback(H, calls, D=2048):
+def _cpu_moe_callback(H, calls, D=2048, fetch=None):
     """nm_cpu_moe_fn running the oracle's routed part (the stand-in for the
-    reference's qc_moe, cpu.c:235-261) on the packed rows."""
+    reference's qc_moe, cpu.c:235-261) on the packed rows (expert bytes from
+    `fetch`, a copy of the device's, when given)."""
     def fn(ctx, out, xp, idp, wp, n):
         try:
             xs = np.ctypeslib.as_array((C.c_float * (n * D)).from_address(xp)).reshape(n, D).copy()
             ids = np.ctypeslib.as_array((C.c_int * (n * 10)).from_address(idp)).reshape(n, 10).copy()
             w = np.ctypeslib.as_array((C.c_float * (n * 10)).from_address(wp)).reshape(n, 10).copy()
-            y = np.ascontiguousarray(H.routed(xs, ids, w), np.float32)
+            y = np.ascontiguousarray(H.routed(xs, ids, w, fetch), np.float32)
             C.memmove(out, y.ctypes.data, y.nbytes)
             calls.append((xs, ids, w, y))
             return 0

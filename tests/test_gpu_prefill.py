@@ -203,6 +203,55 @@ def test_prefill_partial_residency(layer1):
         L.desc = saved
 
 
+def test_prefill_handoff_round_trip(layer1):
+    """The CPU handoff at a prefill size (200 tokens, 20 resident experts):
+    nm_moe_handoff packs the flag-2 tokens (count and rows checked against the
+    oracle's flags), the oracle computes their routed part, and after the
+    merge sampled rows of every flag match the oracle's full layer."""
+    from test_gpu_parity import _cpu_moe_callback
+    L, H = layer1
+    nt = 200
+    x = synth.inputs(77, nt, 2048, correlated=True)
+    ids_all, w_all = O.route(H.logits(x))
+    score = np.zeros(512)
+    np.add.at(score, ids_all.ravel(), w_all.ravel().astype(np.float64))
+    resident = np.zeros(512, np.uint8)
+    resident[np.lexsort((np.arange(512), -score))[:20]] = 1
+    desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    rdev = Device(resident)
+    desc.resident, desc.threshold = rdev.p, 0.10
+    saved = L.desc
+    L.desc = desc
+    try:
+        fw = synth.Forward(2048, 512, nt)
+        fw.x.set(x)
+        say(f"prefill forward with residency nt={nt}")
+        fw.run(L, nt)
+        qg.call("sync")
+    finally:
+        L.desc = saved
+    flags, _ = O.coverage(ids_all, w_all, resident)
+    np.testing.assert_array_equal(fw.flags.get()[:nt], flags)
+    want = np.nonzero(flags == 2)[0]
+    assert 0 < len(want) < nt
+    h = qg.host()
+    sb = h.nm_handoff_scratch_bytes(2048, nt)
+    scratch = Device(nbytes=sb)
+    calls = []
+    cb = _cpu_moe_callback(H, calls, fetch=fetcher(L))
+    handed = C.c_int(-1)
+    say(f"prefill handoff round trip: {len(want)} of {nt} tokens to the host")
+    assert h.nm_moe_handoff(fw.out.p, None, fw.flags.p, fw.x.p, fw.ids.p, fw.w.p, nt, 2048, scratch.p, sb, cb, None,
+                            C.byref(handed)) == 0, h.nm_last_error()
+    assert handed.value == len(want) and len(calls) == 1
+    np.testing.assert_array_equal(calls[0][0].view('u4'), x[want].view('u4'))
+    rows = np.unique(np.concatenate([sample_rows(nt, 16, 3), want[:8]]))
+    out, _, _, _, oflags, _ = H.forward(x[rows], resident, fetch=fetcher(L))
+    ok = oflags < 3
+    maxabs, rel = assert_close(fw.out.get()[rows][ok], out[ok], "prefill handoff round trip")
+    say(f"  {len(rows)} sampled rows, max-abs {maxabs:.2e}, rel-L2 {rel:.2e}")
+
+
 def test_prefill_residual_matches_forward(layer1):
     """qg_moe_forward_residual at a prefill size: h + MoE(RMSNorm(h))."""
     L, H = layer1
