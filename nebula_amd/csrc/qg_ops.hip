@@ -243,7 +243,8 @@ template <int TYPE>
 void launch_mm_exact(float *out, const uint8_t *w, int type, int rows, int cols, const float *x, int nt, size_t stride,
                      const uint8_t *extra, hipStream_t s) {
     if constexpr (TYPE == QT_Q4_K || TYPE == QT_IQ4_NL) {
-        if (!extra && cols % 256 == 0) {
+        // the tiled kernel's 16-byte copies need 16-byte aligned rows and x
+        if (!extra && cols % 256 == 0 && (((uintptr_t)w | (uintptr_t)x | stride) & 15) == 0) {
         if (nt == 1) launch_mm_tile<TYPE, 1>(out, w, rows, cols, x, nt, stride, s);
         else if (nt <= 4) launch_mm_tile<TYPE, 4>(out, w, rows, cols, x, nt, stride, s);
         else if (nt <= 8) launch_mm_tile<TYPE, 8>(out, w, rows, cols, x, nt, stride, s);

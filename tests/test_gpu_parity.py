@@ -104,6 +104,23 @@ def test_matmul_tiled_shapes_bitexact(qgl):
                                               err_msg=f"type {typ} {rows}x{cols} nt {nt}")
 
 
+def test_matmul_unaligned_operands_bitexact(qgl):
+    """Q4_K rows and x at addresses that are only 4-byte aligned take the
+    byte-granular kernel; results stay bit for bit the oracle's."""
+    rng = np.random.default_rng(27)
+    rows, cols, nt = 11, 512, 5
+    w = legal_blocks(rng, 12, rows, cols)
+    x = rng.normal(0, .5, (nt, cols)).astype(np.float32)
+    dw = Device(nbytes=w.nbytes + 16)
+    dx = Device(nbytes=x.nbytes + 16)
+    call("write", dw.p + 4, w.ctypes.data, w.nbytes)
+    call("write", dx.p + 4, x.ctypes.data, x.nbytes)
+    out = Device(shape=(nt, rows), dtype=np.float32)
+    say("matmul unaligned Q4_K")
+    call("matmul", out.p, dw.p + 4, 12, rows, cols, dx.p + 4, nt)
+    np.testing.assert_array_equal(out.get().view('u4'), O.matmul(w, 12, rows, cols, x).view('u4'))
+
+
 def test_matmul_router_shape_and_errors(qgl):
     rng = np.random.default_rng(1)
     w = rng.normal(0, .02, (512, 2048)).astype(np.float32)
