@@ -122,6 +122,9 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
  * the sigmoid-gated shared expert (which stays on the device, qwen.c:661-663),
  * or 0 without one; qg_moe_handoff_pack/merge move the routed part through
  * the host.  flags==3 rows are 0.
+ * Device pointers to weights, activations, outputs and the workspace must be
+ * 16-byte aligned (qg_alloc returns 256-byte aligned memory); otherwise the
+ * call returns an invalid-value error and launches nothing.
  * tokens 1..8192: up to 17 the decode kernels (any format qg_matmul takes);
  * above, the prefill grouped GEMMs, which need Q4_K gate/up, Q4_K or IQ4_NL
  * down, D a multiple of 256 and F a multiple of 128 (else an error). */

@@ -1233,8 +1233,15 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     return hipGetLastError();
 }
 
+// The layer kernels copy weight, activation and output rows with 16-byte
+// direct global->shared copies and vector accesses.
+bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 int validate_layer(const qg_moe_layer *L, int nt) {
     if (!L || nt < 1 || nt > QG_MAX_TOKENS) return hipErrorInvalidValue;
+    if (!al16(L->router) || !al16(L->gate) || !al16(L->up) || !al16(L->down) || !al16(L->sh_gate) || !al16(L->sh_up) ||
+        !al16(L->sh_down) || !al16(L->sh_gate_inp) || !al16(L->router_bias))
+        return hipErrorInvalidValue;
     const int D = L->width, F = L->ff;
     if (D < 256 || D % 256 || D > 8192 || F < 32 || F % 32 || F > 4096) return hipErrorInvalidValue;
     if (!L->router || !L->gate || !L->up || !L->down) return hipErrorInvalidValue;
@@ -1286,7 +1293,8 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
                    const qg_moe_layer *L, void *workspace, size_t ws_bytes) {
     int rc = validate_layer(L, nt);
     if (rc) return rc;
-    if (!out || !ids || !weights || !x || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt))
+    if (!out || !ids || !weights || !x || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt) ||
+        !al16(out) || !al16(x) || !al16(workspace))
         return hipErrorInvalidValue;
     if (nt > MB) return qg_prefill_forward(out, nullptr, ids, weights, flags, stats, x, nullptr, 0, nt, L, workspace);
     if (!dec_ok(L)) return qg_generic_forward(out, ids, weights, flags, stats, x, nt, L, workspace, ws_bytes);
@@ -1297,7 +1305,8 @@ int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *f
                             float *out, int nt, const qg_moe_layer *L, void *workspace, size_t ws_bytes) {
     int rc = validate_layer(L, nt);
     if (rc) return rc;
-    if (!h || !ids || !weights || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt))
+    if (!h || !ids || !weights || !workspace || ws_bytes < qg_moe_workspace_bytes(L->width, L->ff, nt) || !al16(h) ||
+        !al16(xn_out) || !al16(out) || !al16(workspace))
         return hipErrorInvalidValue;
     if (nt > MB) return qg_prefill_forward(out, h, ids, weights, flags, stats, h, xn_out, 1, nt, L, workspace);
     if (dec_ok(L)) return dec_forward(out, h, ids, weights, flags, stats, h, xn_out, 1, nt, L, (uint8_t *)workspace);

@@ -121,6 +121,25 @@ def test_matmul_unaligned_operands_bitexact(qgl):
     np.testing.assert_array_equal(out.get().view('u4'), O.matmul(w, 12, rows, cols, x).view('u4'))
 
 
+def test_forward_rejects_unaligned_pointers(layer1):
+    """qg_moe_forward / _residual with a misaligned activation, output or
+    expert pointer return an invalid-value error (nothing is launched)."""
+    L, _ = layer1
+    nt = 4
+    fw = synth.Forward(2048, 512, nt)
+    bad_desc = qg.MoeLayer.from_buffer_copy(L.desc)
+    bad_desc.gate = bad_desc.gate + 4
+    cases = [("x", fw.out.p, fw.x.p + 4, L.desc), ("out", fw.out.p + 4, fw.x.p, L.desc), ("gate", fw.out.p, fw.x.p, bad_desc)]
+    for what, out, x, desc in cases:
+        say(f"forward with misaligned {what}")
+        rc = qg.lib().qg_moe_forward(out, fw.ids.p, fw.w.p, fw.flags.p, None, x, nt, C.byref(desc), fw.ws.p, fw.ws_bytes)
+        assert rc != 0, what
+    rc = qg.lib().qg_moe_forward_residual(fw.x.p + 4, fw.ids.p, fw.w.p, fw.flags.p, None, None, None, nt, C.byref(L.desc),
+                                          fw.ws.p, fw.ws_bytes)
+    assert rc != 0
+    qg.call("sync")
+
+
 def test_matmul_router_shape_and_errors(qgl):
     rng = np.random.default_rng(1)
     w = rng.normal(0, .02, (512, 2048)).astype(np.float32)
