@@ -185,6 +185,10 @@ int qg_device_info(char *name, size_t name_len, int *cus, int *clock_khz, int *m
  * sigma*N(0,1) from a counter-based hash; encoded to type 0/12/20.  The
  * bytes equal the CPU generator's in oracle/nb_synth.c. */
 int qg_synth_matrix(void *out, int type, uint64_t seed, uint64_t stream, int rows, int cols, float sigma);
+/* `experts` such matrices in one launch: matrix e uses stream
+ * (tensor << 32 | e) and starts e * rows * row_bytes(type, cols) bytes after
+ * out, the per-tensor expert layout of a layer. */
+int qg_synth_experts(void *out, int type, uint64_t seed, int tensor, int experts, int rows, int cols, float sigma);
 
 #ifdef __cplusplus
 }

@@ -90,8 +90,11 @@ QG_DEV double f16_to_f64(uint32_t h) { return (double)qg_half_u16(h); }
 QG_DEV double clampd(double v, double lo, double hi) { return v < lo ? lo : v > hi ? hi : v; }
 
 // One Q4_K superblock from 256 values (same steps as the host encoder).
+// Bytes are written straight to `blk`; every per-group array is indexed by
+// unrolled loops only, so it lives in registers.
 QG_DEV void encode_q4k(uint8_t *blk, const float *x) {
     double scale[8], offs[8], maxs = 0, maxm = 0;
+#pragma unroll
     for (int g = 0; g < 8; g++) {
         double lo = 0, hi = 0;
         for (int l = 0; l < 32; l++) { const double v = x[g * 32 + l]; if (v < lo) lo = v; if (v > hi) hi = v; }
@@ -103,73 +106,96 @@ QG_DEV void encode_q4k(uint8_t *blk, const float *x) {
     const uint32_t d16 = f32_to_f16((float)(maxs / 63.0)), m16 = f32_to_f16((float)(maxm / 63.0));
     const double d = f16_to_f64(d16), dm = f16_to_f64(m16);
     int s[8], m[8];
+#pragma unroll
     for (int g = 0; g < 8; g++) {
         s[g] = d > 0 ? (int)clampd(__builtin_rint(scale[g] / d), 0, 63) : 0;
         m[g] = dm > 0 ? (int)clampd(__builtin_rint(offs[g] / dm), 0, 63) : 0;
     }
-    uint8_t out[144];
-    for (int i = 0; i < 144; i++) out[i] = 0;
-    out[0] = (uint8_t)d16; out[1] = (uint8_t)(d16 >> 8); out[2] = (uint8_t)m16; out[3] = (uint8_t)(m16 >> 8);
+    blk[0] = (uint8_t)d16; blk[1] = (uint8_t)(d16 >> 8); blk[2] = (uint8_t)m16; blk[3] = (uint8_t)(m16 >> 8);
+#pragma unroll
     for (int g = 0; g < 4; g++) {
-        out[4 + g] = (uint8_t)((s[g] & 63) | ((s[g + 4] >> 4) << 6));
-        out[8 + g] = (uint8_t)((m[g] & 63) | ((m[g + 4] >> 4) << 6));
-        out[12 + g] = (uint8_t)((s[g + 4] & 15) | ((m[g + 4] & 15) << 4));
+        blk[4 + g] = (uint8_t)((s[g] & 63) | ((s[g + 4] >> 4) << 6));
+        blk[8 + g] = (uint8_t)((m[g] & 63) | ((m[g + 4] >> 4) << 6));
+        blk[12 + g] = (uint8_t)((s[g + 4] & 15) | ((m[g + 4] & 15) << 4));
     }
-    for (int g = 0; g < 8; g++) {
-        const double step = d * (double)s[g], off = dm * (double)m[g];
+#pragma unroll
+    for (int gp = 0; gp < 4; gp++) {
+        const double step0 = d * (double)s[2 * gp], off0 = dm * (double)m[2 * gp];
+        const double step1 = d * (double)s[2 * gp + 1], off1 = dm * (double)m[2 * gp + 1];
         for (int l = 0; l < 32; l++) {
-            const int q = step > 0 ? (int)clampd(__builtin_rint(((double)x[g * 32 + l] + off) / step), 0, 15) : 0;
-            out[16 + (g / 2) * 32 + l] |= (uint8_t)(q << ((g % 2) * 4));
+            const int q0 = step0 > 0 ? (int)clampd(__builtin_rint(((double)x[2 * gp * 32 + l] + off0) / step0), 0, 15) : 0;
+            const int q1 = step1 > 0 ? (int)clampd(__builtin_rint(((double)x[(2 * gp + 1) * 32 + l] + off1) / step1), 0, 15) : 0;
+            blk[16 + gp * 32 + l] = (uint8_t)(q0 | (q1 << 4));
         }
     }
-    for (int i = 0; i < 144; i++) blk[i] = out[i];
+}
+
+// Nearest IQ4_NL table entry of v (lowest index on ties, the host encoder's
+// strict-less scan).
+QG_DEV int iq4nl_nearest(double v) {
+    constexpr int lut[16] = {-127,-104,-83,-65,-49,-35,-22,-10,1,13,25,38,53,69,89,113};
+    double err = __builtin_fabs(v - lut[0]);
+    int best = 0;
+#pragma unroll
+    for (int q = 1; q < 16; q++) { const double e = __builtin_fabs(v - lut[q]); if (e < err) { err = e; best = q; } }
+    return best;
 }
 
 QG_DEV void encode_iq4nl(uint8_t *blk, const float *x) {
-    const int lut[16] = {-127,-104,-83,-65,-49,-35,-22,-10,1,13,25,38,53,69,89,113};
     double amax = 0;
     for (int j = 0; j < 32; j++) { const double a = __builtin_fabs((double)x[j]); if (a > amax) amax = a; }
     const uint32_t d16 = f32_to_f16((float)(amax / 127.0));
     const double d = f16_to_f64(d16);
-    uint8_t out[18];
-    for (int i = 0; i < 18; i++) out[i] = 0;
-    out[0] = (uint8_t)d16; out[1] = (uint8_t)(d16 >> 8);
-    for (int j = 0; j < 32; j++) {
-        int best = 8;
-        if (d > 0) {
-            const double v = (double)x[j] / d;
-            double err = __builtin_fabs(v - lut[0]);
-            best = 0;
-            for (int q = 1; q < 16; q++) { const double e = __builtin_fabs(v - lut[q]); if (e < err) { err = e; best = q; } }
-        }
-        out[2 + j % 16] |= (uint8_t)(best << ((j / 16) * 4));
+    blk[0] = (uint8_t)d16; blk[1] = (uint8_t)(d16 >> 8);
+    for (int j = 0; j < 16; j++) {
+        const int q0 = d > 0 ? iq4nl_nearest((double)x[j] / d) : 8;
+        const int q1 = d > 0 ? iq4nl_nearest((double)x[j + 16] / d) : 8;
+        blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
     }
-    for (int i = 0; i < 18; i++) blk[i] = out[i];
 }
 
-// One thread per block (256 values for Q4_K, 32 for IQ4_NL, 1 for F32).
-__global__ __launch_bounds__(64) void synth_kernel(uint8_t *out, int type, uint64_t seed, uint64_t stream, int rows, int cols,
-                                                   float sigma, size_t rb) {
+// One thread per quantisation block (256 values for Q4_K, 32 for IQ4_NL, 1
+// for F32) of `experts` consecutive matrices: matrix e (stream base | e) sits
+// e * rows * rb bytes after `out`.  A block's values are staged in shared
+// memory (no per-thread scratch memory).
+constexpr int SYN_THREADS = 32;
+__global__ __launch_bounds__(SYN_THREADS) void synth_kernel(uint8_t *out, int type, uint64_t seed, uint64_t stream, int experts,
+                                                            int rows, int cols, float sigma, size_t rb) {
+    __shared__ float stage[SYN_THREADS * 256];
     const int block = type == QT_Q4_K ? 256 : type == QT_IQ4_NL ? 32 : 1;
-    const int per_row = cols / block;
+    const size_t per_row = (size_t)(cols / block), per_expert = (size_t)rows * per_row;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)rows * per_row) return;
-    const int r = (int)(i / per_row), c0 = (int)(i % per_row) * block;
-    float v[256];
-    for (int j = 0; j < block; j++) v[j] = (float)((double)sigma * gauss(seed, stream, (uint64_t)r * cols + c0 + j));
-    uint8_t *dst = out + (size_t)r * rb;
+    if (i >= per_expert * (size_t)experts) return;
+    const int e = (int)(i / per_expert);
+    const size_t j = i % per_expert;
+    const int r = (int)(j / per_row), c0 = (int)(j % per_row) * block;
+    const uint64_t st = stream | (uint64_t)(uint32_t)e;
+    float *v = stage + threadIdx.x * 256;
+    for (int k = 0; k < block; k++) v[k] = (float)((double)sigma * gauss(seed, st, (uint64_t)r * cols + c0 + k));
+    uint8_t *dst = out + ((size_t)e * rows + r) * rb;
     if (type == QT_F32) *(float *)(dst + (size_t)c0 * 4) = v[0];
     else if (type == QT_Q4_K) encode_q4k(dst + (size_t)(c0 / 256) * 144, v);
     else encode_iq4nl(dst + (size_t)(c0 / 32) * 18, v);
 }
 
+int synth_launch(void *out, int type, uint64_t seed, uint64_t stream, int experts, int rows, int cols, float sigma) {
+    const size_t rb = qg_row_bytes_host(type, cols);
+    if (!out || !rb || rows < 1 || experts < 1 || (type != QT_F32 && type != QT_Q4_K && type != QT_IQ4_NL)) return hipErrorInvalidValue;
+    const int block = type == QT_Q4_K ? 256 : type == QT_IQ4_NL ? 32 : 1;
+    const size_t n = (size_t)experts * rows * (cols / block);
+    if ((n + SYN_THREADS - 1) / SYN_THREADS > 0x7fffffffULL) return hipErrorInvalidValue;
+    synth_kernel<<<(unsigned)((n + SYN_THREADS - 1) / SYN_THREADS), SYN_THREADS, 0, qg_stream()>>>(
+        (uint8_t *)out, type, seed, stream, experts, rows, cols, sigma, rb);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" int qg_synth_matrix(void *out, int type, uint64_t seed, uint64_t stream, int rows, int cols, float sigma) {
-    const size_t rb = qg_row_bytes_host(type, cols);
-    if (!out || !rb || rows < 1 || (type != QT_F32 && type != QT_Q4_K && type != QT_IQ4_NL)) return hipErrorInvalidValue;
-    const int block = type == QT_Q4_K ? 256 : type == QT_IQ4_NL ? 32 : 1;
-    const size_t n = (size_t)rows * (cols / block);
-    synth_kernel<<<(unsigned)((n + 63) / 64), 64, 0, qg_stream()>>>((uint8_t *)out, type, seed, stream, rows, cols, sigma, rb);
-    return hipGetLastError();
+    return synth_launch(out, type, seed, stream, 1, rows, cols, sigma);
+}
+
+extern "C" int qg_synth_experts(void *out, int type, uint64_t seed, int tensor, int experts, int rows, int cols, float sigma) {
+    if (tensor < 0) return hipErrorInvalidValue;
+    return synth_launch(out, type, seed, (uint64_t)(uint32_t)tensor << 32, experts, rows, cols, sigma);
 }

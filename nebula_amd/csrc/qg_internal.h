@@ -6,6 +6,11 @@
 // The calling thread's launch stream (null stream, or the capture stream).
 hipStream_t qg_stream(void);
 
+// Grows a library-owned scratch buffer to at least `need` bytes (0 or an
+// error code).  Superseded buffers stay allocated until the process ends, so
+// a graph captured with the old address never touches freed memory.
+int qg_scratch_grow(void **buf, size_t *cap, size_t need);
+
 // Shapes used by the entry points that take no width (gather, scatter,
 // reduce, mtp_moe, shared_add); set by qg_moe_configure.
 int qg_cfg_width(void);

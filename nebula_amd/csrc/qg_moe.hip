@@ -825,20 +825,13 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
         return hipErrorInvalidValue;
     if (!slots || !mid || !x || !ids || !weights || !g || !u || !d) return hipErrorInvalidValue;
     // Scratch for the dispatch and the entry-indexed rows, grown on demand
-    // (never inside a capture: the first call per shape must be eager).
+    // (never inside a capture: the first call per shape must be eager; an
+    // outgrown buffer stays allocated for graphs captured with it).
     static thread_local void *scratch = nullptr;
     static thread_local size_t scratch_bytes = 0;
     const WsLayout lay = ws_layout(D, F);
-    if (scratch_bytes < lay.total) {
-        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-        if (qg_stream() && hipStreamIsCapturing(qg_stream(), &st) == hipSuccess && st != hipStreamCaptureStatusNone)
-            return hipErrorInvalidValue;
-        if (scratch) (void)hipFree(scratch);
-        scratch = nullptr;
-        scratch_bytes = 0;
-        if (hipMalloc(&scratch, lay.total) != hipSuccess) return hipErrorOutOfMemory;
-        scratch_bytes = lay.total;
-    }
+    int grc = qg_scratch_grow(&scratch, &scratch_bytes, lay.total);
+    if (grc) return grc;
     hipStream_t s = qg_stream();
     uint8_t *ws = (uint8_t *)scratch;
     Disp *ds = (Disp *)(ws + lay.disp);
@@ -864,20 +857,12 @@ int qg_mtp_moe(float *slots, float *mid, const float *x, const int *ids, const f
 int qg_moe_dispatch(int *offsets, int *row_token, int *row_slot, int *status, const int *ids, int nt) {
     if (!offsets || !row_token || !row_slot || !status || !ids || nt < 1 || nt > QG_MAX_TOKENS) return hipErrorInvalidValue;
     // chunk histograms, grown on demand (never inside a capture: the first
-    // call per size must be eager)
+    // call per size must be eager; an outgrown buffer stays allocated for
+    // graphs captured with it)
     static thread_local void *scratch = nullptr;
     static thread_local size_t scratch_bytes = 0;
-    const size_t need = qg_prefill_dispatch_scratch(nt);
-    if (scratch_bytes < need) {
-        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-        if (qg_stream() && hipStreamIsCapturing(qg_stream(), &st) == hipSuccess && st != hipStreamCaptureStatusNone)
-            return hipErrorInvalidValue;
-        if (scratch) (void)hipFree(scratch);
-        scratch = nullptr;
-        scratch_bytes = 0;
-        if (hipMalloc(&scratch, need) != hipSuccess) return hipErrorOutOfMemory;
-        scratch_bytes = need;
-    }
+    int grc = qg_scratch_grow(&scratch, &scratch_bytes, qg_prefill_dispatch_scratch(nt));
+    if (grc) return grc;
     return qg_prefill_dispatch(offsets, row_token, row_slot, status, ids, nt, scratch);
 }
 

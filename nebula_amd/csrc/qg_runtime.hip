@@ -5,6 +5,8 @@
 #include "qg_internal.h"
 #include <stdlib.h>
 #include <string.h>
+#include <mutex>
+#include <vector>
 
 // Kernels launch on the calling thread's stream: the null stream, or the
 // capture stream between qg_graph_begin and qg_graph_end (gpu.cu:10,21-34).
@@ -70,6 +72,37 @@ int qg_zero(void *d, size_t n) {
     return hipGetLastError();
 }
 int qg_sync(void) { return hipDeviceSynchronize(); }
+
+}  // extern "C"
+
+// Library-owned scratch that grows on demand.  A graph captured earlier may
+// still hold the old buffer's address, so a superseded buffer is never freed:
+// it is kept on a retired list until the process ends.  Growth is at least
+// twofold, so the retired buffers together stay below the live one's size.
+// Growing is refused inside a capture (the allocation would not be replayed).
+namespace {
+std::mutex g_retired_mu;
+std::vector<void *> *g_retired = nullptr;
+}
+int qg_scratch_grow(void **buf, size_t *cap, size_t need) {
+    if (*cap >= need) return hipSuccess;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (tl_stream && hipStreamIsCapturing(tl_stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone)
+        return hipErrorInvalidValue;
+    size_t bytes = need > 2 * *cap ? need : 2 * *cap;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return hipErrorOutOfMemory;
+    if (*buf) {
+        std::lock_guard<std::mutex> lock(g_retired_mu);
+        if (!g_retired) g_retired = new std::vector<void *>();
+        g_retired->push_back(*buf);
+    }
+    *buf = p;
+    *cap = bytes;
+    return hipSuccess;
+}
+
+extern "C" {
 int qg_memory(size_t *f, size_t *t) { return hipMemGetInfo(f, t); }
 const char *qg_error(int e) { return hipGetErrorString((hipError_t)e); }
 

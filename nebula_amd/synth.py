@@ -95,8 +95,7 @@ def build_layer(spec: LayerSpec, resident: np.ndarray | None = None, threshold: 
                                                ("down", DOWN, spec.down_type, D, Fd, "d")):
         per = rows * rb[key]
         buf = qg.Device(nbytes=EXPERTS * per)
-        for e in range(EXPERTS):
-            _synth(buf, e * per, typ, spec.seed, stream(tensor, e), rows, cols)
+        qg.call("synth_experts", buf.p, typ, spec.seed, tensor, EXPERTS, rows, cols, qg.F(SIGMA))
         L.bufs[name] = buf
     desc = qg.MoeLayer()
     desc.width, desc.ff = D, Fd

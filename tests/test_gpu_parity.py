@@ -62,6 +62,13 @@ def test_device_generator_matches_host(qgl, typ, rows, cols):
     dev = Device(nbytes=rows * qg.row_bytes(typ, cols))
     qg.call("synth_matrix", dev.p, typ, 1234, strm, rows, cols, qg.F(0.02))
     np.testing.assert_array_equal(dev.get(), O.fill_matrix(typ, 1234, strm, rows, cols))
+    # several experts of one tensor in one launch: expert e from stream (tensor << 32 | e)
+    per = rows * qg.row_bytes(typ, cols)
+    many = Device(nbytes=3 * per)
+    qg.call("synth_experts", many.p, typ, 1234, synth.UP, 3, rows, cols, qg.F(0.02))
+    got = many.get()
+    for e in range(3):
+        np.testing.assert_array_equal(got[e * per:(e + 1) * per], O.fill_matrix(typ, 1234, synth.stream(synth.UP, e), rows, cols))
 
 
 # ---------------- drop-in operators ----------------

@@ -434,3 +434,30 @@ def test_reference_signatures_bind():
         assert m, name
         args = [a for a in m.group(1).split(",") if a.strip() and a.strip() != "void"]
         assert len(args) == n, (name, args)
+
+
+def test_tensor_bytes_host_logic():
+    """qg_tensor_bytes (gpu.cu:114-120): row bytes of dims[0] columns times
+    the other dims; columns must fill whole blocks; a zero dim or overflow is
+    an error.  Pure host arithmetic, so it runs without a GPU."""
+    gpu = ROOT / "nebula_amd" / "lib" / "libqwen_gpu.so"
+    if not gpu.exists():
+        pytest.skip("native libraries not built")
+    from nebula_amd import qg
+    lib = qg.lib()
+    out = C.c_uint64()
+
+    def tb(typ, dims):
+        d = (C.c_uint64 * 4)(*dims)
+        rc = lib.qg_tensor_bytes(typ, d, C.byref(out))
+        return None if rc else out.value
+    assert tb(0, (2560, 512, 1, 1)) == 2560 * 512 * 4
+    assert tb(12, (2560, 640, 512, 1)) == 10 * 144 * 640 * 512
+    assert tb(20, (640, 2560, 512, 1)) == 20 * 18 * 2560 * 512
+    assert tb(12, (2048, 512, 512, 1)) == 8 * 144 * 512 * 512
+    assert tb(1, (100, 3, 1, 1)) == 600
+    assert tb(12, (2000, 1, 1, 1)) is None          # not a whole superblock
+    assert tb(20, (48, 1, 1, 1)) is None
+    assert tb(12, (2560, 0, 1, 1)) is None          # zero dim
+    assert tb(0, (1 << 30, 1 << 30, 1 << 30, 1)) is None  # overflow
+    assert tb(99, (256, 1, 1, 1)) is None           # unknown type
