@@ -131,6 +131,18 @@ size_t qg_moe_workspace_bytes(int width, int ff, int tokens);
 int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
                    const float *x, int tokens, const qg_moe_layer *layer, void *workspace, size_t workspace_bytes);
 
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  qg_moe_forward with the library's own workspace, a static
+ * 16 MiB array in device memory per GPU (held until the process ends); no
+ * allocation of any kind happens.  Layers whose qg_moe_workspace_bytes at
+ * `tokens` exceeds 16 MiB are rejected with the invalid-value code before
+ * anything is launched (every decode batch of 1..17 tokens fits up to
+ * D=8192/F=4096; at D=2048/F=512 prefill batches up to about 120 tokens
+ * fit).  Calls that overlap on one GPU share the workspace and race. */
+int qg_moe_forward_noalloc(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats,
+                           const float *x, int tokens, const qg_moe_layer *layer);
+
 /* The layer applied to a residual stream, as one layer of qwen_target's loop
  * without attention (qwen.c:759-762): x = RMSNorm(h) (eps 1e-6, unit weight,
  * the norm of gpu.cu:204-214), h += MoE(x).  xn_out [tokens, D] (the

@@ -34,6 +34,7 @@
 #include "qg_internal.h"
 #include "qg_frag.h"
 #include <hip/hip_ext.h>
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -1262,6 +1263,33 @@ __global__ void add_rows_kernel(float *h, const float *o, size_t n) {
 
 }  // namespace
 
+// Library-held workspace for qg_moe_forward_noalloc: one copy per GPU in
+// the code object's device memory (it lives until the process ends).  Host
+// code never passes `scratch` itself to a kernel: its host-side name is a
+// stand-in, not a device address.  The device address of each GPU's copy is
+// looked up once per device (hipGetSymbolAddress with that device current)
+// and kept in noalloc_ptr.
+constexpr size_t NOALLOC_BYTES = (size_t)16 << 20;
+constexpr int NOALLOC_DEVICES = 64;
+__device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+void *noalloc_ptr[NOALLOC_DEVICES] = {nullptr};
+std::mutex noalloc_mu;
+
+int noalloc_workspace(void **ws) {
+    int dev = 0, rc = hipGetDevice(&dev);
+    if (rc) return rc;
+    if (dev < 0 || dev >= NOALLOC_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(noalloc_mu);
+    if (!noalloc_ptr[dev]) {
+        void *p = nullptr;
+        if ((rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))) return rc;
+        if (!p) return hipErrorInvalidSymbol;
+        noalloc_ptr[dev] = p;
+    }
+    *ws = noalloc_ptr[dev];
+    return hipSuccess;
+}
+
 bool qg_kernel_event_pair(int slot, void **begin, void **end) {
     if (slot < 0 || 2 * slot + 1 >= tl_kev_n || !tl_kev[2 * slot] || !tl_kev[2 * slot + 1]) return false;
     *begin = tl_kev[2 * slot];
@@ -1299,6 +1327,23 @@ int qg_moe_forward(float *out, int *ids, float *weights, unsigned char *flags, q
     if (nt > MB) return qg_prefill_forward(out, nullptr, ids, weights, flags, stats, x, nullptr, 0, nt, L, workspace);
     if (!dec_ok(L)) return qg_generic_forward(out, ids, weights, flags, stats, x, nt, L, workspace, ws_bytes);
     return dec_forward(out, nullptr, ids, weights, flags, stats, x, nullptr, 0, nt, L, (uint8_t *)workspace);
+}
+
+// qg_moe_forward with the library's static per-device workspace: no
+// allocation of any kind, for callers that cannot allocate.  Rejects (invalid
+// value, nothing launched) a layer whose workspace at `nt` tokens exceeds
+// NOALLOC_BYTES.  The workspace needs no initialisation (every kernel writes
+// what it later reads), so nothing is cleared between calls; calls that
+// overlap on one GPU share it and race.
+int qg_moe_forward_noalloc(float *out, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, const float *x,
+                           int nt, const qg_moe_layer *L) {
+    int rc = validate_layer(L, nt);
+    if (rc) return rc;
+    const size_t need = qg_moe_workspace_bytes(L->width, L->ff, nt);
+    if (!need || need > NOALLOC_BYTES) return hipErrorInvalidValue;
+    void *ws = nullptr;
+    if ((rc = noalloc_workspace(&ws))) return rc;
+    return qg_moe_forward(out, ids, weights, flags, stats, x, nt, L, ws, NOALLOC_BYTES);
 }
 
 int qg_moe_forward_residual(float *h, int *ids, float *weights, unsigned char *flags, qg_prune_stats *stats, float *xn_out,

@@ -34,6 +34,7 @@ SIGNATURES = {
     # additions
     "moe_configure": ([I, I], I), "moe_dispatch": ([P, P, P, P, P, I], I),
     "moe_workspace_bytes": ([I, I, I], Z), "moe_phase_events": ([P, I], I), "moe_forward": ([P, P, P, P, P, P, I, P, P, Z], I),
+    "moe_forward_noalloc": ([P, P, P, P, P, P, I, P], I),
     "moe_forward_residual": ([P, P, P, P, P, P, P, I, P, P, Z], I), "moe_kernel_events": ([P, I], I),
     "event_create": ([], P), "event_destroy": ([P], None), "event_record": ([P], I), "event_elapsed": ([P, P, P], I),
     "device_info": ([P, Z, P, P, P, P], I),
