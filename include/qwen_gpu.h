@@ -77,7 +77,8 @@ int qg_shared_add(float *out, const float *shared, const float *gate, int tokens
  * shapes and drives the layer from the host, qwen.c:633-735) ---- */
 
 /* Hidden width D and expert FFN width F used by the width-less entry points
- * above.  D multiple of 256, F multiple of 32, D <= 8192, F <= 4096. */
+ * above, for the calling thread (each thread starts at 2560/640).  D
+ * multiple of 256, F multiple of 32, D <= 8192, F <= 4096. */
 int qg_moe_configure(int width, int ff);
 
 /* Dispatch of routing ids into per-expert contiguous row lists (CSR), the

@@ -20,7 +20,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 HIP_SOURCES = ["qg_runtime.hip", "qg_ops.hip", "qg_moe.hip", "qg_decode.hip", "qg_prefill.hip", "nb_synth.hip"]
-HOST_SOURCES = ["moe_host.c"]
+HOST_SOURCES = ["moe_host.c", "qwen_moe.c"]
 ARCH = os.environ.get("NEBULA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

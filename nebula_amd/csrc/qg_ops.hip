@@ -5,7 +5,9 @@
 #include "qg_internal.h"
 #include "qg_frag.h"
 
-static int g_width = 2560, g_ff = 640;  // gpu.cu:508-553 hard-code these
+// Per calling thread, like the launch stream: callers on two threads with
+// differently shaped models do not see each other's setting.
+static thread_local int g_width = 2560, g_ff = 640;  // gpu.cu:508-553 hard-code these
 int qg_cfg_width(void) { return g_width; }
 int qg_cfg_ff(void) { return g_ff; }
 

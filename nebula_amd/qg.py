@@ -53,6 +53,40 @@ HOST_SIGNATURES = {
 }
 
 
+# libnebula_moe.so's qwen_* surface (include/qwen_moe.h, after qwen.h)
+QWEN_CPU_MOE_FN = C.CFUNCTYPE(I, P, P, P, P, P, I, P, I, P, I, P, I)
+QWEN_SIGNATURES = {
+    "validate_index": ([C.c_char_p], I), "open": ([C.c_char_p, I, I, I], P), "close": ([P], None),
+    "last_error": ([], C.c_char_p), "max_draft": ([], I), "set_hotlist": ([P, P, I, I], I),
+    "set_cpu_threads": ([P, I], I), "cpu_threads": ([P], I), "get_cpu_stats": ([P, P], None),
+    "handoff_version": ([], I), "get_prune_stats": ([P, P], I), "get_handoff_profile": ([P, P], None),
+    "get_stats": ([P, P], None), "profile_routes": ([P, C.c_char_p], I), "set_cpu_moe": ([P, QWEN_CPU_MOE_FN, P], I),
+    "moe_shape": ([P, P, P, P, P], I), "moe": ([P, I, P, P, I, I], I),
+}
+
+
+class QwenStats(C.Structure):
+    """qwen_stats (qwen.h:11-18)."""
+    _fields_ = [(k, C.c_uint64) for k in (
+        "gpu_weight_bytes", "gpu_state_bytes", "gpu_workspace_bytes", "gpu_arena_bytes", "target_tokens", "mtp_tokens",
+        "expert_handoffs", "expert_upload_bytes", "expert_hits", "expert_requests", "metadata_read_bytes", "ple_read_bytes",
+        "host_weight_bytes", "host_staging_bytes")] + [(k, C.c_double) for k in (
+        "target_seconds", "mtp_seconds", "expert_handoff_host_seconds", "expert_dma_seconds", "ple_lookup_seconds",
+        "core_load_seconds", "host_load_seconds")] + [(k, C.c_int) for k in (
+        "target_position", "mtp_position", "context", "resident_per_layer")]
+
+
+class QwenHandoffProfile(C.Structure):
+    """qwen_handoff_profile (qwen.h:19-21)."""
+    _fields_ = [("layer_calls", C.c_uint64 * 48), ("layer_handoffs", C.c_uint64 * 48)]
+
+
+class QwenCpuStats(C.Structure):
+    """qwen_cpu_stats (qwen.h:68-71)."""
+    _fields_ = [(k, C.c_uint64) for k in ("layer_handoffs", "token_layers", "missing_selections", "activation_bytes")] + [
+        ("compute_seconds", C.c_double), ("handoff_seconds", C.c_double)]
+
+
 class PruneStats(C.Structure):
     _fields_ = [(k, C.c_uint64) for k in ("token_layers", "missing_selections", "skipped_selections", "avoided_token_handoffs")] + [
         ("skipped_mass", C.c_double)]
@@ -98,6 +132,21 @@ def host() -> C.CDLL:
             fn.argtypes, fn.restype = args, res
         _HOST = handle
     return _HOST
+
+
+_QWEN = None
+
+
+def qwen() -> C.CDLL:
+    """libnebula_moe.so with the qwen_* surface bound."""
+    global _QWEN
+    if _QWEN is None:
+        handle = host()
+        for name, (args, res) in QWEN_SIGNATURES.items():
+            fn = getattr(handle, "qwen_" + name)
+            fn.argtypes, fn.restype = args, res
+        _QWEN = handle
+    return _QWEN
 
 
 def call(name: str, *args) -> None:
