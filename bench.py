@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import gc
 import json
 import os
 import sys
@@ -187,6 +188,46 @@ def kernel_times(step, names, steps) -> dict:
     return kern
 
 
+_HOST_CPUS = None
+
+
+def host_cpus() -> dict:
+    """This process's CPUs: model name, sockets, physical cores and logical
+    CPUs among the CPUs it may run on, from /proc and /sys.  Read once, at
+    the first call, which main() makes before the OpenMP runtime starts (with
+    OMP_PROC_BIND set the runtime binds the calling thread to one place,
+    which would shrink sched_getaffinity afterwards)."""
+    global _HOST_CPUS
+    if _HOST_CPUS is not None:
+        return _HOST_CPUS
+    cpus = sorted(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cores, sockets = set(), set()
+    for c in cpus:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            pkg = int((base / "physical_package_id").read_text())
+            core = int((base / "core_id").read_text())
+        except (OSError, ValueError):
+            pkg, core = 0, c
+        sockets.add(pkg)
+        cores.add((pkg, core))
+    _HOST_CPUS = {"model": model, "sockets": len(sockets), "physical_cores": len(cores), "logical_cpus": len(cpus)}
+    return _HOST_CPUS
+
+
+def cpu_threads() -> int:
+    """min(28, physical cores available): 28 is cpu.c's own cap (cpu.c:121,150,164)."""
+    return max(1, min(28, host_cpus()["physical_cores"]))
+
+
 def cpu_baseline(wl, budget_s: float, tokens: int | None = None) -> dict | None:
     """The reference's cpu.c on layer 0 of the workload: router qc_matmul (F32),
     qc_moe on the routed experts, shared expert through qc_matmul x 3 plus the
@@ -220,8 +261,8 @@ def cpu_baseline(wl, budget_s: float, tokens: int | None = None) -> dict | None:
             buf = np.empty(L.bufs[name].nbytes, np.uint8)
             qg.call("read", buf.ctypes.data, L.bufs[name].p, buf.nbytes)
             shared[name] = buf
-    cores = len(os.sched_getaffinity(0))
-    threads = max(1, min(28, cores))
+    hc = host_cpus()
+    threads = cpu_threads()
     ws = ref.qc_create(max(nt, 1), threads)
     out = np.empty((nt, D), np.float32)
     logits = np.empty((nt, EXPERTS), np.float32)
@@ -260,7 +301,11 @@ def cpu_baseline(wl, budget_s: float, tokens: int | None = None) -> dict | None:
             "sample": f"cpu.c {parts} on layer 0, {nt} tokens"
                       f"{f' (the first {nt} of the {wl.nt}-token batch, their GPU routing)' if nt < wl.nt else ''}, "
                       f"isa={ref.qc_backend_name().decode()}; "
-                      f"median of {len(times)} runs after 3 warm-ups; OMP threads={threads} of {cores} host CPUs"}
+                      f"median of {len(times)} runs after 3 warm-ups; {threads} OpenMP threads "
+                      f"(OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}, OMP_PLACES={os.environ.get('OMP_PLACES')}) on "
+                      f"{hc['physical_cores']} physical cores / {hc['logical_cpus']} logical CPUs, {hc['sockets']} socket(s), "
+                      f"{hc['model']}",
+            "host": hc, "isa": ref.qc_backend_name().decode()}
 
 
 def bench_stack(args) -> dict:
@@ -351,7 +396,7 @@ def bench_prefill(args, data: str) -> dict:
     line = {
         "metric": METRIC, "value": round(nt / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": data,
+        "scaling": "weak", "vs_baseline": None, "dtype": DTYPE, "data": data,
         "config": {"workload": f"config3: routed-MoE prefill, B={nt}, D=2048, 512 experts top-10, F=512, Q4_K gate/up, "
                                "IQ4_NL down, router biased to Zipf(1.1) expert popularity; one captured graph per step",
                    "batch_tokens": nt, "experts_touched": touched, "dense_experts": int(dense.sum()),
@@ -364,7 +409,7 @@ def bench_prefill(args, data: str) -> dict:
                    "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
         "roofline": {"bound": "mfma", "kernel": "gate_up_dense", "achieved": round(achieved, 1) if achieved else None,
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4) if achieved else None,
-                     **load_traffic(f"gate_up_dense_config3_B{nt}"), "algorithmic_ops": ops_gu(rows_dense)},
+                     **load_traffic(f"gate_up_dense_config3_B{nt}", 1), "algorithmic_ops": ops_gu(rows_dense)},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
@@ -436,8 +481,7 @@ def cpu_matmul(w, rows, cols, x, nt, budget_s) -> dict | None:
     qg.call("read", hw.ctypes.data, w.p, nbytes)
     hx = x.get()
     out = np.empty((nt, rows), np.float32)
-    cores = len(os.sched_getaffinity(0))
-    threads = max(1, min(28, cores))
+    threads = cpu_threads()
     run = lambda: ref.qc_matmul(out.ctypes.data, hw.ctypes.data, 12, rows, cols, hx.ctypes.data, nt, threads)
     for _ in range(3):
         assert run() == 0
@@ -462,12 +506,23 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sections", action="store_true",
+                    help="default workload only: leave out the other configurations of the metric (B=1/4/8, config 4, "
+                         "the 48-layer stack, the prefill)")
     ap.add_argument("--matmul", action="store_true",
                     help="measure qg_matmul on the dense projections instead of the MoE layer (--batch tokens, default 1)")
+    ap.add_argument("--counter-pass", type=int, default=0, metavar="P",
+                    help="for rocprofv3 counter runs: build the workload, print each layer's routing and algorithmic "
+                         "bytes as one JSON line, then run P eager passes over the layers in order (dispatch k of a "
+                         "kernel is layer k %% layers) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy kernel over MIB MiB 5 times (qg_unary identity: MIB read, MIB "
                          "written; the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes) and exit")
     args = ap.parse_args()
+    # the CPU baseline's OpenMP placement (read when the runtime starts)
+    host_cpus()
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
         src, dst = qg.Device(nbytes=n), qg.Device(nbytes=n)
@@ -476,6 +531,8 @@ def main() -> int:
         qg.call("sync")
         print(json.dumps({"calibration_copy_bytes": n, "copies": 5, "kernel": "unary_kernel (identity)"}), flush=True)
         return 0
+    if args.counter_pass:
+        return counter_pass(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the layer; --gpus {args.gpus} is not supported "
               "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
@@ -505,7 +562,7 @@ def main() -> int:
         line = {
             "metric": METRIC, "value": round(1 / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": r["steps"], "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": data,
+            "scaling": "weak", "vs_baseline": None, "dtype": DTYPE, "data": data,
             "config": {"workload": f"config2: {r['layers']}-layer routed-MoE stack, B=1, D=2048, 512 experts top-10, F=512, Q4_K; "
                                    "h <- h + MoE(RMSNorm(h)); one captured graph",
                        "layers": r["layers"], "stack_bytes": int(r["bytes"]),
@@ -518,65 +575,171 @@ def main() -> int:
         return 0
 
     wl = Workload(args.config, batch, args.layers, seed=9000)
-    uniq = [wl.unique_experts(i) for i in range(len(wl.layers))]
-    U = float(np.mean(uniq))
-    ms, kern = time_decode(wl, args.steps, args.warmup)
-    gu_ms = kern.get("gate_up")
-    nbytes = layer_bytes(wl.nt, U, wl.shared)
-    gu_bytes = gateup_bytes(wl.nt, U, wl.shared)
-    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None
+    r = decode_result(wl, args.steps, args.warmup)
     names = {0: f"config0: routed-MoE layer, B={wl.nt}, D=2048, 512 experts top-10, F=512, Q4_K",
              1: f"config1: routed-MoE layer, B={wl.nt}, D=2048, 512 experts top-10, F=512, Q4_K gate/up, IQ4_NL down, shared Q4_K expert",
              4: f"config4: config 1 at B={wl.nt} with 128/512 resident experts per layer and 90% coverage flags"}
     line = {
         "metric": METRIC,
-        "value": round(wl.nt / (ms * 1e-3), 1),
+        "value": round(wl.nt / (r["ms"] * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(r["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": DTYPE,
         "data": data,
-        "config": {"workload": names[args.config],
-                   "arithmetic": "router fp32 in the reference order; experts on fp16 16x16x32 MFMA with exact integer "
-                                 "weights x fp16 hi/lo activation planes, fp32 accumulate and scales",
-                   "batch_tokens": wl.nt, "layers_rotated": len(wl.layers), "unique_experts_mean": U,
-                   "layer_bytes": int(nbytes), "layer_hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                   "layer_hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                   "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
-        "roofline": {"bound": "hbm", "kernel": "gate_up", "achieved": round(achieved, 1) if achieved else None,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-                     **load_traffic(f"gate_up_config{args.config}_B{wl.nt}"),
-                     "algorithmic_bytes": int(gu_bytes)},
+        "config": {"workload": names[args.config], "arithmetic": ARITHMETIC,
+                   "batch_tokens": wl.nt, "layers_rotated": len(wl.layers), "unique_experts_mean": r["U"],
+                   "layer_bytes": int(r["nbytes"]), "layer_hbm_GBps": round(r["nbytes"] / (r["ms"] * 1e-3) / 1e9, 1),
+                   "layer_hbm_frac": r["layer_frac"],
+                   "kernel_us": {k: round(v * 1000, 2) for k, v in r["kern"].items()}},
+        "roofline": {"bound": "hbm", "kernel": "gate_up", "achieved": round(r["achieved"], 1) if r["achieved"] else None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r["achieved"] / HBM_PEAK_GBS, 4) if r["achieved"] else None,
+                     **load_traffic(f"gate_up_config{args.config}_B{wl.nt}", len(wl.layers)),
+                     "algorithmic_bytes": int(r["gu_bytes"])},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
+    if args.config == 1 and args.batch is None and not args.no_sections:
+        # the rest of the metric in the same line: B=4/8 on the same layers,
+        # config 4, B=1 (config 0), the 48-layer stack and the prefill
+        line["config"]["sections"] = sections(wl, args)
     print(json.dumps(line), flush=True)
     return 0
 
 
-def load_traffic(name: str) -> dict:
+def counter_pass(args) -> int:
+    """Eager passes over the workload's layers in order, for counter runs."""
+    if args.config == 3:
+        nt = args.batch if args.batch is not None else 2048
+        wl = PrefillWorkload(nt, seed=9300)
+        ids, _ = wl.routing()
+        n_e = np.bincount(ids[ids >= 0].ravel(), minlength=EXPERTS)
+        dense = n_e >= DENSE_MIN
+        info = {"config": 3, "batch": nt, "layers": [{"layer": 0, "dense_experts": int(dense.sum()),
+                                                       "dense_rows": int(n_e[dense].sum()),
+                                                       "gate_up_dense_algorithmic_bytes": int(dense.sum()) * GATEUP_BYTES
+                                                       + int(n_e[dense].sum()) * D * 4}]}
+    else:
+        batch = args.batch if args.batch is not None else (17 if args.config in (1, 4) else 1)
+        wl = Workload(args.config, batch, args.layers, seed=9000)
+        layers = []
+        for i in range(len(wl.layers)):
+            u = wl.unique_experts(i)
+            layers.append({"layer": i, "unique_experts": u, "gate_up_algorithmic_bytes": int(gateup_bytes(batch, u, wl.shared))})
+        info = {"config": args.config, "batch": batch, "layers": layers}
+    qg.call("sync")
+    print(json.dumps(info), flush=True)
+    for _ in range(args.counter_pass):
+        for i in range(len(wl.layers)):
+            wl.step(i)
+    qg.call("sync")
+    return 0
+
+
+DTYPE = "f16x2+f32"
+ARITHMETIC = ("router fp32 in the reference's order (ids bit-exact); experts on fp16 16x16x32 MFMA: exact integer "
+              "weights x two fp16 activation planes (hi = fp16(x), lo = fp16(x - hi), ~22 significant bits), fp32 "
+              "accumulate, fp32 group/superblock scales")
+
+
+def decode_result(wl: Workload, steps: int, warmup: int) -> dict:
+    uniq = [wl.unique_experts(i) for i in range(len(wl.layers))]
+    U = float(np.mean(uniq))
+    ms, kern = time_decode(wl, steps, warmup)
+    gu_ms = kern.get("gate_up")
+    nbytes = layer_bytes(wl.nt, U, wl.shared)
+    gu_bytes = gateup_bytes(wl.nt, U, wl.shared)
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None
+    return {"ms": ms, "kern": kern, "U": U, "nbytes": nbytes, "gu_bytes": gu_bytes, "achieved": achieved,
+            "layer_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def decode_section(wl: Workload, steps: int, warmup: int, cpu_budget: float | None) -> dict:
+    r = decode_result(wl, steps, warmup)
+    out = {"tokens_per_s": round(wl.nt / (r["ms"] * 1e-3), 1), "us_per_layer": round(r["ms"] * 1e3, 2),
+           "unique_experts_mean": r["U"], "layer_bytes": int(r["nbytes"]), "layer_hbm_frac": r["layer_frac"],
+           "gate_up_GBps": round(r["achieved"], 1) if r["achieved"] else None,
+           "gate_up_hbm_frac": round(r["achieved"] / HBM_PEAK_GBS, 4) if r["achieved"] else None,
+           "kernel_us": {k: round(v * 1000, 2) for k, v in r["kern"].items()}}
+    if cpu_budget:
+        c = cpu_baseline(wl, cpu_budget)
+        if c:
+            out["cpu_tokens_per_s"] = c["value"]
+    return out
+
+
+def sections(wl1: Workload, args) -> dict:
+    """Every other configuration of the metric, measured in the same run."""
+    steps, warm = min(args.steps, 100), min(args.warmup, 10)
+    cpu = None if args.no_cpu else min(args.cpu_budget, 3.0)
+    out = {}
+    for nt in (4, 8):
+        wl1.nt = nt
+        wl1.fw = synth.Forward(D, FF, nt)
+        wl1.x = synth.inputs(9000 + 1000 + nt, nt, D, correlated=True)
+        wl1.fw.x.set(wl1.x)
+        out[f"config1_B{nt}"] = decode_section(wl1, steps, warm, cpu)
+    # config 4: the same layers with 128 resident experts each and the coverage flags
+    wl1.nt = 17
+    wl1.fw = synth.Forward(D, FF, 17)
+    wl1.x = synth.inputs(9000 + 1000, 17, D, correlated=True)
+    wl1.fw.x.set(wl1.x)
+    for L in wl1.layers:
+        mask = resident_set(L, seed=L.spec.seed + 77)
+        L.bufs["resident"] = qg.Device(mask)
+        L.desc.resident, L.desc.threshold = L.bufs["resident"].p, 0.10
+    flags = np.concatenate([wl1.routing(i)[1] for i in range(len(wl1.layers))])
+    sec = decode_section(wl1, steps, warm, None)
+    sec["flag_counts"] = np.bincount(flags, minlength=4).tolist()
+    out["config4_B17"] = sec
+    del wl1.layers[:]
+    gc.collect()
+    wl0 = Workload(0, 1, args.layers, seed=9000)
+    out["config0_B1"] = decode_section(wl0, steps, warm, cpu)
+    del wl0
+    gc.collect()
+    a = argparse.Namespace(layers=48, warmup=20, steps=40)
+    r = bench_stack(a)
+    out["config2_stack48_B1"] = {"tokens_per_s": round(1 / (r["ms"] * 1e-3), 1), "us_per_layer": round(r["ms"] * 1000 / 48, 2),
+                                 "stack_bytes": int(r["bytes"]),
+                                 "stack_hbm_frac": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    gc.collect()
+    a = argparse.Namespace(batch=2048, warmup=warm, steps=min(args.steps, 50), no_cpu=True, cpu_budget=0)
+    p = bench_prefill(a, "")
+    pc = p["config"]
+    out["config3_prefill_B2048"] = {
+        "tokens_per_s": p["value"], "ms_per_layer": p["ms_per_step"],
+        "dense_pass_int8_util_algorithmic": pc["dense_pass_int8_util_algorithmic"],
+        "dense_pass_fp16_util_issued": pc["dense_pass_fp16_util_issued"],
+        "gate_up_dense_TOPS": p["roofline"]["achieved"], "gate_up_dense_int8_frac": p["roofline"]["frac"],
+        "dense_experts": pc["dense_experts"], "layer_hbm_frac": pc["layer_hbm_frac"], "kernel_us": pc["kernel_us"]}
+    return out
+
+
+def load_traffic(name: str, layers: int) -> dict:
     """HBM bytes per launch of the roofline kernel, measured with rocprofv3
     FETCH_SIZE/WRITE_SIZE counters scaled by a copy kernel of known size
-    (profiles/traffic.json): {"traffic": bytes or None, "traffic_detail": ...}.
-    The counter runs profile the first two layers of the rotation, so the
-    detail carries their algorithmic bytes and the measured/algorithmic ratio."""
+    (profiles/traffic.json, written from the counter runs).  Reported only
+    when the counter runs covered the same layers this run averages over
+    (the first `layers` seeded layers of the workload), so `traffic` and
+    `algorithmic_bytes` describe the same launches; the record's own
+    algorithmic mean and the ratio ride along."""
     p = ROOT / "profiles" / "traffic.json"
     try:
         rec = json.loads(p.read_text()).get(name) if p.exists() else None
     except (OSError, ValueError):
         rec = None
-    if not rec:
+    if not rec or sorted(l["layer"] for l in rec.get("layers", [])) != list(range(layers)):
         return {"traffic": None}
-    return {"traffic": rec["bytes"],
-            "traffic_detail": {"layers_profiled": [l["layer"] for l in rec.get("layers", [])],
-                               "algorithmic_bytes_profiled": rec["algorithmic_bytes"],
-                               "measured_over_algorithmic": rec["ratio"], "source": rec.get("profile")}}
+    return {"traffic": rec["bytes"], "traffic_algorithmic_bytes": rec["algorithmic_bytes"],
+            "traffic_over_algorithmic": rec["ratio"], "traffic_source": rec.get("profile")}
 
 
 if __name__ == "__main__":
