@@ -675,11 +675,37 @@ def decode_section(wl: Workload, steps: int, warmup: int, cpu_budget: float | No
     return out
 
 
+def graph_floor(reps: int = 200) -> dict:
+    """Replay time of a captured graph of n dependent one-block kernels
+    (qg_zero of 256 bytes), n = 1, 3, 5, 10: the floor under a layer of n
+    kernels, whatever they compute."""
+    buf = qg.Device(nbytes=256)
+    out = {}
+    for n in (1, 3, 5, 10):
+        g = C.c_void_p()
+        qg.call("graph_begin", C.byref(g))
+        for _ in range(n):
+            qg.call("zero", buf.p, 256)
+        qg.call("graph_end", g)
+        for _ in range(20):
+            qg.call("graph_launch", g)
+        qg.call("sync")
+        b, e = qg.Event(), qg.Event()
+        b.record()
+        for _ in range(reps):
+            qg.call("graph_launch", g)
+        e.record()
+        qg.call("sync")
+        out[str(n)] = round(qg.elapsed_ms(b, e) * 1e3 / reps, 2)
+        qg.lib().qg_graph_destroy(g)
+    return out
+
+
 def sections(wl1: Workload, args) -> dict:
     """Every other configuration of the metric, measured in the same run."""
     steps, warm = min(args.steps, 100), min(args.warmup, 10)
     cpu = None if args.no_cpu else min(args.cpu_budget, 3.0)
-    out = {}
+    out = {"graph_floor_us": graph_floor()}
     for nt in (4, 8):
         wl1.nt = nt
         wl1.fw = synth.Forward(D, FF, nt)
