@@ -675,30 +675,34 @@ def decode_section(wl: Workload, steps: int, warmup: int, cpu_budget: float | No
     return out
 
 
-def graph_floor(reps: int = 200) -> dict:
-    """Replay time of a captured graph of n dependent one-block kernels
-    (qg_zero of 256 bytes), n = 1, 3, 5, 10: the floor under a layer of n
-    kernels, whatever they compute."""
+def graph_floor(reps: int = 50) -> dict:
+    """What a chain of kernels costs whatever they compute: the device time
+    per dependent one-block kernel (qg_zero of 256 bytes) inside one captured
+    graph of 100 such kernels, the resulting floor of a 3- and a 5-kernel
+    layer, and the host-side replay rate of a one-kernel graph (back-to-back
+    hipGraphLaunch calls)."""
     buf = qg.Device(nbytes=256)
-    out = {}
-    for n in (1, 3, 5, 10):
+
+    def replay_us(n, r):
         g = C.c_void_p()
         qg.call("graph_begin", C.byref(g))
         for _ in range(n):
             qg.call("zero", buf.p, 256)
         qg.call("graph_end", g)
-        for _ in range(20):
+        for _ in range(5):
             qg.call("graph_launch", g)
         qg.call("sync")
         b, e = qg.Event(), qg.Event()
         b.record()
-        for _ in range(reps):
+        for _ in range(r):
             qg.call("graph_launch", g)
         e.record()
         qg.call("sync")
-        out[str(n)] = round(qg.elapsed_ms(b, e) * 1e3 / reps, 2)
         qg.lib().qg_graph_destroy(g)
-    return out
+        return qg.elapsed_ms(b, e) * 1e3 / r
+    per = replay_us(100, reps) / 100
+    return {"per_dependent_kernel_us": round(per, 2), "floor_3_kernels_us": round(3 * per, 2),
+            "floor_5_kernels_us": round(5 * per, 2), "one_kernel_graph_replay_us": round(replay_us(1, 200), 2)}
 
 
 def sections(wl1: Workload, args) -> dict:
