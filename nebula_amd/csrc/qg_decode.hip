@@ -1191,18 +1191,15 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const int items2 = tiles * (F / GU2_ROWS), per2 = (GU2_NT - 1) * (F / GU2_ROWS);
     int nwg2 = items2 < GU_WGS ? items2 : GU_WGS;
     if ((long long)nwg2 * per2 < items2) nwg2 = (items2 + per2 - 1) / per2;
-    if (D == 2048 && F % GU2_ROWS == 0) {
+    if (D == 2048) {
+        // F is a multiple of 32 (validate_layer), so of GU2_ROWS
         if (inl) dec_launch(2, dec_gateup2_kernel<true>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
         else dec_launch(2, dec_gateup2_kernel<false>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
     } else {
+        // D = 2560 (dec_ok): the register-weight kernel, 10 superblocks per row
         const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
-        if (D == 2048) {
-            if (inl) dec_launch(2, dec_gateup_kernel<8, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-            else dec_launch(2, dec_gateup_kernel<8, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-        } else {
-            if (inl) dec_launch(2, dec_gateup_kernel<10, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-            else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
-        }
+        if (inl) dec_launch(2, dec_gateup_kernel<10, true>, dim3(nwg), dim3(256), gu_bytes, s, G2);
+        else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
     }
     if ((rc = hipGetLastError())) return rc;
     const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;

@@ -82,6 +82,16 @@ QG_DEV void dma16_ordered(const void *g, void *lds_base) {
                  : "v"(g), "s"(base)
                  : "memory");
 }
+// dma16_ordered for 4 bytes per lane (global_load_lds_dword): lane l's word
+// lands at lds_base + 4*l.
+QG_DEV void dma4_ordered(const void *g, void *lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(qg_lds_void *)lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(base)
+                 : "memory");
+}
 QG_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order), leaving the other counters alone.

@@ -39,6 +39,7 @@
 #include "qg_internal.h"
 #include "qg_frag.h"
 #include <hip/hip_ext.h>
+#include <type_traits>
 
 namespace {
 
@@ -46,8 +47,8 @@ constexpr int PF_MIN = QG_MAX_DECODE + 1;   // smallest batch on this path
 constexpr int PF_CHUNK = 32;                 // tokens per routing chunk (one 32-bit mask per expert)
 constexpr int PT = 64;                       // rows per GEMM tile
 constexpr int KC = 256;                      // K elements per staged chunk
-constexpr int GU_FB = 128;                   // F rows per gate/up item (32 per wave)
-constexpr int DN_DB = 256;                   // D rows per down item (64 per wave)
+constexpr int GU_FB = 128;                   // F rows per gate/up item (16 per wave)
+constexpr int DN_DB = 256;                   // D rows per down item (32 per wave)
 constexpr int NG = QG_EXPERTS + 1;           // groups: experts + shared expert
 constexpr int DENSE_MIN = 256;               // rows from which an expert runs in the dense pass
 constexpr int STAGE_BYTES = PT * 2 * KC * 2; // [64 rows][2 planes][256] fp16
@@ -388,6 +389,9 @@ __global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_s
 
 // ---------------- GEMM building blocks ----------------
 
+constexpr int PF_WAVES = 8;                  // waves per GEMM workgroup
+constexpr int NCT = 2;                       // column tiles of 16 weight rows per wave
+
 // Stage K chunk `chunk` of the tile's first nrows rows (a multiple of 16):
 // plane rows of `planes` (row stride `stride` elements per plane, 2 planes
 // per source row; source row of tile row r = src[r]) into `stage`, swizzled;
@@ -395,15 +399,15 @@ __global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_s
 // group sums of the chunk ([tile row][plane][8]).
 QG_DEV void stage_rows(uint8_t *stage, uint8_t *sums, const _Float16 *planes, int stride, const _Float16 *sum_planes,
                        int sum_stride, const int *src, int chunk, int nck, int nrows, int wave, int lane) {
-    for (int q = wave; q < nrows; q += 4) {
+    for (int q = wave; q < nrows; q += PF_WAVES) {
         const int R = 2 * q + (lane >> 5), tr = R >> 1, p = R & 1;
         int c = (lane & 31) ^ (tr & 15);
         if (c >= nck) c = 0;  // positions no reader uses
-        dma16(planes + ((size_t)src[tr] * 2 + p) * stride + (size_t)chunk * KC + c * 8, stage + q * 1024);
+        dma16_ordered(planes + ((size_t)src[tr] * 2 + p) * stride + (size_t)chunk * KC + c * 8, stage + q * 1024);
     }
     if (sums && wave * 32 < nrows) {
         const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
-        dma16(sum_planes + ((size_t)src[tr] * 2 + p) * sum_stride + (size_t)chunk * 8, sums + wave * 1024);
+        dma16_ordered(sum_planes + ((size_t)src[tr] * 2 + p) * sum_stride + (size_t)chunk * 8, sums + wave * 1024);
     }
 }
 
@@ -412,11 +416,13 @@ QG_DEV qg_half8 stage_frag(const uint8_t *st, int r, int p, int c) {
     return ld_frag((const _Float16 *)(st + (r * 2 + p) * 512 + 16 * (c ^ (r & 15))));
 }
 
-// Q4_K operands of one superblock for the wave's 4 column tiles.
-struct Q4Ops { uint4 hd[4], c0[4], c1[4]; };
+// Q4_K operands of one superblock for the wave's column tiles: 3 loads per
+// tile (header, qs chunks kq and kq + 4).
+constexpr int Q4_LOADS = 3 * NCT;
+struct Q4Ops { uint4 hd[NCT], c0[NCT], c1[NCT]; };
 QG_DEV void q4_load(Q4Ops &o, const uint8_t *const *wrow, int sb, int kq) {
 #pragma unroll
-    for (int n = 0; n < 4; n++) {
+    for (int n = 0; n < NCT; n++) {
         const uint8_t *p = wrow[n] + (size_t)sb * 144;
         o.hd[n] = qg_ld16(p);
         o.c0[n] = qg_ld16(p + 16 + 16 * kq);
@@ -425,127 +431,106 @@ QG_DEV void q4_load(Q4Ops &o, const uint8_t *const *wrow, int sb, int kq) {
 }
 
 // y[m][n] += d * (s*q . x) - dmin * (m . X) over one Q4_K superblock, for the
-// first M row tiles.  The A fragments of K step f+1 are read from shared
-// memory while step f's products run (one wave per SIMD: nothing else would
-// hide the shared-memory latency).
-template <int M>
-QG_DEV void q4_chunk(qg_f4 (&y)[4][4], const Q4Ops &o, const uint8_t *st, const uint8_t *ss, int j, int kq) {
-    Q4kHeader h[4];
+// first M row tiles (A fragments read from shared memory per K step; the
+// other wave on the SIMD hides their latency).
+QG_DEV void q4_chunk(qg_f4 (&y)[4][NCT], const Q4Ops &o, const uint8_t *st, const uint8_t *ss, int j, int kq, int M) {
+    Q4kHeader h[NCT];
 #pragma unroll
-    for (int n = 0; n < 4; n++) h[n] = q4k_header(o.hd[n]);
-    qg_f4 acc[M][4];
+    for (int n = 0; n < NCT; n++) h[n] = q4k_header(o.hd[n]);
+    qg_f4 acc[4][NCT];
 #pragma unroll
-    for (int m = 0; m < M; m++)
+    for (int m = 0; m < 4; m++)
 #pragma unroll
-        for (int n = 0; n < 4; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int n = 0; n < NCT; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int gA = 2 * (kq >> 1);
-    qg_half8 a[2][M][2];
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        a[0][m][0] = stage_frag(st, m * 16 + j, 0, kq);
-        a[0][m][1] = stage_frag(st, m * 16 + j, 1, kq);
-    }
 #pragma unroll
     for (int f = 0; f < 8; f++) {
-        const int cur = f & 1;
-        if (f + 1 < 8) {
+        qg_half8 b[NCT];
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                a[cur ^ 1][m][0] = stage_frag(st, m * 16 + j, 0, 4 * (f + 1) + kq);
-                a[cur ^ 1][m][1] = stage_frag(st, m * 16 + j, 1, 4 * (f + 1) + kq);
-            }
-        }
-        qg_half8 b[4];
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
+        for (int n = 0; n < NCT; n++) {
             const uint4 c = f < 4 ? o.c0[n] : o.c1[n];
             const int g = (f < 4 ? gA : gA + 4) + ((f & 3) >> 1);
             b[n] = q4k_chunk_frag(c, f & 3, (_Float16)q4k_s(h[n], g));
         }
-        // plane-major: the two products into one accumulator are 4*M apart
 #pragma unroll
-        for (int p = 0; p < 2; p++)
+        for (int m = 0; m < 4; m++) {
+            if (m < M) {  // uniform
+                const qg_half8 a0 = stage_frag(st, m * 16 + j, 0, 4 * f + kq), a1 = stage_frag(st, m * 16 + j, 1, 4 * f + kq);
 #pragma unroll
-            for (int n = 0; n < 4; n++)
-#pragma unroll
-                for (int m = 0; m < M; m++)
-                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][p], b[n], acc[m][n], 0, 0, 0);
+                for (int n = 0; n < NCT; n++) {
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[n], acc[m][n], 0, 0, 0);
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[n], acc[m][n], 0, 0, 0);
+                }
+            }
+        }
     }
     // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
-    qg_half8 as[M];
     const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int m = 0; m < M; m++) as[m] = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
-#pragma unroll
-    for (int n = 0; n < 4; n++) {
+    for (int n = 0; n < NCT; n++) {
         qg_half8 bm;
 #pragma unroll
         for (int g = 0; g < 8; g++) bm[g] = kq < 2 ? (_Float16)q4k_m(h[n], g) : (_Float16)0.0f;
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as[m], bm, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        for (int m = 0; m < 4; m++) {
+            if (m < M) {
+                const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
+                const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                y[m][n][i] = __builtin_fmaf(h[n].d, acc[m][n][i], __builtin_fmaf(-h[n].dmin, mm[i], y[m][n][i]));
+                for (int i = 0; i < 4; i++)
+                    y[m][n][i] = __builtin_fmaf(h[n].d, acc[m][n][i], __builtin_fmaf(-h[n].dmin, mm[i], y[m][n][i]));
+            }
         }
     }
 }
 
-// IQ4_NL operands of one K chunk (up to 8 blocks) for the wave's 4 column tiles.
-struct IqOps { uint32_t q[4][8], d[4][8]; };
+// IQ4_NL operands of one K chunk (8 blocks) for the wave's column tiles: the
+// block scale and the lane's 4 qs bytes per block and tile (the blocks are 18
+// bytes, 2-byte aligned).
+// Blocks past the chunk's nb load block 0 again, so every chunk issues the
+// same number of loads.
+// Vector-memory instructions of one iq_load, counted low: the compiler may
+// fuse a block's two 2-byte qs loads into one 4-byte load, never fewer than
+// one load per block scale and one per qs word (waiting for at most this many
+// outstanding operations is then at least as strict as intended).
+constexpr int IQ_LOADS = 2 * 8 * NCT;
+struct IqOps { uint32_t q[NCT][8], d[NCT][4]; };   // d: the 8 fp16 block scales, two per word
 QG_DEV void iq_load(IqOps &o, const uint8_t *const *wrow, int kc, int nb, int kq) {
 #pragma unroll
-    for (int n = 0; n < 4; n++)
+    for (int n = 0; n < NCT; n++)
 #pragma unroll
-        for (int b = 0; b < 8; b++)
-            if (b < nb) {
-                const uint16_t *p16 = (const uint16_t *)(wrow[n] + (size_t)(kc * 8 + b) * 18);  // 2-byte aligned
-                o.d[n][b] = p16[0];
-                o.q[n][b] = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
-            }
+        for (int b = 0; b < 8; b++) {
+            const uint16_t *p16 = (const uint16_t *)(wrow[n] + (size_t)(kc * 8 + (b < nb ? b : 0)) * 18);
+            const uint32_t d = p16[0];
+            if (b & 1) o.d[n][b >> 1] |= d << 16;
+            else o.d[n][b >> 1] = d;
+            o.q[n][b] = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
+        }
 }
 
-// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk, with the A
-// fragments of block b+1 read while block b's products run.
-template <int M>
-QG_DEV void iq_chunk(qg_f4 (&y)[4][4], const IqOps &o, const uint8_t *st, int j, int kq, int nb) {
-    qg_half8 a[2][M][2];
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        a[0][m][0] = stage_frag(st, m * 16 + j, 0, kq);
-        a[0][m][1] = stage_frag(st, m * 16 + j, 1, kq);
-    }
+// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk.
+QG_DEV void iq_chunk(qg_f4 (&y)[4][NCT], const IqOps &o, const uint8_t *st, int j, int kq, int nb, int M) {
 #pragma unroll
     for (int b = 0; b < 8; b++) {
         if (b >= nb) break;  // uniform
-        const int cur = b & 1;
-        if (b + 1 < nb) {
+        qg_half8 bf[NCT];
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                a[cur ^ 1][m][0] = stage_frag(st, m * 16 + j, 0, 4 * (b + 1) + kq);
-                a[cur ^ 1][m][1] = stage_frag(st, m * 16 + j, 1, 4 * (b + 1) + kq);
+        for (int n = 0; n < NCT; n++) bf[n] = iq4_frag4(o.q[n][b]);
+        float d[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++) d[n] = qg_half_u16((o.d[n][b >> 1] >> (16 * (b & 1))) & 0xffffu);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m < M) {  // uniform
+                const qg_half8 a0 = stage_frag(st, m * 16 + j, 0, 4 * b + kq), a1 = stage_frag(st, m * 16 + j, 1, 4 * b + kq);
+#pragma unroll
+                for (int n = 0; n < NCT; n++) {
+                    qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[n], acc, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
+                }
             }
-        }
-        qg_half8 bf[4];
-#pragma unroll
-        for (int n = 0; n < 4; n++) bf[n] = iq4_frag4(o.q[n][b]);
-        qg_f4 acc[M][4];
-#pragma unroll
-        for (int n = 0; n < 4; n++)
-#pragma unroll
-            for (int m = 0; m < M; m++)
-                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][0], bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-        for (int n = 0; n < 4; n++)
-#pragma unroll
-            for (int m = 0; m < M; m++) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][m][1], bf[n], acc[m][n], 0, 0, 0);
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
-            const float d = qg_half_u16(o.d[n][b]);
-#pragma unroll
-            for (int m = 0; m < M; m++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d, acc[m][n][i], y[m][n][i]);
         }
     }
 }
@@ -560,6 +545,7 @@ QG_DEV ItemRange xcd_items(int total) {
     const int C = (total + 7) >> 3;
     return ItemRange{x * C + slot, min(total, (x + 1) * C), n_x};
 }
+QG_DEV int range_count(const ItemRange &r) { return r.next < r.end ? (r.end - r.next + r.step - 1) / r.step : 0; }
 
 // Tile -> order position (block-uniform): the largest p with tb[p] <= tile_idx
 // (empty groups share their successor's start).
@@ -573,6 +559,43 @@ QG_DEV int find_group(const int *tb, int tile_idx) {
     return lo;
 }
 
+// The GEMM workgroups stream (item, K chunk) steps: while step s computes,
+// the activation stage of step s + 1 and the weights of step s + 2 are in
+// flight.  Only the newest weight loads (those of step s + 2) may be
+// outstanding when step s + 1 starts: loads complete in issue order, so
+// waiting for at most that many outstanding operations leaves every older
+// load done, whatever the epilogue's stores (issued in between) do.
+// An item's group, rows and block, from the workgroup's shared-memory copies
+// of the tile table and the CSR offsets (no global loads in the stream).
+struct PfItem { int g, tile, n_g, r0, nv, M, blk, off; bool shared; };
+QG_DEV PfItem pf_item(const int *s_tb, const int *s_go, const int *s_off, int nt, int t_lo, int nblk, int item) {
+    PfItem it;
+    const int tile_idx = t_lo + item / nblk;
+    it.blk = item % nblk;
+    const int gp = find_group(s_tb, tile_idx);
+    it.g = s_go[gp];
+    it.tile = tile_idx - s_tb[gp];
+    it.shared = it.g == QG_EXPERTS;
+    it.off = it.shared ? 0 : s_off[it.g];
+    it.n_g = it.shared ? nt : s_off[it.g + 1] - it.off;
+    it.r0 = it.tile * PT;
+    it.nv = min(PT, it.n_g - it.r0);
+    it.M = (it.nv + 15) >> 4;
+    return it;
+}
+
+// Tile row r (< 64, past the item's rows: its last row) of a routed item as
+// per-row indices into shared memory by a 4-byte direct copy per lane of
+// wave 0 (tracked like the stage copies); shared-expert rows are computed.
+// `list` is the CSR array to index (row_token or row_slot), `shared_base`
+// the index of shared row 0.
+QG_DEV void item_rows(int *dst, const PfItem &it, const int *list, int shared_base, int wave, int lane) {
+    if (wave != 0) return;
+    const int r = it.r0 + min(lane, it.nv - 1);
+    if (it.shared) dst[lane] = shared_base + r;
+    else dma4_ordered(list + it.off + r, dst);
+}
+
 // ---------------- P5: gate/up + SwiGLU ----------------
 struct GuArgs {
     int nt, D, F;
@@ -584,101 +607,138 @@ struct GuArgs {
     int down_fmt, sh_down_fmt;
 };
 
-__global__ __launch_bounds__(256, 1) void pf_gateup_kernel(GuArgs A) {
+// Item = (group, 64-row tile, 128 F rows); wave w: F rows f0 = 16 w .. +15 of
+// the block, column tile 0 their gate rows, tile 1 their up rows.  Steps are
+// the item's D/256 superblocks.
+__global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
-    __shared__ int s_tb[NG + 1], s_go[NG];
-    __shared__ int s_src[PT], s_mrow[PT];
+    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int s_src[2][PT];
+    __shared__ float s_gs[PF_WAVES][PT];     // 16-row partial sums of the 32-row groups (Q4_K down format)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    for (int i = tid; i <= NG; i += 256) {
+    for (int i = tid; i <= NG; i += 512) {
         s_tb[i] = A.tt->tbase[i];
         if (i < NG) s_go[i] = A.tt->gorder[i];
+        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
     }
-    __syncthreads();
     const int nfb = A.F / GU_FB, NSB = A.D / 256, D32 = A.D / 32, F = A.F;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
     const ItemRange ir = xcd_items(total);
-    for (int item = ir.next; item < ir.end; item += ir.step) {
-        const int tile_idx = t_lo + item / nfb, fb = item % nfb;
-        const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
-        const bool shared = g == QG_EXPERTS;
-        const int n_g = shared ? A.nt : A.offsets[g + 1] - A.offsets[g];
-        const int r0 = tile * PT, nv = min(PT, n_g - r0), M = (nv + 15) >> 4;
-        if (tid < PT) {
-            const int r = r0 + min(tid, nv - 1);
-            s_src[tid] = shared ? r : A.row_token[A.offsets[g] + r];
-            s_mrow[tid] = shared ? A.nt * QG_TOP + r : A.offsets[g] + r;
-        }
+    const int nitems = range_count(ir), steps = nitems * NSB;
+    __syncthreads();
+    if (steps == 0) return;  // block-uniform
+    auto item_of = [&](int k) { return pf_item(s_tb, s_go, s_off, A.nt, t_lo, nfb, ir.next + k * ir.step); };
+    // mid row of tile row tr (< nv): the CSR position, shared rows after the 10 nt selections
+    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.r0 + tr : it.off + it.r0 + tr; };
+    auto weight_rows = [&](const PfItem &it, const uint8_t **wrow) {
+        const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
+        const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
+        const int f = it.blk * GU_FB + wave * 16 + j;
+        wrow[0] = bg + (size_t)f * A.rb;
+        wrow[1] = bu + (size_t)f * A.rb;
+    };
+    auto stage = [&](const PfItem &it, int buf, int sb, int b) {
+        stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src[buf], sb, 32,
+                   16 * it.M, wave, lane);
+    };
+    // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
+    PfItem cur = item_of(0);
+    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
+    wait_vmem();
+    __syncthreads();
+    stage(cur, 0, 0, 0);
+    const uint8_t *wrow[NCT];
+    auto load_step = [&](Q4Ops &o, int s2) {
+        const PfItem it = item_of(s2 / NSB);
+        weight_rows(it, wrow);
+        q4_load(o, wrow, s2 % NSB, kq);
+    };
+    // weights of step s live in w[s % 3]: loaded two steps ahead, never copied
+    // between registers (a copy would wait for the loads in flight)
+    Q4Ops w0, w1, w2;
+    load_step(w0, 0);
+    if (1 < steps) load_step(w1, 1);
+    qg_f4 y[4][NCT];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](int s, const Q4Ops &wc, Q4Ops &wn) {
+        const int k = s / NSB, sb = s % NSB;
+        if (s + 1 < steps) wait_vmem_but<Q4_LOADS>();
+        else wait_vmem();
         __syncthreads();
-        const int f0 = fb * GU_FB + wave * 32;
-        const uint8_t *bg = shared ? A.sh_gate : A.gate + (size_t)g * F * A.rb;
-        const uint8_t *bu = shared ? A.sh_up : A.up + (size_t)g * F * A.rb;
-        const uint8_t *wrow[4];
-#pragma unroll
-        for (int n = 0; n < 4; n++) wrow[n] = (n < 2 ? bg : bu) + (size_t)(f0 + 16 * (n & 1) + j) * A.rb;
-        stage_rows(lds, lds + 2 * STAGE_BYTES, A.xp, A.D, A.xsp, D32, s_src, 0, 32, 16 * M, wave, lane);
-        Q4Ops cur, nxt;
-        q4_load(cur, wrow, 0, kq);
-        qg_f4 y[4][4];
-#pragma unroll
-        for (int m = 0; m < 4; m++)
-#pragma unroll
-            for (int n = 0; n < 4; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int sb = 0; sb < NSB; sb++) {
-            wait_vmem();
-            __syncthreads();
-            if (sb + 1 < NSB) {
-                const int b = (sb + 1) & 1;
-                stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src, sb + 1, 32,
-                           16 * M, wave, lane);
-                q4_load(nxt, wrow, sb + 1, kq);
-            }
-            const uint8_t *st = lds + (sb & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (sb & 1) * SUMS_BYTES;
-            switch (M) {
-            case 1: q4_chunk<1>(y, cur, st, ss, j, kq); break;
-            case 2: q4_chunk<2>(y, cur, st, ss, j, kq); break;
-            case 3: q4_chunk<3>(y, cur, st, ss, j, kq); break;
-            default: q4_chunk<4>(y, cur, st, ss, j, kq); break;
-            }
-            cur = nxt;
-        }
-        // SwiGLU: column tiles 0/1 are gate rows f0+j / f0+16+j, tiles 2/3 the same up rows
-        const int fmt = shared ? A.sh_down_fmt : A.down_fmt;
-        const int pa = plane_pos(fmt, f0 + j), pb = plane_pos(fmt, f0 + 16 + j);
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            if (m >= M) break;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tr = m * 16 + 4 * kq + i;
-                const float ma = qg_swiglu(y[m][0][i], y[m][2][i]), mb = qg_swiglu(y[m][1][i], y[m][3][i]);
-                const bool ok = tr < nv;
-                const size_t mrow = (size_t)s_mrow[ok ? tr : 0];
-                if (ok) {
-                    _Float16 *hp = A.midp + mrow * 2 * F;
-                    const _Float16 ha = (_Float16)ma, hb = (_Float16)mb;
-                    hp[pa] = ha;
-                    hp[F + pa] = (_Float16)(ma - (float)ha);
-                    hp[pb] = hb;
-                    hp[F + pb] = (_Float16)(mb - (float)hb);
+        // the next item's rows, copied while this item streams (its buffer
+        // held item k - 1's rows, staged long ago)
+        if (sb == 0 && k + 1 < nitems) item_rows(s_src[(k + 1) & 1], item_of(k + 1), A.row_token, 0, wave, lane);
+        // the next step's stage
+        if (s + 1 < steps) {
+            const int k1 = (s + 1) / NSB, sb1 = (s + 1) % NSB;
+            if (k1 != k) {
+                if (NSB == 1) {  // the rows were copied just above
+                    wait_vmem();
+                    __syncthreads();
                 }
-                if (fmt == QT_Q4_K) {
-                    // the 32-group sum of these F rows (lanes of one kq hold all 16 j)
-                    float s = ma + mb;
-                    s += __shfl_xor(s, 1);
-                    s += __shfl_xor(s, 2);
-                    s += __shfl_xor(s, 4);
-                    s += __shfl_xor(s, 8);
-                    if (ok && j == 0) {
-                        _Float16 *sp = A.msp + mrow * 2 * (F / 32) + f0 / 32;
-                        const _Float16 hs = (_Float16)s;
-                        sp[0] = hs;
-                        sp[F / 32] = (_Float16)(s - (float)hs);
+                stage(item_of(k1), k1 & 1, sb1, (s + 1) & 1);
+            } else {
+                stage(cur, k & 1, sb1, (s + 1) & 1);
+            }
+        }
+        if (s + 2 < steps) load_step(wn, s + 2);  // the weights two steps ahead
+        const uint8_t *st = lds + (s & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
+        q4_chunk(y, wc, st, ss, j, kq, cur.M);
+        if (sb == NSB - 1) {
+            // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
+            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt;
+            const int f = cur.blk * GU_FB + wave * 16 + j, pa = plane_pos(fmt, f);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                if (m >= cur.M) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tr = m * 16 + 4 * kq + i;
+                    const float ma = qg_swiglu_fast(y[m][0][i], y[m][1][i]);
+                    const bool ok = tr < cur.nv;
+                    if (ok) {
+                        _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
+                        const _Float16 ha = (_Float16)ma;
+                        hp[pa] = ha;
+                        hp[F + pa] = (_Float16)(ma - (float)ha);
+                    }
+                    if (fmt == QT_Q4_K) {
+                        // this wave's 16 rows of the 32-row group (lanes of one kq hold all 16 j)
+                        float sp = ma;
+                        sp += __shfl_xor(sp, 1);
+                        sp += __shfl_xor(sp, 2);
+                        sp += __shfl_xor(sp, 4);
+                        sp += __shfl_xor(sp, 8);
+                        if (j == 0) s_gs[wave][tr] = sp;
                     }
                 }
             }
+            if (fmt == QT_Q4_K) {  // block-uniform
+                __syncthreads();
+                // waves 2i and 2i+1 hold the two halves of 32-row group i of the block
+                if ((wave & 1) == 0 && lane < cur.nv) {
+                    const float sum = s_gs[wave][lane] + s_gs[wave + 1][lane];
+                    _Float16 *sp = A.msp + (size_t)mrow(cur, lane) * 2 * (F / 32) + (cur.blk * GU_FB + wave * 16) / 32;
+                    const _Float16 hs = (_Float16)sum;
+                    sp[0] = hs;
+                    sp[F / 32] = (_Float16)(sum - (float)hs);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s + 1 < steps) cur = item_of(k + 1);
         }
-        __syncthreads();  // s_src / s_mrow and the stage buffers are rewritten by the next item
+    };
+    for (int s = 0; s < steps; s += 3) {
+        step(s, w0, w2);
+        if (s + 1 < steps) step(s + 1, w1, w0);
+        if (s + 2 < steps) step(s + 2, w2, w1);
     }
 }
 
@@ -692,104 +752,127 @@ struct DnArgs {
     float *slots;                    // [rows][D]: slot t*10+k, shared rows at nt*10+t
 };
 
+// Item = (group, 64-row tile, 256 D rows); wave w: D rows 32 w .. +31 of the
+// block as two column tiles.  Steps are the item's K chunks of 256 (F / 256
+// superblocks for Q4_K, 8 blocks per chunk for IQ4_NL).
 template <int FMT>
-__global__ __launch_bounds__(256, 1) void pf_down_kernel(DnArgs A) {
+__global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
-    __shared__ int s_tb[NG + 1], s_go[NG];
-    __shared__ int s_src[PT], s_slot[PT];
+    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int s_src[2][PT], s_slot[2][PT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    for (int i = tid; i <= NG; i += 256) {
+    for (int i = tid; i <= NG; i += 512) {
         s_tb[i] = A.tt->tbase[i];
         if (i < NG) s_go[i] = A.tt->gorder[i];
+        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
     }
-    __syncthreads();
     const int ndb = A.D / DN_DB, F = A.F, F32 = A.F / 32, nkc = (F + KC - 1) / KC;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
     const ItemRange ir = xcd_items(total);
-    for (int item = ir.next; item < ir.end; item += ir.step) {
-        const int tile_idx = t_lo + item / ndb, db = item % ndb;
-        const int gp = find_group(s_tb, tile_idx), g = s_go[gp], tile = tile_idx - s_tb[gp];
-        const bool shared = g == QG_EXPERTS;
-        const int n_g = shared ? A.nt : A.offsets[g + 1] - A.offsets[g];
-        const int r0 = tile * PT, nv = min(PT, n_g - r0), M = (nv + 15) >> 4;
-        if (tid < PT) {
-            const int r = r0 + min(tid, nv - 1);
-            s_src[tid] = shared ? A.nt * QG_TOP + r : A.offsets[g] + r;
-            s_slot[tid] = shared ? A.nt * QG_TOP + r : A.row_slot[A.offsets[g] + r];
-        }
+    const int nitems = range_count(ir), steps = nitems * nkc;
+    __syncthreads();
+    if (steps == 0) return;  // block-uniform
+    auto item_of = [&](int k) { return pf_item(s_tb, s_go, s_off, A.nt, t_lo, ndb, ir.next + k * ir.step); };
+    // the item's mid rows (computed) and output slots (copied from row_slot)
+    auto set_rows = [&](const PfItem &it, int buf) {
+        if (wave == 0) s_src[buf][lane] = it.shared ? A.nt * QG_TOP + it.r0 + min(lane, it.nv - 1) : it.off + it.r0 + min(lane, it.nv - 1);
+        item_rows(s_slot[buf], it, A.row_slot, A.nt * QG_TOP, wave, lane);
+    };
+    auto weight_rows = [&](const PfItem &it, const uint8_t **wrow) {
+        const uint8_t *bw = it.shared ? A.sh_down : A.down + (size_t)it.g * A.D * A.rb;
+        const size_t rb = it.shared ? A.sh_rb : A.rb;
+        const int d = it.blk * DN_DB + wave * 32 + j;
+#pragma unroll
+        for (int n = 0; n < NCT; n++) wrow[n] = bw + (size_t)(d + 16 * n) * rb;
+    };
+    auto nblocks = [&](int kc) { return min(8, (F - kc * KC) / 32); };
+    auto stage = [&](const PfItem &it, int buf, int kc, int b) {
+        if (FMT == QT_Q4_K)
+            stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src[buf], kc, 32,
+                       16 * it.M, wave, lane);
+        else
+            stage_rows(lds + b * STAGE_BYTES, nullptr, A.midp, F, nullptr, 0, s_src[buf], kc, 4 * nblocks(kc), 16 * it.M, wave,
+                       lane);
+    };
+    using Ops = typename std::conditional<FMT == QT_Q4_K, Q4Ops, IqOps>::type;
+    auto load = [&](Ops &o, const uint8_t *const *wrow, int kc) {
+        if constexpr (FMT == QT_Q4_K) q4_load(o, wrow, kc, kq);
+        else iq_load(o, wrow, kc, nblocks(kc), kq);
+    };
+    PfItem cur = item_of(0);
+    set_rows(cur, 0);
+    wait_vmem();
+    __syncthreads();
+    stage(cur, 0, 0, 0);
+    const uint8_t *wrow[NCT];
+    auto load_step = [&](Ops &o, int s2) {
+        const PfItem it = item_of(s2 / nkc);
+        weight_rows(it, wrow);
+        load(o, wrow, s2 % nkc);
+    };
+    Ops w0, w1, w2;   // weights of step s in w[s % 3], loaded two steps ahead, never copied
+    load_step(w0, 0);
+    if (1 < steps) load_step(w1, 1);
+    qg_f4 y[4][NCT];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](int s, const Ops &wc, Ops &wn) {
+        const int k = s / nkc, kc = s % nkc;
+        if (s + 1 < steps) wait_vmem_but<FMT == QT_Q4_K ? Q4_LOADS : IQ_LOADS>();
+        else wait_vmem();
         __syncthreads();
-        const int d0 = db * DN_DB + wave * 64;
-        const uint8_t *bw = shared ? A.sh_down : A.down + (size_t)g * A.D * A.rb;
-        const size_t rb = shared ? A.sh_rb : A.rb;
-        const uint8_t *wrow[4];
-#pragma unroll
-        for (int n = 0; n < 4; n++) wrow[n] = bw + (size_t)(d0 + 16 * n + j) * rb;
-        qg_f4 y[4][4];
-#pragma unroll
-        for (int m = 0; m < 4; m++)
-#pragma unroll
-            for (int n = 0; n < 4; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (FMT == QT_Q4_K) {
-            stage_rows(lds, lds + 2 * STAGE_BYTES, A.midp, F, A.msp, F32, s_src, 0, 32, 16 * M, wave, lane);
-            Q4Ops cur, nxt;
-            q4_load(cur, wrow, 0, kq);
-            for (int kc = 0; kc < nkc; kc++) {
-                wait_vmem();
-                __syncthreads();
-                if (kc + 1 < nkc) {
-                    const int b = (kc + 1) & 1;
-                    stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src, kc + 1,
-                               32, 16 * M, wave, lane);
-                    q4_load(nxt, wrow, kc + 1, kq);
+        // the next item's rows, copied while this item streams
+        if (kc == 0 && k + 1 < nitems) set_rows(item_of(k + 1), (k + 1) & 1);
+        if (s + 1 < steps) {
+            const int k1 = (s + 1) / nkc, kc1 = (s + 1) % nkc;
+            if (k1 != k) {
+                if (nkc == 1) {  // the rows were copied just above
+                    wait_vmem();
+                    __syncthreads();
                 }
-                const uint8_t *st = lds + (kc & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (kc & 1) * SUMS_BYTES;
-                switch (M) {
-                case 1: q4_chunk<1>(y, cur, st, ss, j, kq); break;
-                case 2: q4_chunk<2>(y, cur, st, ss, j, kq); break;
-                case 3: q4_chunk<3>(y, cur, st, ss, j, kq); break;
-                default: q4_chunk<4>(y, cur, st, ss, j, kq); break;
-                }
-                cur = nxt;
+                stage(item_of(k1), k1 & 1, kc1, (s + 1) & 1);
+            } else {
+                stage(cur, k & 1, kc1, (s + 1) & 1);
             }
+        }
+        if (s + 2 < steps) load_step(wn, s + 2);
+        const uint8_t *st = lds + (s & 1) * STAGE_BYTES;
+        if constexpr (FMT == QT_Q4_K) {
+            const uint8_t *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
+            q4_chunk(y, wc, st, ss, j, kq, cur.M);
         } else {
-            auto nblocks = [&](int kc) { return min(8, (F - kc * KC) / 32); };
-            stage_rows(lds, nullptr, A.midp, F, nullptr, 0, s_src, 0, 4 * nblocks(0), 16 * M, wave, lane);
-            IqOps cur, nxt;
-            iq_load(cur, wrow, 0, nblocks(0), kq);
-            for (int kc = 0; kc < nkc; kc++) {
-                wait_vmem();
-                __syncthreads();
-                if (kc + 1 < nkc) {
-                    stage_rows(lds + ((kc + 1) & 1) * STAGE_BYTES, nullptr, A.midp, F, nullptr, 0, s_src, kc + 1, 4 * nblocks(kc + 1),
-                               16 * M, wave, lane);
-                    iq_load(nxt, wrow, kc + 1, nblocks(kc + 1), kq);
-                }
-                const uint8_t *st = lds + (kc & 1) * STAGE_BYTES;
-                const int nb = nblocks(kc);
-                switch (M) {
-                case 1: iq_chunk<1>(y, cur, st, j, kq, nb); break;
-                case 2: iq_chunk<2>(y, cur, st, j, kq, nb); break;
-                case 3: iq_chunk<3>(y, cur, st, j, kq, nb); break;
-                default: iq_chunk<4>(y, cur, st, j, kq, nb); break;
-                }
-                cur = nxt;
-            }
+            const int nb = nblocks(kc);
+            iq_chunk(y, wc, st, j, kq, nb, cur.M);
         }
+        if (kc == nkc - 1) {
+            const int d0 = cur.blk * DN_DB + wave * 32;
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            if (m >= M) break;
+            for (int m = 0; m < 4; m++) {
+                if (m >= cur.M) break;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tr = m * 16 + 4 * kq + i;
-                if (tr < nv) {
-                    float *o = A.slots + (size_t)s_slot[tr] * A.D + d0 + j;
+                for (int i = 0; i < 4; i++) {
+                    const int tr = m * 16 + 4 * kq + i;
+                    if (tr < cur.nv) {
+                        float *o = A.slots + (size_t)s_slot[k & 1][tr] * A.D + d0 + j;
 #pragma unroll
-                    for (int n = 0; n < 4; n++) o[16 * n] = y[m][n][i];
+                        for (int n = 0; n < NCT; n++) o[16 * n] = y[m][n][i];
+                    }
                 }
             }
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s + 1 < steps) cur = item_of(k + 1);
         }
-        __syncthreads();
+    };
+    for (int s = 0; s < steps; s += 3) {
+        step(s, w0, w2);
+        if (s + 1 < steps) step(s + 1, w1, w0);
+        if (s + 2 < steps) step(s + 2, w2, w1);
     }
 }
 
@@ -939,14 +1022,14 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
         GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
                  xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type};
-        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(256), PF_LDS, s, G);
+        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(512), PF_LDS, s, G);
         if ((rc = hipGetLastError())) return rc;
     }
     auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
         DnArgs DA{nt, D, F, offsets, tt, seg_lo, seg_hi, row_slot, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr,
                   qg_row_bytes_host(L->down_type, F), sh ? qg_row_bytes_host(L->sh_down_type, F) : 0, midp, msp, slots};
-        if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel<QT_Q4_K>, dim3(grid), dim3(256), PF_LDS, s, DA);
-        else pf_launch(slot, pf_down_kernel<QT_IQ4_NL>, dim3(grid), dim3(256), PF_LDS, s, DA);
+        if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel<QT_Q4_K>, dim3(grid), dim3(512), PF_LDS, s, DA);
+        else pf_launch(slot, pf_down_kernel<QT_IQ4_NL>, dim3(grid), dim3(512), PF_LDS, s, DA);
         return hipGetLastError();
     };
     if ((rc = down(0, 1, L->down_type, 6))) return rc;
