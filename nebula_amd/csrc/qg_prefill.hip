@@ -565,24 +565,44 @@ QG_DEV int find_group(const int *tb, int tile_idx) {
 // outstanding when step s + 1 starts: loads complete in issue order, so
 // waiting for at most that many outstanding operations leaves every older
 // load done, whatever the epilogue's stores (issued in between) do.
-// An item's group, rows and block, from the workgroup's shared-memory copies
-// of the tile table and the CSR offsets (no global loads in the stream).
-struct PfItem { int g, tile, n_g, r0, nv, M, blk, off; bool shared; };
-QG_DEV PfItem pf_item(const int *s_tb, const int *s_go, const int *s_off, int nt, int t_lo, int nblk, int item) {
-    PfItem it;
-    const int tile_idx = t_lo + item / nblk;
-    it.blk = item % nblk;
+//
+// An item of a workgroup's range: group g (QG_EXPERTS: the shared expert),
+// block blk of its output rows, nv valid rows (1..64) from `base` (the CSR
+// position of the tile's first row; the shared expert: its first token).
+struct PfItem { int g, blk, nv, M, base; bool shared; };
+QG_DEV int2 pf_item_packed(const int *s_tb, const int *s_go, const int *s_off, int nt, int t_lo, int nblk, int item) {
+    const int tile_idx = t_lo + item / nblk, blk = item % nblk;
     const int gp = find_group(s_tb, tile_idx);
-    it.g = s_go[gp];
-    it.tile = tile_idx - s_tb[gp];
-    it.shared = it.g == QG_EXPERTS;
-    it.off = it.shared ? 0 : s_off[it.g];
-    it.n_g = it.shared ? nt : s_off[it.g + 1] - it.off;
-    it.r0 = it.tile * PT;
-    it.nv = min(PT, it.n_g - it.r0);
+    const int g = s_go[gp], r0 = (tile_idx - s_tb[gp]) * PT;
+    const bool shared = g == QG_EXPERTS;
+    const int off = shared ? 0 : s_off[g], n_g = shared ? nt : s_off[g + 1] - off;
+    return make_int2(g | blk << 10 | min(PT, n_g - r0) << 17, off + r0);
+}
+QG_DEV PfItem pf_unpack(int2 v) {
+    PfItem it;
+    it.g = v.x & 1023;
+    it.blk = (v.x >> 10) & 127;
+    it.nv = v.x >> 17;
     it.M = (it.nv + 15) >> 4;
+    it.base = v.y;
+    it.shared = it.g == QG_EXPERTS;
     return it;
 }
+
+// The workgroup's items, decoded ahead into a ring in shared memory (the
+// search over the tile table stays out of the step stream): items k .. k+63
+// are written by threads 0..63 when item k - 64 starts (k a multiple of 64),
+// into the slots of items k - 128 .. k - 65, all finished by then; the next
+// reader of the new slots is two steps or more (and a barrier) away.
+constexpr int IT_RING = 128, IT_BATCH = 64;
+struct ItemRing {
+    int2 *ring; const int *tb, *go, *off; int nt, t_lo, nblk, nitems; ItemRange ir;
+    __device__ __forceinline__ void fill(int k0, int n, int tid) const {
+        const int k = k0 + tid;
+        if (tid < n && k < nitems) ring[k & (IT_RING - 1)] = pf_item_packed(tb, go, off, nt, t_lo, nblk, ir.next + k * ir.step);
+    }
+    __device__ __forceinline__ PfItem at(int k) const { return pf_unpack(ring[k & (IT_RING - 1)]); }
+};
 
 // Tile row r (< 64, past the item's rows: its last row) of a routed item as
 // per-row indices into shared memory by a 4-byte direct copy per lane of
@@ -591,10 +611,14 @@ QG_DEV PfItem pf_item(const int *s_tb, const int *s_go, const int *s_off, int nt
 // the index of shared row 0.
 QG_DEV void item_rows(int *dst, const PfItem &it, const int *list, int shared_base, int wave, int lane) {
     if (wave != 0) return;
-    const int r = it.r0 + min(lane, it.nv - 1);
+    const int r = it.base + min(lane, it.nv - 1);
     if (it.shared) dst[lane] = shared_base + r;
-    else dma4_ordered(list + it.off + r, dst);
+    else dma4_ordered(list + r, dst);
 }
+
+// Position (item k, chunk c) of a step, advanced without division.
+struct StepPos { int k, c; };
+QG_DEV StepPos next_pos(StepPos p, int nc) { return ++p.c == nc ? StepPos{p.k + 1, 0} : p; }
 
 // ---------------- P5: gate/up + SwiGLU ----------------
 struct GuArgs {
@@ -614,6 +638,7 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
     __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int2 s_it[IT_RING];
     __shared__ int s_src[2][PT];
     __shared__ float s_gs[PF_WAVES][PT];     // 16-row partial sums of the 32-row groups (Q4_K down format)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
@@ -626,11 +651,13 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
     const ItemRange ir = xcd_items(total);
     const int nitems = range_count(ir), steps = nitems * NSB;
-    __syncthreads();
     if (steps == 0) return;  // block-uniform
-    auto item_of = [&](int k) { return pf_item(s_tb, s_go, s_off, A.nt, t_lo, nfb, ir.next + k * ir.step); };
+    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
+    __syncthreads();
+    R.fill(0, IT_RING, tid);
+    __syncthreads();
     // mid row of tile row tr (< nv): the CSR position, shared rows after the 10 nt selections
-    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.r0 + tr : it.off + it.r0 + tr; };
+    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
     auto weight_rows = [&](const PfItem &it, const uint8_t **wrow) {
         const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
         const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
@@ -642,50 +669,53 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
         stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src[buf], sb, 32,
                    16 * it.M, wave, lane);
     };
+    const uint8_t *wrow[NCT];
+    auto load_step = [&](Q4Ops &o, StepPos p) {
+        weight_rows(R.at(p.k), wrow);
+        q4_load(o, wrow, p.c, kq);
+    };
     // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
-    PfItem cur = item_of(0);
+    PfItem cur = R.at(0);
     item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
     wait_vmem();
     __syncthreads();
     stage(cur, 0, 0, 0);
-    const uint8_t *wrow[NCT];
-    auto load_step = [&](Q4Ops &o, int s2) {
-        const PfItem it = item_of(s2 / NSB);
-        weight_rows(it, wrow);
-        q4_load(o, wrow, s2 % NSB, kq);
-    };
     // weights of step s live in w[s % 3]: loaded two steps ahead, never copied
     // between registers (a copy would wait for the loads in flight)
     Q4Ops w0, w1, w2;
-    load_step(w0, 0);
-    if (1 < steps) load_step(w1, 1);
+    StepPos pos{0, 0};
+    load_step(w0, pos);
+    if (1 < steps) load_step(w1, next_pos(pos, NSB));
     qg_f4 y[4][NCT];
 #pragma unroll
     for (int m = 0; m < 4; m++)
 #pragma unroll
         for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     auto step = [&](int s, const Q4Ops &wc, Q4Ops &wn) {
-        const int k = s / NSB, sb = s % NSB;
+        const int k = pos.k, sb = pos.c;
+        const StepPos p1 = next_pos(pos, NSB), p2 = next_pos(p1, NSB);
         if (s + 1 < steps) wait_vmem_but<Q4_LOADS>();
         else wait_vmem();
         __syncthreads();
-        // the next item's rows, copied while this item streams (its buffer
-        // held item k - 1's rows, staged long ago)
-        if (sb == 0 && k + 1 < nitems) item_rows(s_src[(k + 1) & 1], item_of(k + 1), A.row_token, 0, wave, lane);
+        if (sb == 0) {
+            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+            // the next item's rows, copied while this item streams (its buffer
+            // held item k - 1's rows, staged long ago)
+            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+        }
         // the next step's stage
         if (s + 1 < steps) {
-            const int k1 = (s + 1) / NSB, sb1 = (s + 1) % NSB;
-            if (k1 != k) {
+            if (p1.k != k) {
                 if (NSB == 1) {  // the rows were copied just above
                     wait_vmem();
                     __syncthreads();
                 }
-                stage(item_of(k1), k1 & 1, sb1, (s + 1) & 1);
+                stage(R.at(p1.k), p1.k & 1, p1.c, (s + 1) & 1);
             } else {
-                stage(cur, k & 1, sb1, (s + 1) & 1);
+                stage(cur, k & 1, p1.c, (s + 1) & 1);
             }
         }
-        if (s + 2 < steps) load_step(wn, s + 2);  // the weights two steps ahead
+        if (s + 2 < steps) load_step(wn, p2);  // the weights two steps ahead
         const uint8_t *st = lds + (s & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
         q4_chunk(y, wc, st, ss, j, kq, cur.M);
         if (sb == NSB - 1) {
@@ -732,8 +762,9 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
             for (int m = 0; m < 4; m++)
 #pragma unroll
                 for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = item_of(k + 1);
+            if (s + 1 < steps) cur = R.at(k + 1);
         }
+        pos = p1;
     };
     for (int s = 0; s < steps; s += 3) {
         step(s, w0, w2);
@@ -760,6 +791,7 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
     __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int2 s_it[IT_RING];
     __shared__ int s_src[2][PT], s_slot[2][PT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     for (int i = tid; i <= NG; i += 512) {
@@ -771,12 +803,14 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
     const ItemRange ir = xcd_items(total);
     const int nitems = range_count(ir), steps = nitems * nkc;
-    __syncthreads();
     if (steps == 0) return;  // block-uniform
-    auto item_of = [&](int k) { return pf_item(s_tb, s_go, s_off, A.nt, t_lo, ndb, ir.next + k * ir.step); };
+    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, ndb, nitems, ir};
+    __syncthreads();
+    R.fill(0, IT_RING, tid);
+    __syncthreads();
     // the item's mid rows (computed) and output slots (copied from row_slot)
     auto set_rows = [&](const PfItem &it, int buf) {
-        if (wave == 0) s_src[buf][lane] = it.shared ? A.nt * QG_TOP + it.r0 + min(lane, it.nv - 1) : it.off + it.r0 + min(lane, it.nv - 1);
+        if (wave == 0) s_src[buf][lane] = (it.shared ? A.nt * QG_TOP : 0) + it.base + min(lane, it.nv - 1);
         item_rows(s_slot[buf], it, A.row_slot, A.nt * QG_TOP, wave, lane);
     };
     auto weight_rows = [&](const PfItem &it, const uint8_t **wrow) {
@@ -796,56 +830,55 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
                        lane);
     };
     using Ops = typename std::conditional<FMT == QT_Q4_K, Q4Ops, IqOps>::type;
-    auto load = [&](Ops &o, const uint8_t *const *wrow, int kc) {
-        if constexpr (FMT == QT_Q4_K) q4_load(o, wrow, kc, kq);
-        else iq_load(o, wrow, kc, nblocks(kc), kq);
+    const uint8_t *wrow[NCT];
+    auto load_step = [&](Ops &o, StepPos p) {
+        weight_rows(R.at(p.k), wrow);
+        if constexpr (FMT == QT_Q4_K) q4_load(o, wrow, p.c, kq);
+        else iq_load(o, wrow, p.c, nblocks(p.c), kq);
     };
-    PfItem cur = item_of(0);
+    PfItem cur = R.at(0);
     set_rows(cur, 0);
     wait_vmem();
     __syncthreads();
     stage(cur, 0, 0, 0);
-    const uint8_t *wrow[NCT];
-    auto load_step = [&](Ops &o, int s2) {
-        const PfItem it = item_of(s2 / nkc);
-        weight_rows(it, wrow);
-        load(o, wrow, s2 % nkc);
-    };
     Ops w0, w1, w2;   // weights of step s in w[s % 3], loaded two steps ahead, never copied
-    load_step(w0, 0);
-    if (1 < steps) load_step(w1, 1);
+    StepPos pos{0, 0};
+    load_step(w0, pos);
+    if (1 < steps) load_step(w1, next_pos(pos, nkc));
     qg_f4 y[4][NCT];
 #pragma unroll
     for (int m = 0; m < 4; m++)
 #pragma unroll
         for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     auto step = [&](int s, const Ops &wc, Ops &wn) {
-        const int k = s / nkc, kc = s % nkc;
+        const int k = pos.k, kc = pos.c;
+        const StepPos p1 = next_pos(pos, nkc), p2 = next_pos(p1, nkc);
         if (s + 1 < steps) wait_vmem_but<FMT == QT_Q4_K ? Q4_LOADS : IQ_LOADS>();
         else wait_vmem();
         __syncthreads();
-        // the next item's rows, copied while this item streams
-        if (kc == 0 && k + 1 < nitems) set_rows(item_of(k + 1), (k + 1) & 1);
+        if (kc == 0) {
+            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+            // the next item's rows, copied while this item streams
+            if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
+        }
         if (s + 1 < steps) {
-            const int k1 = (s + 1) / nkc, kc1 = (s + 1) % nkc;
-            if (k1 != k) {
+            if (p1.k != k) {
                 if (nkc == 1) {  // the rows were copied just above
                     wait_vmem();
                     __syncthreads();
                 }
-                stage(item_of(k1), k1 & 1, kc1, (s + 1) & 1);
+                stage(R.at(p1.k), p1.k & 1, p1.c, (s + 1) & 1);
             } else {
-                stage(cur, k & 1, kc1, (s + 1) & 1);
+                stage(cur, k & 1, p1.c, (s + 1) & 1);
             }
         }
-        if (s + 2 < steps) load_step(wn, s + 2);
+        if (s + 2 < steps) load_step(wn, p2);
         const uint8_t *st = lds + (s & 1) * STAGE_BYTES;
         if constexpr (FMT == QT_Q4_K) {
             const uint8_t *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
             q4_chunk(y, wc, st, ss, j, kq, cur.M);
         } else {
-            const int nb = nblocks(kc);
-            iq_chunk(y, wc, st, j, kq, nb, cur.M);
+            iq_chunk(y, wc, st, j, kq, nblocks(kc), cur.M);
         }
         if (kc == nkc - 1) {
             const int d0 = cur.blk * DN_DB + wave * 32;
@@ -866,13 +899,213 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
             for (int m = 0; m < 4; m++)
 #pragma unroll
                 for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = item_of(k + 1);
+            if (s + 1 < steps) cur = R.at(k + 1);
         }
+        pos = p1;
     };
     for (int s = 0; s < steps; s += 3) {
         step(s, w0, w2);
         if (s + 1 < steps) step(s + 1, w1, w0);
         if (s + 2 < steps) step(s + 2, w2, w1);
+    }
+}
+
+// ---- IQ4_NL down: the weights through each wave's own shared-memory ring ----
+// IQ4_NL rows are 18-byte blocks, so a lane's bytes of a block (its scale and
+// 4 qs bytes) are two or three narrow loads.  Here each wave instead copies
+// its 32 weight rows' bytes of a step as whole 16-byte pieces (three direct
+// copies of 64 lanes) into one of three slots of its own ring and reads them
+// back from shared memory.  A step is 128 K elements (4 blocks); a row's
+// 72 bytes of it start at byte offset delta = address % 16 (an even value)
+// of its first piece, so 6 pieces hold them.
+constexpr int IQ_KC = 128;                          // K elements per step
+constexpr int IQ_PIECES = 6;                        // 16-byte pieces per weight row and step
+constexpr int IQ_ROWB = IQ_PIECES * 16;
+constexpr int IQ_COPIES = 32 * IQ_PIECES / 64;      // direct copies per wave and step
+constexpr int IQ_SLOT = 32 * IQ_ROWB;               // bytes per wave and slot
+constexpr int IQ_STAGE = PT * 2 * IQ_KC * 2;        // [64 rows][2 planes][128] fp16
+constexpr int PF_IQ_LDS = 2 * IQ_STAGE + PF_WAVES * 3 * IQ_SLOT;
+static_assert(IQ_COPIES * 64 == 32 * IQ_PIECES, "the copies cover the slot exactly");
+
+// Activation stage of one 128-element K chunk: [row][plane][16 chunks of 16
+// bytes], chunk position c ^ (row & 15); one copy covers two rows.
+QG_DEV void stage_rows128(uint8_t *stage, const _Float16 *planes, int stride, const int *src, int chunk, int nck, int nrows,
+                          int wave, int lane) {
+    for (int q = wave; 2 * q < nrows; q += PF_WAVES) {
+        const int tr = 2 * q + (lane >> 5), p = (lane >> 4) & 1;
+        int c = (lane & 15) ^ (tr & 15);
+        if (c >= nck) c = 0;  // positions no reader uses
+        dma16_ordered(planes + ((size_t)src[tr] * 2 + p) * stride + (size_t)chunk * IQ_KC + c * 8, stage + q * 1024);
+    }
+}
+QG_DEV qg_half8 stage_frag128(const uint8_t *st, int r, int p, int c) {
+    return ld_frag((const _Float16 *)(st + (r * 2 + p) * 256 + 16 * (c ^ (r & 15))));
+}
+
+// The wave's copies of step chunk kc (nb blocks) of its 32 consecutive weight
+// rows (row r at w + r * rb): piece i = 6 r + p of the slot is the p-th
+// 16-byte piece from the row's first aligned piece; pieces past the row's
+// last needed one copy that one again into a position no reader uses (so no
+// copy leaves the 16-byte blocks that hold the needed bytes).
+QG_DEV void iq_copy(uint8_t *slot, const uint8_t *w, size_t rb, int kc, int nb, int lane) {
+#pragma unroll
+    for (int t = 0; t < IQ_COPIES; t++) {
+        const int i = t * 64 + lane, r = i / IQ_PIECES, p = i - IQ_PIECES * r;
+        const uintptr_t a = (uintptr_t)(w + (size_t)r * rb) + (uintptr_t)kc * 72;
+        const int delta = (int)(a & 15), np = (delta + 18 * nb + 15) >> 4;
+        dma16_ordered((const void *)((a & ~(uintptr_t)15) + 16 * (uintptr_t)min(p, np - 1)), slot + t * 1024);
+    }
+}
+
+// y[m][n] += d_b * (lut[q] . x) for the nb blocks of a step, weights from the
+// slot (rows 16 n + j of the wave's 32), activations from the stage.
+QG_DEV void iq_chunk_lds(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *w, size_t rb, int kc, const uint8_t *st,
+                         int j, int kq, int nb, int M) {
+    const uint8_t *rowp[NCT];
+#pragma unroll
+    for (int n = 0; n < NCT; n++) {
+        const int r = 16 * n + j;
+        const int delta = (int)(((uintptr_t)(w + (size_t)r * rb) + (uintptr_t)kc * 72) & 15);
+        rowp[n] = slot + r * IQ_ROWB + delta;
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b >= nb) break;  // uniform
+        qg_half8 bf[NCT];
+        float d[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++) {
+            const uint16_t *p16 = (const uint16_t *)(rowp[n] + 18 * b);
+            d[n] = qg_half_u16(p16[0]);
+            bf[n] = iq4_frag4((uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16));
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            if (m < M) {  // uniform
+                const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * b + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * b + kq);
+#pragma unroll
+                for (int n = 0; n < NCT; n++) {
+                    qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[n], acc, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
+                }
+            }
+        }
+    }
+}
+
+// Item = (group, 64-row tile, 256 D rows); wave w: D rows 32 w .. +31 of the
+// block as two column tiles.  Steps are the item's K chunks of 128.
+__global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    uint8_t *lds = (uint8_t *)s_dyn;
+    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int2 s_it[IT_RING];
+    __shared__ int s_src[2][PT], s_slot[2][PT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    for (int i = tid; i <= NG; i += 512) {
+        s_tb[i] = A.tt->tbase[i];
+        if (i < NG) s_go[i] = A.tt->gorder[i];
+        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
+    }
+    const int ndb = A.D / DN_DB, F = A.F, nkc = (F + IQ_KC - 1) / IQ_KC;
+    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
+    const ItemRange ir = xcd_items(total);
+    const int nitems = range_count(ir), steps = nitems * nkc;
+    if (steps == 0) return;  // block-uniform
+    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, ndb, nitems, ir};
+    __syncthreads();
+    R.fill(0, IT_RING, tid);
+    __syncthreads();
+    uint8_t *ring = lds + 2 * IQ_STAGE + (size_t)wave * 3 * IQ_SLOT;   // this wave's three slots
+    auto set_rows = [&](const PfItem &it, int buf) {
+        if (wave == 0) s_src[buf][lane] = (it.shared ? A.nt * QG_TOP : 0) + it.base + min(lane, it.nv - 1);
+        item_rows(s_slot[buf], it, A.row_slot, A.nt * QG_TOP, wave, lane);
+    };
+    // the wave's first weight row of an item, and the row stride
+    auto wave_rows = [&](const PfItem &it, size_t &rb) {
+        rb = it.shared ? A.sh_rb : A.rb;
+        const uint8_t *bw = it.shared ? A.sh_down : A.down + (size_t)it.g * A.D * A.rb;
+        return bw + (size_t)(it.blk * DN_DB + wave * 32) * rb;
+    };
+    auto nblocks = [&](int kc) { return min(4, F / 32 - 4 * kc); };
+    auto stage = [&](const PfItem &it, int buf, int kc, int b) {
+        stage_rows128(lds + b * IQ_STAGE, A.midp, F, s_src[buf], kc, 4 * nblocks(kc), 16 * it.M, wave, lane);
+    };
+    auto copy_step = [&](int q, StepPos p) {
+        size_t rb;
+        const uint8_t *w = wave_rows(R.at(p.k), rb);
+        iq_copy(ring + q * IQ_SLOT, w, rb, p.c, nblocks(p.c), lane);
+    };
+    PfItem cur = R.at(0);
+    set_rows(cur, 0);
+    wait_vmem();
+    __syncthreads();
+    stage(cur, 0, 0, 0);
+    StepPos pos{0, 0};
+    copy_step(0, pos);
+    if (1 < steps) copy_step(1, next_pos(pos, nkc));
+    qg_f4 y[4][NCT];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3,
+    // whose reads (step s - 1) are done
+    auto step = [&](int s, int qc, int qn) {
+        const int k = pos.k, kc = pos.c;
+        const StepPos p1 = next_pos(pos, nkc), p2 = next_pos(p1, nkc);
+        if (s + 1 < steps) wait_vmem_but<IQ_COPIES>();
+        else wait_vmem();
+        __syncthreads();
+        if (kc == 0) {
+            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+            // the next item's rows, copied while this item streams
+            if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
+        }
+        if (s + 1 < steps) {
+            if (p1.k != k) {
+                if (nkc == 1) {  // the rows were copied just above
+                    wait_vmem();
+                    __syncthreads();
+                }
+                stage(R.at(p1.k), p1.k & 1, p1.c, (s + 1) & 1);
+            } else {
+                stage(cur, k & 1, p1.c, (s + 1) & 1);
+            }
+        }
+        if (s + 2 < steps) copy_step(qn, p2);
+        size_t rb;
+        const uint8_t *w = wave_rows(cur, rb);
+        iq_chunk_lds(y, ring + qc * IQ_SLOT, w, rb, kc, lds + (s & 1) * IQ_STAGE, j, kq, nblocks(kc), cur.M);
+        if (kc == nkc - 1) {
+            const int d0 = cur.blk * DN_DB + wave * 32;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                if (m >= cur.M) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tr = m * 16 + 4 * kq + i;
+                    if (tr < cur.nv) {
+                        float *o = A.slots + (size_t)s_slot[k & 1][tr] * A.D + d0 + j;
+#pragma unroll
+                        for (int n = 0; n < NCT; n++) o[16 * n] = y[m][n][i];
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s + 1 < steps) cur = R.at(k + 1);
+        }
+        pos = p1;
+    };
+    for (int s = 0; s < steps; s += 3) {
+        step(s, 0, 2);
+        if (s + 1 < steps) step(s + 1, 1, 0);
+        if (s + 2 < steps) step(s + 2, 2, 1);
     }
 }
 
@@ -1029,7 +1262,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
         DnArgs DA{nt, D, F, offsets, tt, seg_lo, seg_hi, row_slot, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr,
                   qg_row_bytes_host(L->down_type, F), sh ? qg_row_bytes_host(L->sh_down_type, F) : 0, midp, msp, slots};
         if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel<QT_Q4_K>, dim3(grid), dim3(512), PF_LDS, s, DA);
-        else pf_launch(slot, pf_down_kernel<QT_IQ4_NL>, dim3(grid), dim3(512), PF_LDS, s, DA);
+        else pf_launch(slot, pf_down_iq_kernel, dim3(grid), dim3(512), PF_IQ_LDS, s, DA);
         return hipGetLastError();
     };
     if ((rc = down(0, 1, L->down_type, 6))) return rc;
