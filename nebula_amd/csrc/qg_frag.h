@@ -82,6 +82,21 @@ QG_DEV void dma16_ordered(const void *g, void *lds_base) {
                  : "v"(g), "s"(base)
                  : "memory");
 }
+// Three dma16_ordered copies to lds_base, +1024 and +2048 under one M0 value:
+// the instruction offset moves both the shared-memory and the global address,
+// so copy t reads g_t through g_t - 1024 t + offset.
+QG_DEV void dma16x3_ordered(const uint8_t *g0, const uint8_t *g1, const uint8_t *g2, void *lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(qg_lds_void *)lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "global_load_lds_dwordx4 %2, off offset:1024\n\t"
+                 "global_load_lds_dwordx4 %3, off offset:2048\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g0), "v"(g1 - 1024), "v"(g2 - 2048), "s"(base)
+                 : "memory");
+}
 // dma16_ordered for 4 bytes per lane (global_load_lds_dword): lane l's word
 // lands at lds_base + 4*l.
 QG_DEV void dma4_ordered(const void *g, void *lds_base) {

@@ -631,147 +631,7 @@ struct GuArgs {
     int down_fmt, sh_down_fmt;
 };
 
-// Item = (group, 64-row tile, 128 F rows); wave w: F rows f0 = 16 w .. +15 of
-// the block, column tile 0 their gate rows, tile 1 their up rows.  Steps are
-// the item's D/256 superblocks.
-__global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
-    extern __shared__ uint4 s_dyn[];
-    uint8_t *lds = (uint8_t *)s_dyn;
-    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
-    __shared__ int2 s_it[IT_RING];
-    __shared__ int s_src[2][PT];
-    __shared__ float s_gs[PF_WAVES][PT];     // 16-row partial sums of the 32-row groups (Q4_K down format)
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    for (int i = tid; i <= NG; i += 512) {
-        s_tb[i] = A.tt->tbase[i];
-        if (i < NG) s_go[i] = A.tt->gorder[i];
-        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
-    }
-    const int nfb = A.F / GU_FB, NSB = A.D / 256, D32 = A.D / 32, F = A.F;
-    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
-    const ItemRange ir = xcd_items(total);
-    const int nitems = range_count(ir), steps = nitems * NSB;
-    if (steps == 0) return;  // block-uniform
-    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
-    __syncthreads();
-    R.fill(0, IT_RING, tid);
-    __syncthreads();
-    // mid row of tile row tr (< nv): the CSR position, shared rows after the 10 nt selections
-    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
-    auto weight_rows = [&](const PfItem &it, const uint8_t **wrow) {
-        const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
-        const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
-        const int f = it.blk * GU_FB + wave * 16 + j;
-        wrow[0] = bg + (size_t)f * A.rb;
-        wrow[1] = bu + (size_t)f * A.rb;
-    };
-    auto stage = [&](const PfItem &it, int buf, int sb, int b) {
-        stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.xp, A.D, A.xsp, D32, s_src[buf], sb, 32,
-                   16 * it.M, wave, lane);
-    };
-    const uint8_t *wrow[NCT];
-    auto load_step = [&](Q4Ops &o, StepPos p) {
-        weight_rows(R.at(p.k), wrow);
-        q4_load(o, wrow, p.c, kq);
-    };
-    // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
-    PfItem cur = R.at(0);
-    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
-    wait_vmem();
-    __syncthreads();
-    stage(cur, 0, 0, 0);
-    // weights of step s live in w[s % 3]: loaded two steps ahead, never copied
-    // between registers (a copy would wait for the loads in flight)
-    Q4Ops w0, w1, w2;
-    StepPos pos{0, 0};
-    load_step(w0, pos);
-    if (1 < steps) load_step(w1, next_pos(pos, NSB));
-    qg_f4 y[4][NCT];
-#pragma unroll
-    for (int m = 0; m < 4; m++)
-#pragma unroll
-        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto step = [&](int s, const Q4Ops &wc, Q4Ops &wn) {
-        const int k = pos.k, sb = pos.c;
-        const StepPos p1 = next_pos(pos, NSB), p2 = next_pos(p1, NSB);
-        if (s + 1 < steps) wait_vmem_but<Q4_LOADS>();
-        else wait_vmem();
-        __syncthreads();
-        if (sb == 0) {
-            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
-            // the next item's rows, copied while this item streams (its buffer
-            // held item k - 1's rows, staged long ago)
-            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
-        }
-        // the next step's stage
-        if (s + 1 < steps) {
-            if (p1.k != k) {
-                if (NSB == 1) {  // the rows were copied just above
-                    wait_vmem();
-                    __syncthreads();
-                }
-                stage(R.at(p1.k), p1.k & 1, p1.c, (s + 1) & 1);
-            } else {
-                stage(cur, k & 1, p1.c, (s + 1) & 1);
-            }
-        }
-        if (s + 2 < steps) load_step(wn, p2);  // the weights two steps ahead
-        const uint8_t *st = lds + (s & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
-        q4_chunk(y, wc, st, ss, j, kq, cur.M);
-        if (sb == NSB - 1) {
-            // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
-            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt;
-            const int f = cur.blk * GU_FB + wave * 16 + j, pa = plane_pos(fmt, f);
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                if (m >= cur.M) break;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tr = m * 16 + 4 * kq + i;
-                    const float ma = qg_swiglu_fast(y[m][0][i], y[m][1][i]);
-                    const bool ok = tr < cur.nv;
-                    if (ok) {
-                        _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
-                        const _Float16 ha = (_Float16)ma;
-                        hp[pa] = ha;
-                        hp[F + pa] = (_Float16)(ma - (float)ha);
-                    }
-                    if (fmt == QT_Q4_K) {
-                        // this wave's 16 rows of the 32-row group (lanes of one kq hold all 16 j)
-                        float sp = ma;
-                        sp += __shfl_xor(sp, 1);
-                        sp += __shfl_xor(sp, 2);
-                        sp += __shfl_xor(sp, 4);
-                        sp += __shfl_xor(sp, 8);
-                        if (j == 0) s_gs[wave][tr] = sp;
-                    }
-                }
-            }
-            if (fmt == QT_Q4_K) {  // block-uniform
-                __syncthreads();
-                // waves 2i and 2i+1 hold the two halves of 32-row group i of the block
-                if ((wave & 1) == 0 && lane < cur.nv) {
-                    const float sum = s_gs[wave][lane] + s_gs[wave + 1][lane];
-                    _Float16 *sp = A.msp + (size_t)mrow(cur, lane) * 2 * (F / 32) + (cur.blk * GU_FB + wave * 16) / 32;
-                    const _Float16 hs = (_Float16)sum;
-                    sp[0] = hs;
-                    sp[F / 32] = (_Float16)(sum - (float)hs);
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = R.at(k + 1);
-        }
-        pos = p1;
-    };
-    for (int s = 0; s < steps; s += 3) {
-        step(s, w0, w2);
-        if (s + 1 < steps) step(s + 1, w1, w0);
-        if (s + 2 < steps) step(s + 2, w2, w1);
-    }
-}
+// (the kernel follows the down kernels: it shares their 128-element stage)
 
 // ---------------- P6: down ----------------
 struct DnArgs {
@@ -948,19 +808,23 @@ QG_DEV qg_half8 stage_frag128(const uint8_t *st, int r, int p, int c) {
 // last needed one copy that one again into a position no reader uses (so no
 // copy leaves the 16-byte blocks that hold the needed bytes).
 QG_DEV void iq_copy(uint8_t *slot, const uint8_t *w, size_t rb, int kc, int nb, int lane) {
+    const uint8_t *g[IQ_COPIES];
 #pragma unroll
     for (int t = 0; t < IQ_COPIES; t++) {
         const int i = t * 64 + lane, r = i / IQ_PIECES, p = i - IQ_PIECES * r;
         const uintptr_t a = (uintptr_t)(w + (size_t)r * rb) + (uintptr_t)kc * 72;
         const int delta = (int)(a & 15), np = (delta + 18 * nb + 15) >> 4;
-        dma16_ordered((const void *)((a & ~(uintptr_t)15) + 16 * (uintptr_t)min(p, np - 1)), slot + t * 1024);
+        g[t] = (const uint8_t *)((a & ~(uintptr_t)15) + 16 * (uintptr_t)min(p, np - 1));
     }
+    static_assert(IQ_COPIES == 3, "three copies under one M0 value");
+    dma16x3_ordered(g[0], g[1], g[2], slot);
 }
 
 // y[m][n] += d_b * (lut[q] . x) for the nb blocks of a step, weights from the
 // slot (rows 16 n + j of the wave's 32), activations from the stage.
+template <int M>
 QG_DEV void iq_chunk_lds(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *w, size_t rb, int kc, const uint8_t *st,
-                         int j, int kq, int nb, int M) {
+                         int j, int kq, int nb) {
     const uint8_t *rowp[NCT];
 #pragma unroll
     for (int n = 0; n < NCT; n++) {
@@ -980,16 +844,14 @@ QG_DEV void iq_chunk_lds(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t 
             bf[n] = iq4_frag4((uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16));
         }
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            if (m < M) {  // uniform
-                const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * b + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * b + kq);
+        for (int m = 0; m < M; m++) {
+            const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * b + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * b + kq);
 #pragma unroll
-                for (int n = 0; n < NCT; n++) {
-                    qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[n], acc, 0, 0, 0);
+            for (int n = 0; n < NCT; n++) {
+                qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[n], acc, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
-                }
+                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
             }
         }
     }
@@ -1053,8 +915,9 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
         for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
     // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3,
     // whose reads (step s - 1) are done
-    auto step = [&](int s, int qc, int qn) {
-        const int k = pos.k, kc = pos.c;
+    int qc = 0;
+    for (int s = 0; s < steps; s++) {
+        const int k = pos.k, kc = pos.c, qn = qc == 0 ? 2 : qc - 1;
         const StepPos p1 = next_pos(pos, nkc), p2 = next_pos(p1, nkc);
         if (s + 1 < steps) wait_vmem_but<IQ_COPIES>();
         else wait_vmem();
@@ -1078,7 +941,13 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
         if (s + 2 < steps) copy_step(qn, p2);
         size_t rb;
         const uint8_t *w = wave_rows(cur, rb);
-        iq_chunk_lds(y, ring + qc * IQ_SLOT, w, rb, kc, lds + (s & 1) * IQ_STAGE, j, kq, nblocks(kc), cur.M);
+        const uint8_t *slot = ring + qc * IQ_SLOT, *st = lds + (s & 1) * IQ_STAGE;
+        switch (cur.M) {  // block-uniform
+        case 1: iq_chunk_lds<1>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
+        case 2: iq_chunk_lds<2>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
+        case 3: iq_chunk_lds<3>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
+        default: iq_chunk_lds<4>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
+        }
         if (kc == nkc - 1) {
             const int d0 = cur.blk * DN_DB + wave * 32;
 #pragma unroll
@@ -1101,11 +970,232 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
             if (s + 1 < steps) cur = R.at(k + 1);
         }
         pos = p1;
+        qc = qc == 2 ? 0 : qc + 1;
+    }
+}
+
+// ---- gate/up: the Q4_K weights through each wave's own shared-memory ring ----
+// A step is half a superblock (128 K elements, groups 4h .. 4h+3): per weight
+// row the superblock's 16-byte header and the half's 64 qs bytes, 5 pieces,
+// copied like the IQ4_NL rows (160 pieces in 3 copies; lanes past them copy
+// the last piece again into the slot's padding).  The 8 group sums of a
+// superblock are staged with its first half, into their own double buffer.
+constexpr int GQ_PIECES = 5;
+constexpr int GQ_ROWB = GQ_PIECES * 16;
+constexpr int GQ_COPIES = 3;
+constexpr int GQ_SLOT = GQ_COPIES * 64 * 16;
+constexpr int GQ_SUMS = PT * 2 * 16;                 // [64 rows][2 planes][8 group sums] fp16
+constexpr int PF_GQ_LDS = 2 * IQ_STAGE + 2 * GQ_SUMS + PF_WAVES * 3 * GQ_SLOT;
+static_assert(32 * GQ_PIECES <= GQ_COPIES * 64, "the copies cover the slot");
+
+// Row r of the wave's 32 (r < 16: gate row f0 + r, else up row f0 + r - 16),
+// superblock sb, half h: piece 0 the header, pieces 1..4 the half's qs bytes.
+QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_row0, size_t rb, int sb, int h, int lane) {
+    const uint8_t *g[GQ_COPIES];
+#pragma unroll
+    for (int t = 0; t < GQ_COPIES; t++) {
+        const int i = min(t * 64 + lane, 32 * GQ_PIECES - 1), r = i / GQ_PIECES, p = i - GQ_PIECES * r;
+        const uint8_t *row = (r < 16 ? gate_row0 : up_row0) + (size_t)(r & 15) * rb + (size_t)sb * 144;
+        g[t] = row + (p == 0 ? 0 : 16 + 64 * h + 16 * (p - 1));
+    }
+    static_assert(GQ_COPIES == 3, "three copies under one M0 value");
+    dma16x3_ordered(g[0], g[1], g[2], slot);
+}
+
+// One half superblock for the first M row tiles: per K step f (4 of them)
+// the two weight fragments, then every row tile's products (fragment f + 1
+// is built while step f's products run); y += d * acc per half, and with the
+// sums (first half) the min term -dmin * (m . X) over the superblock's 8
+// groups.
+template <int M>
+QG_DEV void gq_chunk(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq) {
+    Q4kHeader hd[NCT];
+    uint4 qc[NCT];
+    uint32_t S[NCT];
+    const int sh = 16 * (kq >> 1);  // bit offset of the lane's low-nibble group in the half's scale word
+#pragma unroll
+    for (int n = 0; n < NCT; n++) {
+        const uint8_t *row = slot + (16 * n + j) * GQ_ROWB;
+        hd[n] = q4k_header(*(const uint4 *)row);
+        qc[n] = *(const uint4 *)(row + 16 + 16 * kq);
+        S[n] = h ? hd[n].S[1] : hd[n].S[0];  // the half's 4 group scales (a select: h is a runtime value)
+    }
+    qg_f4 acc[M][NCT];
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+        qg_half8 b[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++) b[n] = q4k_chunk_frag(qc[n], f, (_Float16)(int)((S[n] >> (sh + 8 * (f >> 1))) & 0xffu));
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * f + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * f + kq);
+#pragma unroll
+            for (int n = 0; n < NCT; n++) {
+                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[n], acc[m][n], 0, 0, 0);
+                acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[n], acc[m][n], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(hd[n].d, acc[m][n][i], y[m][n][i]);
+    if (ss) {
+        // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
+        const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
+        qg_half8 bm[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++)
+#pragma unroll
+            for (int g = 0; g < 8; g++) bm[n][g] = kq < 2 ? (_Float16)q4k_m(hd[n], g) : (_Float16)0.0f;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
+#pragma unroll
+            for (int n = 0; n < NCT; n++) {
+                const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(-hd[n].dmin, mm[i], y[m][n][i]);
+            }
+        }
+    }
+}
+
+// Item = (group, 64-row tile, 128 F rows); wave w: F rows f0 = 16 w .. +15 of
+// the block, column tile 0 their gate rows, tile 1 their up rows.  Steps are
+// the item's D/128 half superblocks.
+__global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    uint8_t *lds = (uint8_t *)s_dyn;
+    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int2 s_it[IT_RING];
+    __shared__ int s_src[2][PT];
+    __shared__ float s_gs[PF_WAVES][PT];     // 16-row partial sums of the 32-row groups (Q4_K down format)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    for (int i = tid; i <= NG; i += 512) {
+        s_tb[i] = A.tt->tbase[i];
+        if (i < NG) s_go[i] = A.tt->gorder[i];
+        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
+    }
+    const int nfb = A.F / GU_FB, NH = A.D / 128, D32 = A.D / 32, F = A.F;   // NH steps per item (even)
+    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
+    const ItemRange ir = xcd_items(total);
+    const int nitems = range_count(ir), steps = nitems * NH;
+    if (steps == 0) return;  // block-uniform
+    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
+    __syncthreads();
+    R.fill(0, IT_RING, tid);
+    __syncthreads();
+    uint8_t *sums = lds + 2 * IQ_STAGE;                                       // two superblock sum buffers
+    uint8_t *ring = lds + 2 * IQ_STAGE + 2 * GQ_SUMS + (size_t)wave * 3 * GQ_SLOT;  // this wave's three slots
+    // mid row of tile row tr (< nv): the CSR position, shared rows after the 10 nt selections
+    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
+    // stage of step s (item it, half c): the activation chunk, and with a
+    // superblock's first half its group sums
+    auto stage = [&](const PfItem &it, int buf, int c, int s) {
+        stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
+        if ((c & 1) == 0 && wave * 32 < 16 * it.M) {
+            const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
+            dma16_ordered(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32 + (size_t)(c >> 1) * 8, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
+        }
     };
-    for (int s = 0; s < steps; s += 3) {
-        step(s, 0, 2);
-        if (s + 1 < steps) step(s + 1, 1, 0);
-        if (s + 2 < steps) step(s + 2, 2, 1);
+    auto copy_step = [&](int q, StepPos p) {
+        const PfItem it = R.at(p.k);
+        const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
+        const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
+        const size_t f0 = (size_t)(it.blk * GU_FB + wave * 16) * A.rb;
+        gq_copy(ring + q * GQ_SLOT, bg + f0, bu + f0, A.rb, p.c >> 1, p.c & 1, lane);
+    };
+    // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
+    PfItem cur = R.at(0);
+    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
+    wait_vmem();
+    __syncthreads();
+    stage(cur, 0, 0, 0);
+    StepPos pos{0, 0};
+    copy_step(0, pos);
+    if (1 < steps) copy_step(1, next_pos(pos, NH));
+    qg_f4 y[4][NCT];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int qc = 0;  // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3 (read by step s - 1)
+    for (int s = 0; s < steps; s++) {
+        const int k = pos.k, c = pos.c, qn = qc == 0 ? 2 : qc - 1;
+        const StepPos p1 = next_pos(pos, NH), p2 = next_pos(p1, NH);
+        if (s + 1 < steps) wait_vmem_but<GQ_COPIES>();
+        else wait_vmem();
+        __syncthreads();
+        if (c == 0) {
+            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+            // the next item's rows, copied while this item streams (its buffer
+            // held item k - 1's rows, staged long ago)
+            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+        }
+        if (s + 1 < steps) stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
+        if (s + 2 < steps) copy_step(qn, p2);
+        const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + qc * GQ_SLOT;
+        const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
+        switch (cur.M) {  // block-uniform
+        case 1: gq_chunk<1>(y, slot, st, ss, c & 1, j, kq); break;
+        case 2: gq_chunk<2>(y, slot, st, ss, c & 1, j, kq); break;
+        case 3: gq_chunk<3>(y, slot, st, ss, c & 1, j, kq); break;
+        default: gq_chunk<4>(y, slot, st, ss, c & 1, j, kq); break;
+        }
+        if (c == NH - 1) {
+            // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
+            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt;
+            const int f = cur.blk * GU_FB + wave * 16 + j, pa = plane_pos(fmt, f);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                if (m >= cur.M) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tr = m * 16 + 4 * kq + i;
+                    const float ma = qg_swiglu_fast(y[m][0][i], y[m][1][i]);
+                    if (tr < cur.nv) {
+                        _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
+                        const _Float16 ha = (_Float16)ma;
+                        hp[pa] = ha;
+                        hp[F + pa] = (_Float16)(ma - (float)ha);
+                    }
+                    if (fmt == QT_Q4_K) {
+                        // this wave's 16 rows of the 32-row group (lanes of one kq hold all 16 j)
+                        float sp = ma;
+                        sp += __shfl_xor(sp, 1);
+                        sp += __shfl_xor(sp, 2);
+                        sp += __shfl_xor(sp, 4);
+                        sp += __shfl_xor(sp, 8);
+                        if (j == 0) s_gs[wave][tr] = sp;
+                    }
+                }
+            }
+            if (fmt == QT_Q4_K) {  // block-uniform
+                __syncthreads();
+                // waves 2i and 2i+1 hold the two halves of 32-row group i of the block
+                if ((wave & 1) == 0 && lane < cur.nv) {
+                    const float sum = s_gs[wave][lane] + s_gs[wave + 1][lane];
+                    _Float16 *sp = A.msp + (size_t)mrow(cur, lane) * 2 * (F / 32) + (cur.blk * GU_FB + wave * 16) / 32;
+                    const _Float16 hs = (_Float16)sum;
+                    sp[0] = hs;
+                    sp[F / 32] = (_Float16)(sum - (float)hs);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s + 1 < steps) cur = R.at(k + 1);
+        }
+        pos = p1;
+        qc = qc == 2 ? 0 : qc + 1;
     }
 }
 
@@ -1255,7 +1345,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
         GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
                  xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type};
-        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(512), PF_LDS, s, G);
+        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
         if ((rc = hipGetLastError())) return rc;
     }
     auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
