@@ -10,6 +10,8 @@ hipStream_t qg_stream(void);
 // error code).  Superseded buffers stay allocated until the process ends, so
 // a graph captured with the old address never touches freed memory.
 int qg_scratch_grow(void **buf, size_t *cap, size_t need);
+// Compute units of the current device (persistent grids: one workgroup each).
+int qg_cu_count();
 
 // Shapes used by the entry points that take no width (gather, scatter,
 // reduce, mtp_moe, shared_add); set by qg_moe_configure.

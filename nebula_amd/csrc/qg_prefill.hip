@@ -87,17 +87,6 @@ PfLayout pf_layout(int D, int F, int nt) {
     return L;
 }
 
-int cu_count() {
-    static int n = 0;
-    if (!n) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            n = v;
-        else
-            return 256;
-    }
-    return n;
-}
 
 template <typename K, typename... Args>
 void pf_launch(int slot, K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
@@ -1340,7 +1329,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
               (const int *)flag, nt);
     if ((rc = hipGetLastError())) return rc;
     // grouped GEMMs: the dense pass (experts with >= 256 rows), then the rest
-    const int grid = cu_count();
+    const int grid = qg_cu_count();
     for (int pass = 0; pass < 2; pass++) {
         GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),

@@ -275,3 +275,15 @@ int qg_device_info(char *name, size_t name_len, int *cus, int *clock_khz, int *m
 }
 
 }  // extern "C"
+
+int qg_cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            v <= 0)
+            return 256;
+        n = v;
+    }
+    return n;
+}
