@@ -382,6 +382,12 @@ def bench_prefill(args, data: str) -> dict:
     ms = qg.elapsed_ms(b, e) / args.steps
     qg.lib().qg_graph_destroy(g)
     kern = kernel_times(wl.step, PF_KERNELS, args.steps)
+    # the int8 variant of the dense gate/up pass, timed the same way
+    prev = qg.lib().qg_prefill_int8_dense(1)
+    try:
+        kern_i8 = kernel_times(wl.step, PF_KERNELS, args.steps)
+    finally:
+        qg.lib().qg_prefill_int8_dense(prev)
     # algorithmic matrix-core work: 2 ops per multiply-add of the useful products
     ops_gu = lambda rows: 2.0 * rows * 2 * D * FF
     ops_dn = lambda rows: 2.0 * rows * D * FF
@@ -404,6 +410,13 @@ def bench_prefill(args, data: str) -> dict:
                    "matrix_cores": "fp16 16x16x32 MFMA, exact integer weights x fp16 hi/lo activation planes, fp32 accumulate",
                    "dense_pass_int8_util_algorithmic": round(util_dense, 4) if util_dense else None,
                    "dense_pass_fp16_util_issued": round(2 * util_dense * INT8_PEAK_TOPS / FP16_PEAK_TFLOPS, 4) if util_dense else None,
+                   "dense_gate_up_int8_variant": {
+                       "arithmetic": "int8 16x16x32 MFMA per Q4_K group and activation plane (two int8 planes, row scale), "
+                                     "per-group int32->fp32 scaling",
+                       "us_fp16": round(t_gu * 1000, 2) if t_gu else None,
+                       "us_int8": round(kern_i8["gate_up_dense"] * 1000, 2) if kern_i8.get("gate_up_dense") else None,
+                       "int8_util_algorithmic": round(ops_gu(rows_dense) / (kern_i8["gate_up_dense"] * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)
+                       if kern_i8.get("gate_up_dense") and rows_dense else None},
                    "expert_gemm_TOPS_all": round((ops_gu(rows_all) + ops_dn(rows_all)) / (t_experts * 1e-3) / 1e12, 1) if t_experts else None,
                    "layer_bytes": int(layer_b), "layer_hbm_frac": round(layer_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                    "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
@@ -511,6 +524,8 @@ def main() -> int:
                          "the 48-layer stack, the prefill)")
     ap.add_argument("--matmul", action="store_true",
                     help="measure qg_matmul on the dense projections instead of the MoE layer (--batch tokens, default 1)")
+    ap.add_argument("--int8-dense", action="store_true",
+                    help="with --counter-pass: run the prefill dense gate/up pass in its int8 variant")
     ap.add_argument("--counter-pass", type=int, default=0, metavar="P",
                     help="for rocprofv3 counter runs: build the workload, print each layer's routing and algorithmic "
                          "bytes as one JSON line, then run P eager passes over the layers in order (dispatch k of a "
@@ -616,6 +631,8 @@ def main() -> int:
 
 def counter_pass(args) -> int:
     """Eager passes over the workload's layers in order, for counter runs."""
+    if args.int8_dense:
+        qg.lib().qg_prefill_int8_dense(1)
     if args.config == 3:
         nt = args.batch if args.batch is not None else 2048
         wl = PrefillWorkload(nt, seed=9300)

@@ -480,6 +480,7 @@ QG_DEV uint4 qg_ld16(const uint8_t *p) { return *(const uint4 *)p; }
 typedef _Float16 qg_half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 qg_half2 __attribute__((ext_vector_type(2)));
 typedef float qg_f4 __attribute__((ext_vector_type(4)));
+typedef int qg_i4 __attribute__((ext_vector_type(4)));
 
 QG_DEV int qg_perm8(int e) { return (e & 4) | ((e & 1) << 1) | ((e & 2) >> 1); }  // 0,2,1,3,4,6,5,7 self-inverse
 

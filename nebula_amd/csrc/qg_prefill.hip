@@ -61,7 +61,8 @@ constexpr int PF_LDS = 2 * (STAGE_BYTES + SUMS_BYTES);
 struct TileTable { int bounds[4]; int tbase[NG + 1]; int gorder[NG]; };
 
 struct PfLayout {
-    size_t logits, flag, missing, mass, xp, xsp, counts, offsets, tbase, row_token, row_slot, midp, msp, slots, xn, total;
+    size_t logits, flag, missing, mass, xp, xsp, counts, offsets, tbase, row_token, row_slot, midp, msp, slots, xn, xi8, xsc,
+        row_sx, total;
 };
 PfLayout pf_layout(int D, int F, int nt) {
     PfLayout L;
@@ -83,6 +84,9 @@ PfLayout pf_layout(int D, int F, int nt) {
     L.msp = take(rows * 2 * (F / 32) * 2);
     L.slots = take(rows * D * 4);
     L.xn = take((size_t)nt * D * 4);
+    L.xi8 = take((size_t)nt * 2 * D);
+    L.xsc = take((size_t)nt * 4);
+    L.row_sx = take((size_t)nt * QG_TOP * 4);
     L.total = off;
     return L;
 }
@@ -211,7 +215,33 @@ struct RouteArgs {
     const uint8_t *resident; double thr;
     int *ids; float *w; uint8_t *flags_out; int *flag; int *missing; double *mass;
     const float *x; int D; _Float16 *xp, *xsp;
+    int8_t *xi8; float *xsc;          // int8 planes and row scales (the int8 dense pass), or null
 };
+
+// The int8 planes of one token row (natural K order): x ~= sx * (256 hi + lo)
+// with q = rint(x / sx) in [-32639, 32639], sx = max|x| / 32639, hi =
+// floor((q + 128) / 256) in [-127, 127], lo = q - 256 hi in [-128, 127].
+QG_DEV void token_planes_i8(const float *xr, int D, int lane, int8_t *hi, int8_t *lo, float *sx_out) {
+    float mx = 0.0f;
+    for (int k = lane; k < D; k += 64) mx = fmaxf(mx, fabsf(xr[k]));
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float sx = mx > 0.0f ? mx / 32639.0f : 1.0f, inv = 1.0f / sx;
+    if (lane == 0) *sx_out = sx;
+    for (int k = 4 * lane; k < D; k += 256) {
+        const float4 v = *(const float4 *)(xr + k);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t ph = 0, pl = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = max(-32639, min(32639, (int)rintf(xv[i] * inv)));
+            const int h = (q + 128) >> 8, l = q - 256 * h;
+            ph |= (uint32_t)(h & 0xff) << (8 * i);
+            pl |= (uint32_t)(l & 0xff) << (8 * i);
+        }
+        *(uint32_t *)(hi + k) = ph;
+        *(uint32_t *)(lo + k) = pl;
+    }
+}
 
 // One wave per token: top-10 of the (biased) logits, coverage/prune, flags;
 // then the token's fp16 hi/lo planes and 32-group sum planes.
@@ -237,6 +267,7 @@ __global__ __launch_bounds__(256) void pf_route_kernel(RouteArgs A) {
     }
     _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
     token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
+    if (A.xi8) token_planes_i8(A.x + (size_t)t * A.D, A.D, lane, A.xi8 + (size_t)t * 2 * A.D, A.xi8 + (size_t)t * 2 * A.D + A.D, A.xsc + t);
 }
 
 // ---------------- P3: offsets, chunk bases, tile table ----------------
@@ -350,7 +381,7 @@ __global__ __launch_bounds__(512) void pf_count_kernel(int *counts, int *bad, co
 
 // ---------------- P4: stable fill ----------------
 __global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_slot, const int *bases, const int *ids,
-                                                      const int *flag, int nt) {
+                                                      const int *flag, int nt, float *row_sx, const float *xsc) {
     __shared__ uint32_t s_mask[QG_EXPERTS];
     const int tid = threadIdx.x, t0 = blockIdx.x * PF_CHUNK;
     s_mask[tid] = 0u;
@@ -373,6 +404,7 @@ __global__ __launch_bounds__(512) void pf_fill_kernel(int *row_token, int *row_s
         const int pos = bases[(size_t)blockIdx.x * QG_EXPERTS + e] + __popc(s_mask[e] & ((1u << tl) - 1u));
         row_token[pos] = t0 + tl;
         row_slot[pos] = (t0 + tl) * QG_TOP + k;
+        if (row_sx) row_sx[pos] = xsc[t0 + tl];
     }
 }
 
@@ -618,6 +650,7 @@ struct GuArgs {
     const _Float16 *xp, *xsp;
     _Float16 *midp, *msp;            // [rows][2][F] (down format order), [rows][2][F/32]
     int down_fmt, sh_down_fmt;
+    const int8_t *xi8; const float *xsc, *row_sx;   // the int8 variant: planes [nt][2][D], scale per token and per CSR row
 };
 
 // (the kernel follows the down kernels: it shares their 128-element stage)
@@ -977,6 +1010,93 @@ constexpr int GQ_SUMS = PT * 2 * 16;                 // [64 rows][2 planes][8 gr
 constexpr int PF_GQ_LDS = 2 * IQ_STAGE + 2 * GQ_SUMS + PF_WAVES * 3 * GQ_SLOT;
 static_assert(32 * GQ_PIECES <= GQ_COPIES * 64, "the copies cover the slot");
 
+// The int8 variant's stage of one 128-element K chunk: [row][plane][8 chunks
+// of 16 bytes] (natural K order), chunk position c ^ (row & 7); one copy
+// covers four rows.
+QG_DEV void stage_rows128_i8(uint8_t *stage, const int8_t *planes, int D, const int *src, int chunk, int nrows, int wave,
+                             int lane) {
+    for (int q = wave; 4 * q < nrows; q += PF_WAVES) {
+        const int tr = 4 * q + (lane >> 4), p = (lane >> 3) & 1, c = (lane & 7) ^ (tr & 7);
+        dma16_ordered(planes + ((size_t)src[tr] * 2 + p) * D + (size_t)chunk * 128 + c * 16, stage + q * 1024);
+    }
+}
+// 8 int8 activations of row r, plane p: elements 8 kq .. 8 kq + 7 of group f
+// of the chunk.
+QG_DEV long stage_frag128_i8(const uint8_t *st, int r, int p, int f, int kq) {
+    return *(const long *)(st + r * 256 + p * 128 + 16 * ((2 * f + (kq >> 1)) ^ (r & 7)) + 8 * (kq & 1));
+}
+
+// The int8 variant of gq_chunk: one v_mfma_i32_16x16x32_i8 per group and
+// activation plane, the weights as their nibbles q (0..15); per group the
+// int32 pair is joined (256 hi + lo, exact) and scaled by s_g in fp32, then
+// d and the row scale sx are applied per half.  The min term is gq_chunk's.
+template <int M>
+QG_DEV void gq_chunk_i8(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, const float (&sx)[4][4],
+                        int h, int j, int kq) {
+    Q4kHeader hd[NCT];
+    const uint8_t *rowp[NCT];
+    uint32_t S[NCT];
+#pragma unroll
+    for (int n = 0; n < NCT; n++) {
+        rowp[n] = slot + (16 * n + j) * GQ_ROWB;
+        hd[n] = q4k_header(*(const uint4 *)rowp[n]);
+        S[n] = h ? hd[n].S[1] : hd[n].S[0];  // group 4h + f scale in byte f
+    }
+    qg_f4 ys[M][NCT];
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++) ys[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+        long w[NCT];
+        float sg[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++) {
+            // group 4h + f: pair f / 2 of the half, nibble f % 2; the lane's 8 elements
+            const uint2 q = *(const uint2 *)(rowp[n] + 16 + 32 * (f >> 1) + 8 * kq);
+            const int sh = 4 * (f & 1);
+            w[n] = (long)(((uint64_t)((q.y >> sh) & 0x0F0F0F0Fu) << 32) | ((q.x >> sh) & 0x0F0F0F0Fu));
+            sg[n] = (float)((S[n] >> (8 * f)) & 0xffu);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const long ah = stage_frag128_i8(st, m * 16 + j, 0, f, kq), al = stage_frag128_i8(st, m * 16 + j, 1, f, kq);
+#pragma unroll
+            for (int n = 0; n < NCT; n++) {
+                const qg_i4 ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, w[n], qg_i4{0, 0, 0, 0}, 0, 0, 0);
+                const qg_i4 cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, w[n], qg_i4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) ys[m][n][i] = __builtin_fmaf(sg[n], (float)(ch[i] * 256 + cl[i]), ys[m][n][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int n = 0; n < NCT; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(hd[n].d * sx[m][i], ys[m][n][i], y[m][n][i]);
+    if (ss) {
+        const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
+        qg_half8 bm[NCT];
+#pragma unroll
+        for (int n = 0; n < NCT; n++)
+#pragma unroll
+            for (int g = 0; g < 8; g++) bm[n][g] = kq < 2 ? (_Float16)q4k_m(hd[n], g) : (_Float16)0.0f;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
+#pragma unroll
+            for (int n = 0; n < NCT; n++) {
+                const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(-hd[n].dmin, mm[i], y[m][n][i]);
+            }
+        }
+    }
+}
+
 // Row r of the wave's 32 (r < 16: gate row f0 + r, else up row f0 + r - 16),
 // superblock sb, half h: piece 0 the header, pieces 1..4 the half's qs bytes.
 QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_row0, size_t rb, int sb, int h, int lane) {
@@ -1059,12 +1179,14 @@ QG_DEV void gq_chunk(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *st,
 // Item = (group, 64-row tile, 128 F rows); wave w: F rows f0 = 16 w .. +15 of
 // the block, column tile 0 their gate rows, tile 1 their up rows.  Steps are
 // the item's D/128 half superblocks.
+template <bool I8>
 __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
     __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
     __shared__ int2 s_it[IT_RING];
     __shared__ int s_src[2][PT];
+    __shared__ float s_sx[2][PT];            // the int8 variant: row scales of the item's rows
     __shared__ float s_gs[PF_WAVES][PT];     // 16-row partial sums of the 32-row groups (Q4_K down format)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     for (int i = tid; i <= NG; i += 512) {
@@ -1087,8 +1209,14 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
     // stage of step s (item it, half c): the activation chunk, and with a
     // superblock's first half its group sums
+    // tile rows: their tokens (and with the int8 variant their row scales)
+    auto set_rows = [&](const PfItem &it, int buf) {
+        item_rows(s_src[buf], it, A.row_token, 0, wave, lane);
+        if (I8 && wave == 1) dma4_ordered((it.shared ? A.xsc : A.row_sx) + it.base + min(lane, it.nv - 1), s_sx[buf]);
+    };
     auto stage = [&](const PfItem &it, int buf, int c, int s) {
-        stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
+        if (I8) stage_rows128_i8(lds + (s & 1) * IQ_STAGE, A.xi8, A.D, s_src[buf], c, 16 * it.M, wave, lane);
+        else stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
         if ((c & 1) == 0 && wave * 32 < 16 * it.M) {
             const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
             dma16_ordered(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32 + (size_t)(c >> 1) * 8, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
@@ -1103,7 +1231,7 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     };
     // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
     PfItem cur = R.at(0);
-    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
+    set_rows(cur, 0);
     wait_vmem();
     __syncthreads();
     stage(cur, 0, 0, 0);
@@ -1126,17 +1254,31 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
             if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
             // the next item's rows, copied while this item streams (its buffer
             // held item k - 1's rows, staged long ago)
-            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+            if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
         }
         if (s + 1 < steps) stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
         if (s + 2 < steps) copy_step(qn, p2);
         const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + qc * GQ_SLOT;
         const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
-        switch (cur.M) {  // block-uniform
-        case 1: gq_chunk<1>(y, slot, st, ss, c & 1, j, kq); break;
-        case 2: gq_chunk<2>(y, slot, st, ss, c & 1, j, kq); break;
-        case 3: gq_chunk<3>(y, slot, st, ss, c & 1, j, kq); break;
-        default: gq_chunk<4>(y, slot, st, ss, c & 1, j, kq); break;
+        if constexpr (I8) {
+            float sxv[4][4];  // the scales of the lane's rows m 16 + 4 kq + i
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sxv[m][i] = s_sx[k & 1][m * 16 + 4 * kq + i];
+            switch (cur.M) {  // block-uniform
+            case 1: gq_chunk_i8<1>(y, slot, st, ss, sxv, c & 1, j, kq); break;
+            case 2: gq_chunk_i8<2>(y, slot, st, ss, sxv, c & 1, j, kq); break;
+            case 3: gq_chunk_i8<3>(y, slot, st, ss, sxv, c & 1, j, kq); break;
+            default: gq_chunk_i8<4>(y, slot, st, ss, sxv, c & 1, j, kq); break;
+            }
+        } else {
+            switch (cur.M) {  // block-uniform
+            case 1: gq_chunk<1>(y, slot, st, ss, c & 1, j, kq); break;
+            case 2: gq_chunk<2>(y, slot, st, ss, c & 1, j, kq); break;
+            case 3: gq_chunk<3>(y, slot, st, ss, c & 1, j, kq); break;
+            default: gq_chunk<4>(y, slot, st, ss, c & 1, j, kq); break;
+            }
         }
         if (c == NH - 1) {
             // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
@@ -1273,6 +1415,15 @@ __global__ __launch_bounds__(1024) void pf_stats_kernel(qg_prune_stats *stats, c
 
 }  // namespace
 
+// The dense gate/up pass in int8 (two int8 activation planes, per-group
+// int32 -> fp32 scaling) instead of fp16 hi/lo planes, for the calling thread.
+static thread_local int tl_pf_i8 = 0;
+extern "C" int qg_prefill_int8_dense(int on) {
+    const int prev = tl_pf_i8;
+    tl_pf_i8 = on ? 1 : 0;
+    return prev;
+}
+
 bool qg_prefill_ok(const qg_moe_layer *L) {
     const int D = L->width, F = L->ff;
     if (D % DN_DB || F % GU_FB) return false;
@@ -1316,8 +1467,11 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, L->router_bias, logits};
     pf_launch(0, pf_router_kernel, dim3((nt + RT_TOK - 1) / RT_TOK, (rows + RT_ROWS - 1) / RT_ROWS), dim3(512), RT_LDS, s, R);
     if ((rc = hipGetLastError())) return rc;
+    const bool i8 = tl_pf_i8 != 0;
+    int8_t *xi8 = i8 ? (int8_t *)(ws + lay.xi8) : nullptr;
+    float *xsc = i8 ? (float *)(ws + lay.xsc) : nullptr, *row_sx = i8 ? (float *)(ws + lay.row_sx) : nullptr;
     RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, flag,
-                 (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp};
+                 (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp, xi8, xsc};
     pf_launch(1, pf_route_kernel, dim3((nt + 3) / 4), dim3(256), 0, s, RA);
     if ((rc = hipGetLastError())) return rc;
     pf_launch(10, pf_count_kernel, dim3(nch), dim3(512), 0, s, counts, (int *)nullptr, (const int *)ids, (const int *)flag, nt);
@@ -1326,15 +1480,16 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
               (int *)nullptr);
     if ((rc = hipGetLastError())) return rc;
     pf_launch(3, pf_fill_kernel, dim3(nch), dim3(512), 0, s, row_token, row_slot, (const int *)counts, (const int *)ids,
-              (const int *)flag, nt);
+              (const int *)flag, nt, row_sx, (const float *)xsc);
     if ((rc = hipGetLastError())) return rc;
     // grouped GEMMs: the dense pass (experts with >= 256 rows), then the rest
     const int grid = qg_cu_count();
     for (int pass = 0; pass < 2; pass++) {
         GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
-                 xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type};
-        pf_launch(4 + pass, pf_gateup_kernel, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
+                 xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type, xi8, xsc, row_sx};
+        if (i8 && pass == 0) pf_launch(4 + pass, pf_gateup_kernel<true>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
+        else pf_launch(4 + pass, pf_gateup_kernel<false>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
         if ((rc = hipGetLastError())) return rc;
     }
     auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
@@ -1377,6 +1532,6 @@ int qg_prefill_dispatch(int *offsets, int *row_token, int *row_slot, int *status
     if (rc) return rc;
     pf_scan_kernel<<<1, 512, 0, s>>>(counts, nch, offsets, nullptr, 0, bad, status);
     if ((rc = hipGetLastError())) return rc;
-    pf_fill_kernel<<<nch, 512, 0, s>>>(row_token, row_slot, counts, ids, nullptr, nt);
+    pf_fill_kernel<<<nch, 512, 0, s>>>(row_token, row_slot, counts, ids, nullptr, nt, nullptr, nullptr);
     return hipGetLastError();
 }

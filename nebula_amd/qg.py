@@ -38,7 +38,7 @@ SIGNATURES = {
     "moe_forward_residual": ([P, P, P, P, P, P, P, I, P, P, Z], I), "moe_kernel_events": ([P, I], I),
     "event_create": ([], P), "event_destroy": ([P], None), "event_record": ([P], I), "event_elapsed": ([P, P, P], I),
     "device_info": ([P, Z, P, P, P, P], I),
-    "synth_matrix": ([P, I, U64, U64, I, I, F], I), "synth_experts": ([P, I, U64, I, I, I, I, F], I),
+    "synth_matrix": ([P, I, U64, U64, I, I, F], I), "synth_experts": ([P, I, U64, I, I, I, I, F], I), "prefill_int8_dense": ([I], I),
     "moe_handoff_pack": ([P, P, P, P, P, P, P, P, P, I, I], I), "moe_handoff_merge": ([P, P, P, P, I, I], I),
 }
 

@@ -137,6 +137,29 @@ def test_prefill_config3_routing_dispatch_outputs(layer3):
     check_outputs(fw, L, H, x, rows, "config3 B=2048")
 
 
+def test_prefill_int8_dense_pass(layer3, layer1):
+    """The int8 variant of the dense gate/up pass (qg_prefill_int8_dense):
+    config 3's dense experts, and the shared expert of a 300-token batch
+    (300 rows: in the dense pass), against the oracle at the same bars."""
+    prev = qg.lib().qg_prefill_int8_dense(1)
+    try:
+        L, H = layer3
+        x = synth.inputs(3003, 2048, 2048)
+        fw = forward(L, x)
+        ids, _, _ = check_routing(fw, H, x)
+        n = np.bincount(ids.ravel(), minlength=512)
+        dense = np.flatnonzero(n >= 256)
+        rows_dense = np.flatnonzero(np.isin(ids, dense).any(axis=1))
+        check_outputs(fw, L, H, x, rows_dense[:: max(1, len(rows_dense) // 24)], "config3 int8 dense pass")
+        L1, H1 = layer1
+        x1 = synth.inputs(3101, 300, L1.spec.width, correlated=True)
+        fw1 = forward(L1, x1)
+        check_routing(fw1, H1, x1)
+        check_outputs(fw1, L1, H1, x1, sample_rows(300, 24, 5), "shared expert in the int8 dense pass")
+    finally:
+        qg.lib().qg_prefill_int8_dense(prev)
+
+
 @pytest.mark.parametrize("nt", [18, 33, 100])
 def test_prefill_q4k_down_every_token(layer0, nt):
     """Config-0 formats (Q4_K down, min terms in both products), every row checked;
