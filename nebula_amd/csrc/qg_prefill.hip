@@ -1116,58 +1116,59 @@ QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_r
 // is built while step f's products run); y += d * acc per half, and with the
 // sums (first half) the min term -dmin * (m . X) over the superblock's 8
 // groups.
-template <int M>
-QG_DEV void gq_chunk(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq) {
-    Q4kHeader hd[NCT];
-    uint4 qc[NCT];
-    uint32_t S[NCT];
+template <int M, int NC>
+QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq) {
+    Q4kHeader hd[NC];
+    uint4 qc[NC];
+    uint32_t S[NC];
     const int sh = 16 * (kq >> 1);  // bit offset of the lane's low-nibble group in the half's scale word
 #pragma unroll
-    for (int n = 0; n < NCT; n++) {
+    for (int n = 0; n < NC; n++) {
         const uint8_t *row = slot + (16 * n + j) * GQ_ROWB;
         hd[n] = q4k_header(*(const uint4 *)row);
         qc[n] = *(const uint4 *)(row + 16 + 16 * kq);
         S[n] = h ? hd[n].S[1] : hd[n].S[0];  // the half's 4 group scales (a select: h is a runtime value)
     }
-    qg_f4 acc[M][NCT];
+    qg_f4 acc[M][NC];
 #pragma unroll
     for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int n = 0; n < NCT; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int n = 0; n < NC; n++) acc[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int f = 0; f < 4; f++) {
-        qg_half8 b[NCT];
+        qg_half8 b[NC];
 #pragma unroll
-        for (int n = 0; n < NCT; n++) b[n] = q4k_chunk_frag(qc[n], f, (_Float16)(int)((S[n] >> (sh + 8 * (f >> 1))) & 0xffu));
+        for (int n = 0; n < NC; n++) b[n] = q4k_chunk_frag(qc[n], f, (_Float16)(int)((S[n] >> (sh + 8 * (f >> 1))) & 0xffu));
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * f + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * f + kq);
 #pragma unroll
-            for (int n = 0; n < NCT; n++) {
+            for (int n = 0; n < NC; n++) {
                 acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[n], acc[m][n], 0, 0, 0);
                 acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[n], acc[m][n], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);  // one K step's fragments live at a time
     }
 #pragma unroll
     for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int n = 0; n < NCT; n++)
+        for (int n = 0; n < NC; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(hd[n].d, acc[m][n][i], y[m][n][i]);
     if (ss) {
         // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
         const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
-        qg_half8 bm[NCT];
+        qg_half8 bm[NC];
 #pragma unroll
-        for (int n = 0; n < NCT; n++)
+        for (int n = 0; n < NC; n++)
 #pragma unroll
             for (int g = 0; g < 8; g++) bm[n][g] = kq < 2 ? (_Float16)q4k_m(hd[n], g) : (_Float16)0.0f;
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
 #pragma unroll
-            for (int n = 0; n < NCT; n++) {
+            for (int n = 0; n < NC; n++) {
                 const qg_f4 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bm[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(-hd[n].dmin, mm[i], y[m][n][i]);
@@ -1274,10 +1275,10 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
             }
         } else {
             switch (cur.M) {  // block-uniform
-            case 1: gq_chunk<1>(y, slot, st, ss, c & 1, j, kq); break;
-            case 2: gq_chunk<2>(y, slot, st, ss, c & 1, j, kq); break;
-            case 3: gq_chunk<3>(y, slot, st, ss, c & 1, j, kq); break;
-            default: gq_chunk<4>(y, slot, st, ss, c & 1, j, kq); break;
+            case 1: gq_chunk<1, NCT>(y, slot, st, ss, c & 1, j, kq); break;
+            case 2: gq_chunk<2, NCT>(y, slot, st, ss, c & 1, j, kq); break;
+            case 3: gq_chunk<3, NCT>(y, slot, st, ss, c & 1, j, kq); break;
+            default: gq_chunk<4, NCT>(y, slot, st, ss, c & 1, j, kq); break;
             }
         }
         if (c == NH - 1) {
@@ -1327,6 +1328,150 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
         }
         pos = p1;
         qc = qc == 2 ? 0 : qc + 1;
+    }
+}
+
+// ---- gate/up, wide items (F a multiple of 256): 256 F rows per item ----
+// Wave w takes F rows f0 = 32 w .. +31 of the block as two pairs of column
+// tiles (pair p: gate and up rows f0 + 16 p .. +15), so a tile's activations
+// are staged half as often as with 128-row items and each step's fixed
+// costs (barrier, copy issue) cover twice the weights.  The wave's 64 weight
+// rows of a step (5 pieces each, 320 pieces in 5 copies; slot row 32 p + 16 u
+// + r: pair p, gate (u = 0) or up, row r) go to one of two slots of its ring,
+// copied one step ahead; its 32 rows are one 32-row group of a Q4_K down
+// format, whose sums it forms alone.
+constexpr int GW_FB = 256;
+constexpr int GW_COPIES = 5;
+constexpr int GW_SLOT = GW_COPIES * 64 * 16;
+constexpr int PF_GW_LDS = 2 * IQ_STAGE + 2 * GQ_SUMS + PF_WAVES * 2 * GW_SLOT;
+static_assert(64 * GQ_PIECES == GW_COPIES * 64, "the copies cover the slot");
+
+QG_DEV void gw_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_row0, size_t rb, int sb, int h, int lane) {
+#pragma unroll
+    for (int t = 0; t < GW_COPIES; t++) {
+        const int i = t * 64 + lane, r = i / GQ_PIECES, p = i - GQ_PIECES * r;
+        const uint8_t *row = ((r & 16) ? up_row0 : gate_row0) + (size_t)(16 * (r >> 5) + (r & 15)) * rb + (size_t)sb * 144;
+        dma16_ordered(row + (p == 0 ? 0 : 16 + 64 * h + 16 * (p - 1)), slot + t * 1024);
+    }
+}
+
+__global__ __launch_bounds__(512, 1) void pf_gateup_w_kernel(GuArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    uint8_t *lds = (uint8_t *)s_dyn;
+    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
+    __shared__ int2 s_it[IT_RING];
+    __shared__ int s_src[2][PT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    for (int i = tid; i <= NG; i += 512) {
+        s_tb[i] = A.tt->tbase[i];
+        if (i < NG) s_go[i] = A.tt->gorder[i];
+        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
+    }
+    const int nfb = A.F / GW_FB, NH = A.D / 128, D32 = A.D / 32, F = A.F;   // NH steps per item (even)
+    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
+    const ItemRange ir = xcd_items(total);
+    const int nitems = range_count(ir), steps = nitems * NH;
+    if (steps == 0) return;  // block-uniform
+    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
+    __syncthreads();
+    R.fill(0, IT_RING, tid);
+    __syncthreads();
+    uint8_t *sums = lds + 2 * IQ_STAGE;                                         // two superblock sum buffers
+    uint8_t *ring = lds + 2 * IQ_STAGE + 2 * GQ_SUMS + (size_t)wave * 2 * GW_SLOT;  // this wave's two slots
+    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
+    auto stage = [&](const PfItem &it, int buf, int c, int s) {
+        stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
+        if ((c & 1) == 0 && wave * 32 < 16 * it.M) {
+            const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
+            dma16_ordered(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32 + (size_t)(c >> 1) * 8, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
+        }
+    };
+    auto copy_step = [&](int q, StepPos p) {
+        const PfItem it = R.at(p.k);
+        const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
+        const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
+        const size_t f0 = (size_t)(it.blk * GW_FB + wave * 32) * A.rb;
+        gw_copy(ring + q * GW_SLOT, bg + f0, bu + f0, A.rb, p.c >> 1, p.c & 1, lane);
+    };
+    // prologue: item 0's rows, its first stage and the weights of step 0
+    PfItem cur = R.at(0);
+    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
+    wait_vmem();
+    __syncthreads();
+    stage(cur, 0, 0, 0);
+    StepPos pos{0, 0};
+    copy_step(0, pos);
+    qg_f4 y0[4][2], y1[4][2];   // pair 0, pair 1: [row tile][gate, up]
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < steps; s++) {
+        const int k = pos.k, c = pos.c;
+        const StepPos p1 = next_pos(pos, NH);
+        wait_vmem();  // this step's stage and weights (and every earlier copy)
+        __syncthreads();
+        if (c == 0) {
+            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+        }
+        if (s + 1 < steps) {
+            stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
+            copy_step((s + 1) & 1, p1);  // slot (s + 1) % 2 was read by step s - 1
+        }
+        const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + (s & 1) * GW_SLOT;
+        const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
+        const uint8_t *slot1 = slot + 32 * GQ_ROWB;
+        switch (cur.M) {  // block-uniform
+        case 1: gq_chunk<1, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<1, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
+        case 2: gq_chunk<2, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<2, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
+        case 3: gq_chunk<3, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<3, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
+        default: gq_chunk<4, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<4, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
+        }
+        if (c == NH - 1) {
+            // SwiGLU: pair t, F row f0 + 16 t + j
+            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt, f0 = cur.blk * GW_FB + wave * 32;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                if (m >= cur.M) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tr = m * 16 + 4 * kq + i;
+                    float sp = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const float ma = t ? qg_swiglu_fast(y1[m][0][i], y1[m][1][i]) : qg_swiglu_fast(y0[m][0][i], y0[m][1][i]);
+                        if (tr < cur.nv) {
+                            const int pa = plane_pos(fmt, f0 + 16 * t + j);
+                            _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
+                            const _Float16 ha = (_Float16)ma;
+                            hp[pa] = ha;
+                            hp[F + pa] = (_Float16)(ma - (float)ha);
+                        }
+                        sp += ma;
+                    }
+                    if (fmt == QT_Q4_K) {
+                        // the wave's 32 rows are one group: sum over the 16 j (lanes of one kq)
+                        sp += __shfl_xor(sp, 1);
+                        sp += __shfl_xor(sp, 2);
+                        sp += __shfl_xor(sp, 4);
+                        sp += __shfl_xor(sp, 8);
+                        if (j == 0 && tr < cur.nv) {
+                            _Float16 *spp = A.msp + (size_t)mrow(cur, tr) * 2 * (F / 32) + f0 / 32;
+                            const _Float16 hs = (_Float16)sp;
+                            spp[0] = hs;
+                            spp[F / 32] = (_Float16)(sp - (float)hs);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (s + 1 < steps) cur = R.at(k + 1);
+        }
+        pos = p1;
     }
 }
 
@@ -1489,6 +1634,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
                  xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type, xi8, xsc, row_sx};
         if (i8 && pass == 0) pf_launch(4 + pass, pf_gateup_kernel<true>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
+        else if (pass == 0 && F % GW_FB == 0) pf_launch(4 + pass, pf_gateup_w_kernel, dim3(grid), dim3(512), PF_GW_LDS, s, G);
         else pf_launch(4 + pass, pf_gateup_kernel<false>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
         if ((rc = hipGetLastError())) return rc;
     }
