@@ -19,23 +19,29 @@
 //                 plus the rank of its token in the chunk's mask, so each
 //                 expert's rows are in ascending token order (the order of
 //                 moe_map_kernel, gpu.cu:489-500).
-//   P5 gate/up  : persistent grouped GEMM; item = (group, 64-row tile, 128 F
-//                 rows); SwiGLU; mid rows as fp16 hi/lo planes.
-//   P6 down     : persistent grouped GEMM; item = (group, 64-row tile, 256 D
-//                 rows); y rows written to the selection's slot.
+//   P5 gate/up  : persistent grouped GEMM, two launches (the dense experts,
+//                 then the others and the shared expert); item = (group,
+//                 64-row tile, 128 F rows), or 256 F rows in the dense pass
+//                 when F is a multiple of 256; SwiGLU; mid rows as fp16 hi/lo
+//                 planes.
+//   P6 down     : persistent grouped GEMM, the same two passes; item =
+//                 (group, 64-row tile, 256 D rows); y rows written to the
+//                 selection's slot.
 //   P7 combine  : out[t] = sum over ranks k of w[t,k]*y[t,k] in rank order,
 //                 + sigmoid-gated shared expert, + optional residual.
 // Groups are the 512 experts plus the shared expert (group 512, every token).
 //
-// GEMM tiles (operand conventions of qg_frag.h): a workgroup is 4 waves; the
-// tile's activation rows (64 rows x 2 planes x 256 K, 64 KB) are staged in
-// shared memory by direct global->shared copies, double-buffered over K; each
-// wave owns 4 columns tiles of 16 weight rows whose quantised bytes it loads
-// into registers one K chunk ahead.  A 16x16x32 MFMA pair (hi and lo plane)
-// per (row tile, column tile, K step); row tiles past the group's last row are
-// skipped.  Rows in shared memory are 512 B; 16-byte chunk c of row r is
-// stored at chunk c ^ (r & 15), so the 16 rows one MFMA reads hit 16
-// different bank groups.
+// GEMM tiles (operand conventions of qg_frag.h): a workgroup is 8 waves, one
+// per CU; each workgroup runs a contiguous range of (item, K step) steps.  The
+// tile's activation rows (64 rows x 2 planes x one K step) are staged in
+// shared memory by direct global->shared copies, double-buffered over steps;
+// each wave owns 32 weight rows (gate/up: 16 gate + 16 up, or two such pairs)
+// whose quantised bytes it copies, one step ahead, into a ring of its own in
+// shared memory (the Q4_K down launch keeps them in registers instead).  A
+// 16x16x32 MFMA pair (hi and lo plane) per (row tile, column tile, 32-element
+// group); row tiles past the group's last row are skipped.  16-byte chunk c of
+// a staged row r sits at chunk c ^ (r & 15), so the 16 rows one MFMA reads
+// hit 16 different bank groups.
 #include "qg_internal.h"
 #include "qg_frag.h"
 #include <hip/hip_ext.h>
@@ -1111,13 +1117,18 @@ QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_r
     dma16x3_ordered(g[0], g[1], g[2], slot);
 }
 
+struct NoIssue {
+    __device__ __forceinline__ void operator()(int) const {}
+};
 // One half superblock for the first M row tiles: per K step f (4 of them)
 // the two weight fragments, then every row tile's products (fragment f + 1
 // is built while step f's products run); y += d * acc per half, and with the
 // sums (first half) the min term -dmin * (m . X) over the superblock's 8
-// groups.
-template <int M, int NC>
-QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq) {
+// groups.  issue(f) runs after K step f's products are issued: the caller's
+// copies for later steps go out while the matrix cores work.
+template <int M, int NC, typename Issue = NoIssue>
+QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq,
+                     Issue issue = Issue{}) {
     Q4kHeader hd[NC];
     uint4 qc[NC];
     uint32_t S[NC];
@@ -1148,7 +1159,8 @@ QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, 
                 acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[n], acc[m][n], 0, 0, 0);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);  // one K step's fragments live at a time
+        issue(f);
+        if (M > 2) __builtin_amdgcn_sched_barrier(0);  // one K step's fragments live at a time
     }
 #pragma unroll
     for (int m = 0; m < M; m++)
@@ -1257,8 +1269,17 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
             // held item k - 1's rows, staged long ago)
             if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
         }
-        if (s + 1 < steps) stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
-        if (s + 2 < steps) copy_step(qn, p2);
+        // the next step's stage, then the weights of step s + 2 (in this order:
+        // the wait above relies on it); the fp16 pass issues them between its
+        // first K steps' products
+        auto issue = [&](int f) {
+            if (f == 0 && s + 1 < steps) stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
+            if (f == 1 && s + 2 < steps) copy_step(qn, p2);
+        };
+        if (I8) {
+            issue(0);
+            issue(1);
+        }
         const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + qc * GQ_SLOT;
         const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
         if constexpr (I8) {
@@ -1275,10 +1296,10 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
             }
         } else {
             switch (cur.M) {  // block-uniform
-            case 1: gq_chunk<1, NCT>(y, slot, st, ss, c & 1, j, kq); break;
-            case 2: gq_chunk<2, NCT>(y, slot, st, ss, c & 1, j, kq); break;
-            case 3: gq_chunk<3, NCT>(y, slot, st, ss, c & 1, j, kq); break;
-            default: gq_chunk<4, NCT>(y, slot, st, ss, c & 1, j, kq); break;
+            case 1: gq_chunk<1, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
+            case 2: gq_chunk<2, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
+            case 3: gq_chunk<3, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
+            default: gq_chunk<4, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
             }
         }
         if (c == NH - 1) {
