@@ -1036,9 +1036,10 @@ QG_DEV long stage_frag128_i8(const uint8_t *st, int r, int p, int f, int kq) {
 // activation plane, the weights as their nibbles q (0..15); per group the
 // int32 pair is joined (256 hi + lo, exact) and scaled by s_g in fp32, then
 // d and the row scale sx are applied per half.  The min term is gq_chunk's.
-template <int M>
-QG_DEV void gq_chunk_i8(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, const float (&sx)[4][4],
+template <int M, int MY>
+QG_DEV void gq_chunk_i8(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, const float (&sx)[4][4],
                         int h, int j, int kq) {
+    static_assert(M <= MY, "row tiles");
     Q4kHeader hd[NCT];
     const uint8_t *rowp[NCT];
     uint32_t S[NCT];
@@ -1085,11 +1086,9 @@ QG_DEV void gq_chunk_i8(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *
             for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(hd[n].d * sx[m][i], ys[m][n][i], y[m][n][i]);
     if (ss) {
         const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
-        qg_half8 bm[NCT];
+        qg_half8 bm[NCT];  // lanes kq >= 2 multiply zero sums
 #pragma unroll
-        for (int n = 0; n < NCT; n++)
-#pragma unroll
-            for (int g = 0; g < 8; g++) bm[n][g] = kq < 2 ? (_Float16)q4k_m(hd[n], g) : (_Float16)0.0f;
+        for (int n = 0; n < NCT; n++) bm[n] = q4k_min_frag(hd[n]);
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
@@ -1120,25 +1119,57 @@ QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_r
 struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
+// The lane's two group scales of a half superblock as fp16 pairs: sc = {s_a,
+// s_b / 16}, of = {-1024 s_a, -64 s_b}, where s_a is byte 2 (kq >> 1) of the
+// half's scale word (the group of the lane's low nibbles) and s_b the next
+// byte (the group of its high nibbles); a byte permute puts both under the
+// exponent byte 0x64 (1024 + s, exact) and one packed add removes the 1024.
+QG_DEV void gq_scales(uint32_t S, int kq, qg_half2 &sc, qg_half2 &of) {
+    const uint32_t b = 2u * (uint32_t)(kq >> 1);
+    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, S, b | (4u << 8) | ((b + 1u) << 16) | (4u << 24));
+    const qg_half2 sv = __builtin_bit_cast(qg_half2, u) + qg_half2{(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+    sc = sv * qg_half2{(_Float16)1.0f, (_Float16)0.0625f};
+    of = sv * qg_half2{(_Float16)(-1024.0f), (_Float16)(-64.0f)};
+}
+// 8 Q4_K nibbles of fragment f of a 16-byte qs chunk as s * q in fp16: the
+// nibbles go under the exponent byte 0x64 (1024 + q, or 1024 + 16 q for the
+// high nibbles) and one packed fma per pair applies the scale and removes the
+// offset, exactly (s * q <= 945).
+QG_DEV qg_half8 gq_frag(uint4 c, int f, _Float16 sc, _Float16 of) {
+    uint32_t E;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(E));
+    const uint32_t m = (f & 2) ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t x = (f & 1) ? c.z : c.x, y = (f & 1) ? c.w : c.y;
+    const uint32_t u[4] = {(x & m) | E, ((x >> 8) & m) | E, (y & m) | E, ((y >> 8) & m) | E};
+    const qg_half2 sv = {sc, sc}, ov = {of, of};
+    qg_half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const qg_half2 v = __builtin_elementwise_fma(__builtin_bit_cast(qg_half2, u[i]), sv, ov);
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
 // One half superblock for the first M row tiles: per K step f (4 of them)
 // the two weight fragments, then every row tile's products (fragment f + 1
 // is built while step f's products run); y += d * acc per half, and with the
 // sums (first half) the min term -dmin * (m . X) over the superblock's 8
 // groups.  issue(f) runs after K step f's products are issued: the caller's
 // copies for later steps go out while the matrix cores work.
-template <int M, int NC, typename Issue = NoIssue>
-QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq,
+template <int M, int NC, int MY, typename Issue = NoIssue>
+QG_DEV void gq_chunk(qg_f4 (&y)[MY][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq,
                      Issue issue = Issue{}) {
+    static_assert(M <= MY, "row tiles");
     Q4kHeader hd[NC];
     uint4 qc[NC];
-    uint32_t S[NC];
-    const int sh = 16 * (kq >> 1);  // bit offset of the lane's low-nibble group in the half's scale word
+    qg_half2 sc[NC], of[NC];
 #pragma unroll
     for (int n = 0; n < NC; n++) {
         const uint8_t *row = slot + (16 * n + j) * GQ_ROWB;
         hd[n] = q4k_header(*(const uint4 *)row);
         qc[n] = *(const uint4 *)(row + 16 + 16 * kq);
-        S[n] = h ? hd[n].S[1] : hd[n].S[0];  // the half's 4 group scales (a select: h is a runtime value)
+        gq_scales(h ? hd[n].S[1] : hd[n].S[0], kq, sc[n], of[n]);  // a select: h is a runtime value
     }
     qg_f4 acc[M][NC];
 #pragma unroll
@@ -1149,7 +1180,7 @@ QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, 
     for (int f = 0; f < 4; f++) {
         qg_half8 b[NC];
 #pragma unroll
-        for (int n = 0; n < NC; n++) b[n] = q4k_chunk_frag(qc[n], f, (_Float16)(int)((S[n] >> (sh + 8 * (f >> 1))) & 0xffu));
+        for (int n = 0; n < NC; n++) b[n] = gq_frag(qc[n], f, sc[n][f >> 1], of[n][f >> 1]);
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const qg_half8 a0 = stage_frag128(st, m * 16 + j, 0, 4 * f + kq), a1 = stage_frag128(st, m * 16 + j, 1, 4 * f + kq);
@@ -1169,13 +1200,12 @@ QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, 
 #pragma unroll
             for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(hd[n].d, acc[m][n][i], y[m][n][i]);
     if (ss) {
-        // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group sums
+        // min term: lanes kq = 0 / 1 carry the hi / lo plane of the 8 group
+        // sums, the other lanes zeros (their mins multiply zero)
         const qg_half8 z8 = qg_half8{0, 0, 0, 0, 0, 0, 0, 0};
         qg_half8 bm[NC];
 #pragma unroll
-        for (int n = 0; n < NC; n++)
-#pragma unroll
-            for (int g = 0; g < 8; g++) bm[n][g] = kq < 2 ? (_Float16)q4k_m(hd[n], g) : (_Float16)0.0f;
+        for (int n = 0; n < NC; n++) bm[n] = q4k_min_frag(hd[n]);
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const qg_half8 as = kq < 2 ? ld_frag((const _Float16 *)(ss + ((m * 16 + j) * 2 + kq) * 16)) : z8;
@@ -1191,7 +1221,10 @@ QG_DEV void gq_chunk(qg_f4 (&y)[4][NC], const uint8_t *slot, const uint8_t *st, 
 
 // Item = (group, 64-row tile, 128 F rows); wave w: F rows f0 = 16 w .. +15 of
 // the block, column tile 0 their gate rows, tile 1 their up rows.  Steps are
-// the item's D/128 half superblocks.
+// the item's D/128 half superblocks.  The step loop runs inside one
+// instantiation per row-tile count M, entered once per item, so the
+// accumulators stay in place for the item's steps; the per-lane addresses of
+// the copies are formed once per item and advanced per step.
 template <bool I8>
 __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
@@ -1220,135 +1253,176 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     uint8_t *ring = lds + 2 * IQ_STAGE + 2 * GQ_SUMS + (size_t)wave * 3 * GQ_SLOT;  // this wave's three slots
     // mid row of tile row tr (< nv): the CSR position, shared rows after the 10 nt selections
     auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
-    // stage of step s (item it, half c): the activation chunk, and with a
-    // superblock's first half its group sums
     // tile rows: their tokens (and with the int8 variant their row scales)
     auto set_rows = [&](const PfItem &it, int buf) {
         item_rows(s_src[buf], it, A.row_token, 0, wave, lane);
         if (I8 && wave == 1) dma4_ordered((it.shared ? A.xsc : A.row_sx) + it.base + min(lane, it.nv - 1), s_sx[buf]);
     };
-    auto stage = [&](const PfItem &it, int buf, int c, int s) {
-        if (I8) stage_rows128_i8(lds + (s & 1) * IQ_STAGE, A.xi8, A.D, s_src[buf], c, 16 * it.M, wave, lane);
-        else stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
-        if ((c & 1) == 0 && wave * 32 < 16 * it.M) {
-            const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
-            dma16_ordered(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32 + (size_t)(c >> 1) * 8, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
-        }
-    };
-    auto copy_step = [&](int q, StepPos p) {
-        const PfItem it = R.at(p.k);
+    // Weight copies: piece i = 64 t + lane of a slot is piece p of row r (r <
+    // 16 the gate row f0 + r, else the up row f0 + r - 16): the superblock's
+    // header (p = 0) or 16-byte piece p - 1 of the half's 64 qs bytes.
+    uint32_t w_off[GQ_COPIES], w_h[GQ_COPIES];
+    bool w_up[GQ_COPIES];
+#pragma unroll
+    for (int t = 0; t < GQ_COPIES; t++) {
+        const int i = min(t * 64 + lane, 32 * GQ_PIECES - 1), r = i / GQ_PIECES, p = i - GQ_PIECES * r;
+        w_off[t] = (uint32_t)((r & 15) * A.rb) + (uint32_t)(16 * p);
+        w_h[t] = p == 0 ? 0u : 64u;
+        w_up[t] = r >= 16;
+    }
+    const uint8_t *wp[GQ_COPIES];  // the lane's rows of the item being copied
+    auto set_wp = [&](const PfItem &it) {
         const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
         const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
         const size_t f0 = (size_t)(it.blk * GU_FB + wave * 16) * A.rb;
-        gq_copy(ring + q * GQ_SLOT, bg + f0, bu + f0, A.rb, p.c >> 1, p.c & 1, lane);
+#pragma unroll
+        for (int t = 0; t < GQ_COPIES; t++) wp[t] = (w_up[t] ? bu : bg) + f0 + w_off[t];
+    };
+    auto copy_w = [&](int q, int c) {  // step c of the item being copied into slot q
+        const uint32_t sb = (uint32_t)(c >> 1) * 144u;
+        const bool h = c & 1;
+        static_assert(GQ_COPIES == 3, "three copies under one M0 value");
+        dma16x3_ordered(wp[0] + sb + (h ? w_h[0] : 0u), wp[1] + sb + (h ? w_h[1] : 0u), wp[2] + sb + (h ? w_h[2] : 0u),
+                        ring + q * GQ_SLOT);
+    };
+    // Activation copies of the item being staged: copy i of this wave (tile
+    // rows of copy number q = wave + 8 i) and, for the waves that copy them,
+    // the rows' group sums; step c adds its chunk offset.
+    const uint8_t *sp[4] = {nullptr, nullptr, nullptr, nullptr}, *sump = nullptr;
+    int s_nc = 0;      // this wave's activation copies per step of the item being staged
+    bool s_sum = false; // and whether it copies group sums
+    auto set_sp = [&](const PfItem &it, int buf) {
+        s_nc = I8 ? (4 * it.M - wave + 7) / 8 : it.M;   // copy numbers q = wave + 8 i below 4 M (int8) or 8 M
+        s_sum = wave * 32 < 16 * it.M;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = wave + PF_WAVES * i;
+            if (I8 && 4 * q < 16 * it.M) {
+                const int tr = 4 * q + (lane >> 4), p = (lane >> 3) & 1, c8 = (lane & 7) ^ (tr & 7);
+                sp[i] = (const uint8_t *)A.xi8 + ((size_t)s_src[buf][tr] * 2 + p) * A.D + c8 * 16;
+            } else if (!I8 && 2 * q < 16 * it.M) {
+                const int tr = 2 * q + (lane >> 5), p = (lane >> 4) & 1, c16 = (lane & 15) ^ (tr & 15);
+                sp[i] = (const uint8_t *)(A.xp + ((size_t)s_src[buf][tr] * 2 + p) * A.D + c16 * 8);
+            }
+        }
+        if (s_sum) {
+            const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
+            sump = (const uint8_t *)(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32);
+        }
+    };
+    // the stage of step s (chunk c of the item being staged)
+    auto stage_at = [&](int s, int c) {
+        uint8_t *st = lds + (s & 1) * IQ_STAGE;
+        const size_t co = (size_t)c * (I8 ? 128 : 256);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < s_nc) dma16_ordered(sp[i] + co, st + (wave + PF_WAVES * i) * 1024);
+        if ((c & 1) == 0 && s_sum) dma16_ordered(sump + (size_t)(c >> 1) * 16, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
     };
     // prologue: item 0's rows, its first stage, the weights of steps 0 and 1
     PfItem cur = R.at(0);
     set_rows(cur, 0);
     wait_vmem();
     __syncthreads();
-    stage(cur, 0, 0, 0);
-    StepPos pos{0, 0};
-    copy_step(0, pos);
-    if (1 < steps) copy_step(1, next_pos(pos, NH));
-    qg_f4 y[4][NCT];
+    set_sp(cur, 0);
+    stage_at(0, 0);
+    set_wp(cur);
+    copy_w(0, 0);
+    if (1 < steps) copy_w(1, 1);  // NH >= 2: step 1 is item 0's
+    int s = 0, qc = 0;  // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3 (read by step s - 1)
+    auto run_item = [&](const int k, auto MC) {
+        constexpr int M = decltype(MC)::value;
+        qg_f4 y[M][NCT];
 #pragma unroll
-    for (int m = 0; m < 4; m++)
+        for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    int qc = 0;  // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3 (read by step s - 1)
-    for (int s = 0; s < steps; s++) {
-        const int k = pos.k, c = pos.c, qn = qc == 0 ? 2 : qc - 1;
-        const StepPos p1 = next_pos(pos, NH), p2 = next_pos(p1, NH);
-        if (s + 1 < steps) wait_vmem_but<GQ_COPIES>();
-        else wait_vmem();
-        __syncthreads();
-        if (c == 0) {
-            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
-            // the next item's rows, copied while this item streams (its buffer
-            // held item k - 1's rows, staged long ago)
-            if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
-        }
-        // the next step's stage, then the weights of step s + 2 (in this order:
-        // the wait above relies on it); the fp16 pass issues them between its
-        // first K steps' products
-        auto issue = [&](int f) {
-            if (f == 0 && s + 1 < steps) stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
-            if (f == 1 && s + 2 < steps) copy_step(qn, p2);
-        };
-        if (I8) {
-            issue(0);
-            issue(1);
-        }
-        const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + qc * GQ_SLOT;
-        const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
-        if constexpr (I8) {
-            float sxv[4][4];  // the scales of the lane's rows m 16 + 4 kq + i
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) sxv[m][i] = s_sx[k & 1][m * 16 + 4 * kq + i];
-            switch (cur.M) {  // block-uniform
-            case 1: gq_chunk_i8<1>(y, slot, st, ss, sxv, c & 1, j, kq); break;
-            case 2: gq_chunk_i8<2>(y, slot, st, ss, sxv, c & 1, j, kq); break;
-            case 3: gq_chunk_i8<3>(y, slot, st, ss, sxv, c & 1, j, kq); break;
-            default: gq_chunk_i8<4>(y, slot, st, ss, sxv, c & 1, j, kq); break;
+            for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < NH; c++, s++) {
+            const int qn = qc == 0 ? 2 : qc - 1;
+            if (s + 1 < steps) wait_vmem_but<GQ_COPIES>();
+            else wait_vmem();
+            __syncthreads();
+            if (c == 0) {
+                if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+                // the next item's rows, copied while this item streams (its buffer
+                // held item k - 1's rows, staged long ago)
+                if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
             }
-        } else {
-            switch (cur.M) {  // block-uniform
-            case 1: gq_chunk<1, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
-            case 2: gq_chunk<2, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
-            case 3: gq_chunk<3, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
-            default: gq_chunk<4, NCT>(y, slot, st, ss, c & 1, j, kq, issue); break;
+            // the next step's stage, then the weights of step s + 2 (in this
+            // order: the wait above relies on it); the fp16 pass issues them
+            // between its first K steps' products
+            auto issue = [&](int f) {
+                if (f == 0 && s + 1 < steps) {
+                    if (c == NH - 1) set_sp(R.at(k + 1), (k + 1) & 1);
+                    stage_at(s + 1, c == NH - 1 ? 0 : c + 1);
+                }
+                if (f == 1 && s + 2 < steps) {
+                    if (c == NH - 2) set_wp(R.at(k + 1));
+                    copy_w(qn, c + 2 < NH ? c + 2 : c + 2 - NH);
+                }
+            };
+            const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + qc * GQ_SLOT;
+            const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
+            if constexpr (I8) {
+                issue(0);
+                issue(1);
+                float sxv[4][4];  // the scales of the lane's rows m 16 + 4 kq + i
+#pragma unroll
+                for (int m = 0; m < 4; m++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sxv[m][i] = s_sx[k & 1][m * 16 + 4 * kq + i];
+                gq_chunk_i8<M>(y, slot, st, ss, sxv, c & 1, j, kq);
+            } else {
+                gq_chunk<M, NCT>(y, slot, st, ss, c & 1, j, kq, issue);
             }
+            qc = qc == 2 ? 0 : qc + 1;
         }
-        if (c == NH - 1) {
-            // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
-            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt;
-            const int f = cur.blk * GU_FB + wave * 16 + j, pa = plane_pos(fmt, f);
+        // SwiGLU of the item: tile 0 the gate rows, tile 1 the up rows of F row f
+        const PfItem it = R.at(k);
+        const int fmt = it.shared ? A.sh_down_fmt : A.down_fmt;
+        const int f = it.blk * GU_FB + wave * 16 + j, pa = plane_pos(fmt, f);
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                if (m >= cur.M) break;
+        for (int m = 0; m < M; m++) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tr = m * 16 + 4 * kq + i;
-                    const float ma = qg_swiglu_fast(y[m][0][i], y[m][1][i]);
-                    if (tr < cur.nv) {
-                        _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
-                        const _Float16 ha = (_Float16)ma;
-                        hp[pa] = ha;
-                        hp[F + pa] = (_Float16)(ma - (float)ha);
-                    }
-                    if (fmt == QT_Q4_K) {
-                        // this wave's 16 rows of the 32-row group (lanes of one kq hold all 16 j)
-                        float sp = ma;
-                        sp += __shfl_xor(sp, 1);
-                        sp += __shfl_xor(sp, 2);
-                        sp += __shfl_xor(sp, 4);
-                        sp += __shfl_xor(sp, 8);
-                        if (j == 0) s_gs[wave][tr] = sp;
-                    }
+            for (int i = 0; i < 4; i++) {
+                const int tr = m * 16 + 4 * kq + i;
+                const float ma = qg_swiglu_fast(y[m][0][i], y[m][1][i]);
+                if (tr < it.nv) {
+                    _Float16 *hp = A.midp + (size_t)mrow(it, tr) * 2 * F;
+                    const _Float16 ha = (_Float16)ma;
+                    hp[pa] = ha;
+                    hp[F + pa] = (_Float16)(ma - (float)ha);
+                }
+                if (fmt == QT_Q4_K) {
+                    // this wave's 16 rows of the 32-row group (lanes of one kq hold all 16 j)
+                    float sp2 = ma;
+                    sp2 += __shfl_xor(sp2, 1);
+                    sp2 += __shfl_xor(sp2, 2);
+                    sp2 += __shfl_xor(sp2, 4);
+                    sp2 += __shfl_xor(sp2, 8);
+                    if (j == 0) s_gs[wave][tr] = sp2;
                 }
             }
-            if (fmt == QT_Q4_K) {  // block-uniform
-                __syncthreads();
-                // waves 2i and 2i+1 hold the two halves of 32-row group i of the block
-                if ((wave & 1) == 0 && lane < cur.nv) {
-                    const float sum = s_gs[wave][lane] + s_gs[wave + 1][lane];
-                    _Float16 *sp = A.msp + (size_t)mrow(cur, lane) * 2 * (F / 32) + (cur.blk * GU_FB + wave * 16) / 32;
-                    const _Float16 hs = (_Float16)sum;
-                    sp[0] = hs;
-                    sp[F / 32] = (_Float16)(sum - (float)hs);
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = R.at(k + 1);
         }
-        pos = p1;
-        qc = qc == 2 ? 0 : qc + 1;
+        if (fmt == QT_Q4_K) {  // block-uniform
+            __syncthreads();
+            // waves 2i and 2i+1 hold the two halves of 32-row group i of the block
+            if ((wave & 1) == 0 && lane < it.nv) {
+                const float sum = s_gs[wave][lane] + s_gs[wave + 1][lane];
+                _Float16 *gp = A.msp + (size_t)mrow(it, lane) * 2 * (F / 32) + (it.blk * GU_FB + wave * 16) / 32;
+                const _Float16 hs = (_Float16)sum;
+                gp[0] = hs;
+                gp[F / 32] = (_Float16)(sum - (float)hs);
+            }
+        }
+    };
+    for (int k = 0; k < nitems; k++) {
+        switch (R.at(k).M) {  // block-uniform
+        case 1: run_item(k, std::integral_constant<int, 1>{}); break;
+        case 2: run_item(k, std::integral_constant<int, 2>{}); break;
+        case 3: run_item(k, std::integral_constant<int, 3>{}); break;
+        default: run_item(k, std::integral_constant<int, 4>{}); break;
+        }
     }
 }
 
