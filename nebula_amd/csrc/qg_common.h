@@ -491,8 +491,9 @@ QG_DEV uint32_t iq4_lookup(uint32_t idx) {
     const uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
     const uint32_t sel = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
-    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
-    return (hi & m) | (lo & ~m);
+    // byte i from hi (permute selector 4 + i) where bit 3 of index i is set,
+    // else from lo (selector i)
+    return __builtin_amdgcn_perm(hi, lo, ((idx >> 1) & 0x04040404u) | 0x03020100u);
 }
 
 // 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,

@@ -830,36 +830,16 @@ QG_DEV qg_half8 stage_frag128(const uint8_t *st, int r, int p, int c) {
     return ld_frag((const _Float16 *)(st + (r * 2 + p) * 256 + 16 * (c ^ (r & 15))));
 }
 
-// The wave's copies of step chunk kc (nb blocks) of its 32 consecutive weight
-// rows (row r at w + r * rb): piece i = 6 r + p of the slot is the p-th
-// 16-byte piece from the row's first aligned piece; pieces past the row's
-// last needed one copy that one again into a position no reader uses (so no
-// copy leaves the 16-byte blocks that hold the needed bytes).
-QG_DEV void iq_copy(uint8_t *slot, const uint8_t *w, size_t rb, int kc, int nb, int lane) {
-    const uint8_t *g[IQ_COPIES];
-#pragma unroll
-    for (int t = 0; t < IQ_COPIES; t++) {
-        const int i = t * 64 + lane, r = i / IQ_PIECES, p = i - IQ_PIECES * r;
-        const uintptr_t a = (uintptr_t)(w + (size_t)r * rb) + (uintptr_t)kc * 72;
-        const int delta = (int)(a & 15), np = (delta + 18 * nb + 15) >> 4;
-        g[t] = (const uint8_t *)((a & ~(uintptr_t)15) + 16 * (uintptr_t)min(p, np - 1));
-    }
-    static_assert(IQ_COPIES == 3, "three copies under one M0 value");
-    dma16x3_ordered(g[0], g[1], g[2], slot);
-}
-
 // y[m][n] += d_b * (lut[q] . x) for the nb blocks of a step, weights from the
-// slot (rows 16 n + j of the wave's 32), activations from the stage.
-template <int M>
-QG_DEV void iq_chunk_lds(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t *w, size_t rb, int kc, const uint8_t *st,
-                         int j, int kq, int nb) {
+// slot (row 16 n + j of the wave's 32: its step's bytes start at byte del[n]
+// of its slot row), activations from the stage.
+template <int M, int MY>
+QG_DEV void iq_chunk_lds(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const int (&del)[NCT], const uint8_t *st, int j, int kq,
+                         int nb) {
+    static_assert(M <= MY, "row tiles");
     const uint8_t *rowp[NCT];
 #pragma unroll
-    for (int n = 0; n < NCT; n++) {
-        const int r = 16 * n + j;
-        const int delta = (int)(((uintptr_t)(w + (size_t)r * rb) + (uintptr_t)kc * 72) & 15);
-        rowp[n] = slot + r * IQ_ROWB + delta;
-    }
+    for (int n = 0; n < NCT; n++) rowp[n] = slot + (16 * n + j) * IQ_ROWB + del[n];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         if (b >= nb) break;  // uniform
@@ -886,7 +866,9 @@ QG_DEV void iq_chunk_lds(qg_f4 (&y)[4][NCT], const uint8_t *slot, const uint8_t 
 }
 
 // Item = (group, 64-row tile, 256 D rows); wave w: D rows 32 w .. +31 of the
-// block as two column tiles.  Steps are the item's K chunks of 128.
+// block as two column tiles.  Steps are the item's K chunks of 128.  As in
+// the gate/up kernel, the step loop runs inside one instantiation per row-tile
+// count, and the per-lane copy addresses are formed once per item.
 __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
@@ -920,85 +902,140 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
         return bw + (size_t)(it.blk * DN_DB + wave * 32) * rb;
     };
     auto nblocks = [&](int kc) { return min(4, F / 32 - 4 * kc); };
-    auto stage = [&](const PfItem &it, int buf, int kc, int b) {
-        stage_rows128(lds + b * IQ_STAGE, A.midp, F, s_src[buf], kc, 4 * nblocks(kc), 16 * it.M, wave, lane);
-    };
-    auto copy_step = [&](int q, StepPos p) {
+    // Weight copies: piece i = 64 t + lane of a slot is piece p of the wave's
+    // row r; wrow[t] is that row in the item being copied.
+    int w_p[IQ_COPIES];
+    const uint8_t *wrow[IQ_COPIES];
+#pragma unroll
+    for (int t = 0; t < IQ_COPIES; t++) w_p[t] = (t * 64 + lane) % IQ_PIECES;
+    auto set_wc = [&](const PfItem &it) {
         size_t rb;
-        const uint8_t *w = wave_rows(R.at(p.k), rb);
-        iq_copy(ring + q * IQ_SLOT, w, rb, p.c, nblocks(p.c), lane);
+        const uint8_t *w = wave_rows(it, rb);
+#pragma unroll
+        for (int t = 0; t < IQ_COPIES; t++) wrow[t] = w + (size_t)((t * 64 + lane) / IQ_PIECES) * rb;
+    };
+    // step kc of the item being copied into slot q: piece p of a row is the
+    // p-th 16-byte piece from the row's first aligned one; pieces past its
+    // last needed one copy that one again into a position no reader uses
+    auto copy_w = [&](int q, int kc) {
+        const int nb = nblocks(kc);
+        const uint8_t *g[IQ_COPIES];
+#pragma unroll
+        for (int t = 0; t < IQ_COPIES; t++) {
+            const uintptr_t a = (uintptr_t)wrow[t] + (uintptr_t)kc * 72;
+            const int delta = (int)(a & 15), np = (delta + 18 * nb + 15) >> 4;
+            g[t] = (const uint8_t *)((a & ~(uintptr_t)15) + 16 * (uintptr_t)min(w_p[t], np - 1));
+        }
+        static_assert(IQ_COPIES == 3, "three copies under one M0 value");
+        dma16x3_ordered(g[0], g[1], g[2], ring + q * IQ_SLOT);
+    };
+    // Mid-plane copies of the item being staged: copy i of this wave covers
+    // tile rows 2 q, 2 q + 1 (q = wave + 8 i); the lane's 16-byte chunk c16 is
+    // the same for every i.
+    const uint8_t *sp[4] = {nullptr, nullptr, nullptr, nullptr};
+    int s_nc = 0;
+    const int c16 = (lane & 15) ^ ((2 * wave + (lane >> 5)) & 15);
+    auto set_sp = [&](const PfItem &it, int buf) {
+        s_nc = it.M;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tr = 2 * (wave + PF_WAVES * i) + (lane >> 5), p = (lane >> 4) & 1;
+            if (i < it.M) sp[i] = (const uint8_t *)(A.midp + ((size_t)s_src[buf][tr] * 2 + p) * F);
+        }
+    };
+    auto stage_at = [&](int s, int kc) {
+        uint8_t *st = lds + (s & 1) * IQ_STAGE;
+        const int c = c16 < 4 * nblocks(kc) ? c16 : 0;  // positions past the chunk: no reader uses them
+        const size_t co = ((size_t)kc * IQ_KC + c * 8) * 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < s_nc) dma16_ordered(sp[i] + co, st + (wave + PF_WAVES * i) * 1024);
     };
     PfItem cur = R.at(0);
     set_rows(cur, 0);
     wait_vmem();
     __syncthreads();
-    stage(cur, 0, 0, 0);
-    StepPos pos{0, 0};
-    copy_step(0, pos);
-    if (1 < steps) copy_step(1, next_pos(pos, nkc));
-    qg_f4 y[4][NCT];
-#pragma unroll
-    for (int m = 0; m < 4; m++)
-#pragma unroll
-        for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    set_sp(cur, 0);
+    stage_at(0, 0);
+    set_wc(cur);
+    copy_w(0, 0);
+    if (1 < steps) {
+        if (nkc == 1) set_wc(R.at(1));
+        copy_w(1, nkc == 1 ? 0 : 1);
+    }
     // step s reads slot s % 3; the copies of step s + 2 go to slot (s + 2) % 3,
     // whose reads (step s - 1) are done
-    int qc = 0;
-    for (int s = 0; s < steps; s++) {
-        const int k = pos.k, kc = pos.c, qn = qc == 0 ? 2 : qc - 1;
-        const StepPos p1 = next_pos(pos, nkc), p2 = next_pos(p1, nkc);
-        if (s + 1 < steps) wait_vmem_but<IQ_COPIES>();
-        else wait_vmem();
-        __syncthreads();
-        if (kc == 0) {
-            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
-            // the next item's rows, copied while this item streams
-            if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
+    int s = 0, qc = 0;
+    auto run_item = [&](const int k, auto MC) {
+        constexpr int M = decltype(MC)::value;
+        const PfItem it = R.at(k);
+        // the lane's compute rows 16 n + j: low address bits, for the slot offsets
+        uint32_t rlo[NCT];
+        {
+            size_t rb;
+            const uint8_t *w = wave_rows(it, rb);
+#pragma unroll
+            for (int n = 0; n < NCT; n++) rlo[n] = (uint32_t)(uintptr_t)(w + (size_t)(16 * n + j) * rb);
         }
-        if (s + 1 < steps) {
-            if (p1.k != k) {
-                if (nkc == 1) {  // the rows were copied just above
-                    wait_vmem();
-                    __syncthreads();
-                }
-                stage(R.at(p1.k), p1.k & 1, p1.c, (s + 1) & 1);
-            } else {
-                stage(cur, k & 1, p1.c, (s + 1) & 1);
+        qg_f4 y[M][NCT];
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+            for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kc = 0; kc < nkc; kc++, s++) {
+            const int qn = qc == 0 ? 2 : qc - 1;
+            if (s + 1 < steps) wait_vmem_but<IQ_COPIES>();
+            else wait_vmem();
+            __syncthreads();
+            if (kc == 0) {
+                if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+                // the next item's rows, copied while this item streams
+                if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
             }
-        }
-        if (s + 2 < steps) copy_step(qn, p2);
-        size_t rb;
-        const uint8_t *w = wave_rows(cur, rb);
-        const uint8_t *slot = ring + qc * IQ_SLOT, *st = lds + (s & 1) * IQ_STAGE;
-        switch (cur.M) {  // block-uniform
-        case 1: iq_chunk_lds<1>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
-        case 2: iq_chunk_lds<2>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
-        case 3: iq_chunk_lds<3>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
-        default: iq_chunk_lds<4>(y, slot, w, rb, kc, st, j, kq, nblocks(kc)); break;
-        }
-        if (kc == nkc - 1) {
-            const int d0 = cur.blk * DN_DB + wave * 32;
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                if (m >= cur.M) break;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tr = m * 16 + 4 * kq + i;
-                    if (tr < cur.nv) {
-                        float *o = A.slots + (size_t)s_slot[k & 1][tr] * A.D + d0 + j;
-#pragma unroll
-                        for (int n = 0; n < NCT; n++) o[16 * n] = y[m][n][i];
+            if (s + 1 < steps) {
+                if (kc == nkc - 1) {
+                    if (nkc == 1) {  // the rows were copied just above
+                        wait_vmem();
+                        __syncthreads();
                     }
+                    set_sp(R.at(k + 1), (k + 1) & 1);
+                }
+                stage_at(s + 1, kc + 1 < nkc ? kc + 1 : 0);
+            }
+            if (s + 2 < steps) {
+                // step s + 2 is step kc + 2 of this item or of the next one(s)
+                const int kc2 = (kc + 2) % nkc;
+                if (kc2 == 0) set_wc(R.at(k + (kc + 2) / nkc));  // it starts a later item
+                copy_w(qn, kc2);
+            }
+            int del[NCT];
+#pragma unroll
+            for (int n = 0; n < NCT; n++) del[n] = (int)((rlo[n] + (uint32_t)kc * 72u) & 15u);
+            const uint8_t *slot = ring + qc * IQ_SLOT, *st = lds + (s & 1) * IQ_STAGE;
+            iq_chunk_lds<M>(y, slot, del, st, j, kq, nblocks(kc));
+            qc = qc == 2 ? 0 : qc + 1;
+        }
+        const int d0 = it.blk * DN_DB + wave * 32;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tr = m * 16 + 4 * kq + i;
+                if (tr < it.nv) {
+                    float *o = A.slots + (size_t)s_slot[k & 1][tr] * A.D + d0 + j;
+#pragma unroll
+                    for (int n = 0; n < NCT; n++) o[16 * n] = y[m][n][i];
                 }
             }
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int n = 0; n < NCT; n++) y[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = R.at(k + 1);
         }
-        pos = p1;
-        qc = qc == 2 ? 0 : qc + 1;
+    };
+    for (int k = 0; k < nitems; k++) {
+        switch (R.at(k).M) {  // block-uniform
+        case 1: run_item(k, std::integral_constant<int, 1>{}); break;
+        case 2: run_item(k, std::integral_constant<int, 2>{}); break;
+        case 3: run_item(k, std::integral_constant<int, 3>{}); break;
+        default: run_item(k, std::integral_constant<int, 4>{}); break;
+        }
     }
 }
 
