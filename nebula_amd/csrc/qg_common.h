@@ -492,8 +492,11 @@ QG_DEV uint32_t iq4_lookup(uint32_t idx) {
     const uint32_t sel = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
     // byte i from hi (permute selector 4 + i) where bit 3 of index i is set,
-    // else from lo (selector i)
-    return __builtin_amdgcn_perm(hi, lo, ((idx >> 1) & 0x04040404u) | 0x03020100u);
+    // else from lo (selector i); the identity selector as an opaque register
+    // value makes the mask-and-insert one v_and_or_b32
+    uint32_t I;
+    asm("v_mov_b32 %0, 0x03020100" : "=v"(I));
+    return __builtin_amdgcn_perm(hi, lo, ((idx >> 1) & 0x04040404u) | I);
 }
 
 // 8 nibbles of one byte octet (low or high half) times s -> fp16 fragment,

@@ -9,8 +9,9 @@
 // (bytes 0-7 / 8-15).  Every weight enters as s_g*q (an integer <= 945, exact
 // in fp16), so elements of different groups may share an MFMA; the superblock
 // scale d and the min term dmin*sum_g m_g*X_g are applied in fp32.  IQ4_NL:
-// one MFMA per 32-element block, lane kq takes qs bytes 4kq..4kq+3 (slots in
-// (low, high) nibble pairs per byte), the block scale is applied in fp32.  Activation planes (fp16 hi and lo = x - hi) are
+// one MFMA per 32-element block, lane kq takes qs bytes 4kq..4kq+3 (slots 0..3
+// their low nibbles, 4..7 their high nibbles), the block scale is applied in
+// fp32.  Activation planes (fp16 hi and lo = x - hi) are
 // stored in the matching permuted order (pos_q4k / pos_iq4), so every A
 // fragment is one 16-byte load.
 #pragma once
@@ -24,11 +25,11 @@ QG_DEV int pos_q4k(int e) {
 }
 QG_DEV int qg_perm4(int i) { return ((i & 1) << 1) | ((i & 2) >> 1); }  // 0,2,1,3
 // Plane position of element e (0..31) of an IQ4_NL block: lane kq's 8 slots
-// hold the (low, high) nibble pairs of its qs bytes 4kq..4kq+3 in byte order
-// (element r of byte r and element 16 + r).
+// hold the low nibbles of its qs bytes 4kq..4kq+3 (elements 4kq..4kq+3), then
+// their high nibbles (elements 16 + 4kq..16 + 4kq+3).
 QG_DEV int pos_iq4(int e) {
     const int hi = e >> 4, r = e & 15;
-    return (r >> 2) * 8 + 2 * (r & 3) + hi;
+    return (r >> 2) * 8 + 4 * hi + (r & 3);
 }
 QG_DEV int plane_pos(int fmt, int k) {
     return fmt == QT_IQ4_NL ? (k & ~31) | pos_iq4(k & 31) : (k & ~255) | pos_q4k(k & 255);
@@ -40,19 +41,21 @@ QG_DEV qg_half8 q4k_chunk_frag(uint4 c, int f, _Float16 s) {
     return q4_frag((f & 1) ? make_uint2(c.z, c.w) : make_uint2(c.x, c.y), f >> 1, s);
 }
 
-// 4 IQ4_NL qs bytes -> 8 table values in fp16, slot 2i / 2i+1 = low / high
-// nibble of byte i (pos_iq4's order).  The table bytes (value + 128) are
-// permuted under the exponent byte 0x64 (1024 + value + 128) and 1152 is
-// taken off, exactly.
+// 4 IQ4_NL qs bytes -> 8 table values in fp16, slots 0..3 / 4..7 = low /
+// high nibbles of bytes 0..3 (pos_iq4's order).  The table bytes (value +
+// 128) are permuted in pairs under the exponent byte 0x64 (1024 + value +
+// 128) and 1152 is taken off, exactly.
 QG_DEV qg_half8 iq4_frag4(uint32_t q) {
     const uint32_t lo = iq4_lookup(q & 0x0F0F0F0Fu), hi = iq4_lookup((q >> 4) & 0x0F0F0F0Fu);  // lut + 128 as bytes
+    uint32_t X;
+    asm("v_mov_b32 %0, 0x64646464" : "=v"(X));
+    const uint32_t u[4] = {__builtin_amdgcn_perm(X, lo, 0x04010400u), __builtin_amdgcn_perm(X, lo, 0x04030402u),
+                           __builtin_amdgcn_perm(X, hi, 0x04010400u), __builtin_amdgcn_perm(X, hi, 0x04030402u)};
     const qg_half2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
     qg_half8 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t sel = (uint32_t)i | (0x0Cu << 8) | ((uint32_t)(4 + i) << 16) | (0x0Cu << 24);
-        const uint32_t u = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
-        const qg_half2 v = __builtin_bit_cast(qg_half2, u) + off;
+        const qg_half2 v = __builtin_bit_cast(qg_half2, u[i]) + off;
         r[2 * i] = v[0];
         r[2 * i + 1] = v[1];
     }
