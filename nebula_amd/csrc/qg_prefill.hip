@@ -1041,10 +1041,14 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
 
 // ---- gate/up: the Q4_K weights through each wave's own shared-memory ring ----
 // A step is half a superblock (128 K elements, groups 4h .. 4h+3): per weight
-// row the superblock's 16-byte header and the half's 64 qs bytes, 5 pieces,
-// copied like the IQ4_NL rows (160 pieces in 3 copies; lanes past them copy
-// the last piece again into the slot's padding).  The 8 group sums of a
-// superblock are staged with its first half, into their own double buffer.
+// row the superblock's 16-byte header (piece 0) and the half's 64 qs bytes
+// (pieces 1..4).  The sparse pass keeps a slot row-major (row r's pieces at
+// 80 r, 160 pieces in 3 copies, so each copy's lanes read whole runs of few
+// rows; lanes past them copy the last piece again into the slot's padding);
+// the dense pass keeps its slots piece-major (piece p of row r at p * 16 x
+// rows + 16 r: one row address per lane serves every copy).  The 8 group
+// sums of a superblock are staged with its first half, into their own double
+// buffer.
 constexpr int GQ_PIECES = 5;
 constexpr int GQ_ROWB = GQ_PIECES * 16;
 constexpr int GQ_COPIES = 3;
@@ -1139,20 +1143,6 @@ QG_DEV void gq_chunk_i8(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const uint8_t 
     }
 }
 
-// Row r of the wave's 32 (r < 16: gate row f0 + r, else up row f0 + r - 16),
-// superblock sb, half h: piece 0 the header, pieces 1..4 the half's qs bytes.
-QG_DEV void gq_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_row0, size_t rb, int sb, int h, int lane) {
-    const uint8_t *g[GQ_COPIES];
-#pragma unroll
-    for (int t = 0; t < GQ_COPIES; t++) {
-        const int i = min(t * 64 + lane, 32 * GQ_PIECES - 1), r = i / GQ_PIECES, p = i - GQ_PIECES * r;
-        const uint8_t *row = (r < 16 ? gate_row0 : up_row0) + (size_t)(r & 15) * rb + (size_t)sb * 144;
-        g[t] = row + (p == 0 ? 0 : 16 + 64 * h + 16 * (p - 1));
-    }
-    static_assert(GQ_COPIES == 3, "three copies under one M0 value");
-    dma16x3_ordered(g[0], g[1], g[2], slot);
-}
-
 struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
@@ -1193,8 +1183,10 @@ QG_DEV qg_half8 gq_frag(uint4 c, int f, _Float16 sc, _Float16 of) {
 // is built while step f's products run); y += d * acc per half, and with the
 // sums (first half) the min term -dmin * (m . X) over the superblock's 8
 // groups.  issue(f) runs after K step f's products are issued: the caller's
-// copies for later steps go out while the matrix cores work.
-template <int M, int NC, int MY, typename Issue = NoIssue>
+// copies for later steps go out while the matrix cores work.  Row r of the
+// slot starts at RS r, its piece p at PS p from there; column tile n is rows
+// 16 n .. 16 n + 15.
+template <int M, int NC, int RS, int PS, int MY, typename Issue = NoIssue>
 QG_DEV void gq_chunk(qg_f4 (&y)[MY][NC], const uint8_t *slot, const uint8_t *st, const uint8_t *ss, int h, int j, int kq,
                      Issue issue = Issue{}) {
     static_assert(M <= MY, "row tiles");
@@ -1203,9 +1195,9 @@ QG_DEV void gq_chunk(qg_f4 (&y)[MY][NC], const uint8_t *slot, const uint8_t *st,
     qg_half2 sc[NC], of[NC];
 #pragma unroll
     for (int n = 0; n < NC; n++) {
-        const uint8_t *row = slot + (16 * n + j) * GQ_ROWB;
+        const uint8_t *row = slot + (16 * n + j) * RS;
         hd[n] = q4k_header(*(const uint4 *)row);
-        qc[n] = *(const uint4 *)(row + 16 + 16 * kq);
+        qc[n] = *(const uint4 *)(row + (1 + kq) * PS);
         gq_scales(h ? hd[n].S[1] : hd[n].S[0], kq, sc[n], of[n]);  // a select: h is a runtime value
     }
     qg_f4 acc[M][NC];
@@ -1297,7 +1289,8 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     };
     // Weight copies: piece i = 64 t + lane of a slot is piece p of row r (r <
     // 16 the gate row f0 + r, else the up row f0 + r - 16): the superblock's
-    // header (p = 0) or 16-byte piece p - 1 of the half's 64 qs bytes.
+    // header (p = 0) or 16-byte piece p - 1 of the half's 64 qs bytes, at
+    // 16 p + 64 h from the superblock.
     uint32_t w_off[GQ_COPIES], w_h[GQ_COPIES];
     bool w_up[GQ_COPIES];
 #pragma unroll
@@ -1410,7 +1403,7 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
                     for (int i = 0; i < 4; i++) sxv[m][i] = s_sx[k & 1][m * 16 + 4 * kq + i];
                 gq_chunk_i8<M>(y, slot, st, ss, sxv, c & 1, j, kq);
             } else {
-                gq_chunk<M, NCT>(y, slot, st, ss, c & 1, j, kq, issue);
+                gq_chunk<M, NCT, GQ_ROWB, 16>(y, slot, st, ss, c & 1, j, kq, issue);
             }
             qc = qc == 2 ? 0 : qc + 1;
         }
@@ -1468,24 +1461,15 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
 // tiles (pair p: gate and up rows f0 + 16 p .. +15), so a tile's activations
 // are staged half as often as with 128-row items and each step's fixed
 // costs (barrier, copy issue) cover twice the weights.  The wave's 64 weight
-// rows of a step (5 pieces each, 320 pieces in 5 copies; slot row 32 p + 16 u
-// + r: pair p, gate (u = 0) or up, row r) go to one of two slots of its ring,
-// copied one step ahead; its 32 rows are one 32-row group of a Q4_K down
+// rows of a step (slot row 32 p + 16 u + r: pair p, gate (u = 0) or up, row
+// r) go piece-major to one of two slots of its ring, copy t taking piece t of
+// every row, one step ahead; its 32 rows are one 32-row group of a Q4_K down
 // format, whose sums it forms alone.
 constexpr int GW_FB = 256;
 constexpr int GW_COPIES = 5;
 constexpr int GW_SLOT = GW_COPIES * 64 * 16;
 constexpr int PF_GW_LDS = 2 * IQ_STAGE + 2 * GQ_SUMS + PF_WAVES * 2 * GW_SLOT;
-static_assert(64 * GQ_PIECES == GW_COPIES * 64, "the copies cover the slot");
-
-QG_DEV void gw_copy(uint8_t *slot, const uint8_t *gate_row0, const uint8_t *up_row0, size_t rb, int sb, int h, int lane) {
-#pragma unroll
-    for (int t = 0; t < GW_COPIES; t++) {
-        const int i = t * 64 + lane, r = i / GQ_PIECES, p = i - GQ_PIECES * r;
-        const uint8_t *row = ((r & 16) ? up_row0 : gate_row0) + (size_t)(16 * (r >> 5) + (r & 15)) * rb + (size_t)sb * 144;
-        dma16_ordered(row + (p == 0 ? 0 : 16 + 64 * h + 16 * (p - 1)), slot + t * 1024);
-    }
-}
+static_assert(GQ_PIECES == GW_COPIES, "one copy per piece");
 
 __global__ __launch_bounds__(512, 1) void pf_gateup_w_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
@@ -1511,99 +1495,127 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_w_kernel(GuArgs A) {
     uint8_t *sums = lds + 2 * IQ_STAGE;                                         // two superblock sum buffers
     uint8_t *ring = lds + 2 * IQ_STAGE + 2 * GQ_SUMS + (size_t)wave * 2 * GW_SLOT;  // this wave's two slots
     auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
-    auto stage = [&](const PfItem &it, int buf, int c, int s) {
-        stage_rows128(lds + (s & 1) * IQ_STAGE, A.xp, A.D, s_src[buf], c, 16, 16 * it.M, wave, lane);
-        if ((c & 1) == 0 && wave * 32 < 16 * it.M) {
+    // Weight copies: lane l takes slot row l (pair l / 32, the up rows for
+    // bit 4); copy t takes piece t of every row, at 16 t + 64 h from the
+    // superblock (the header, t = 0, at 0).
+    const uint8_t *wp = nullptr;  // the lane's row in the item being copied
+    auto set_wp = [&](const PfItem &it) {
+        const uint8_t *b = (lane & 16) ? (it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb)
+                                       : (it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb);
+        wp = b + (size_t)(it.blk * GW_FB + wave * 32 + 16 * (lane >> 5) + (lane & 15)) * A.rb;
+    };
+    auto copy_w = [&](int q, int c) {  // step c of the item being copied into slot q
+        const uint8_t *x = wp + (size_t)(c >> 1) * 144;
+        const uint32_t hh = (c & 1) ? 64u : 0u;
+#pragma unroll
+        for (int t = 0; t < GW_COPIES; t++) dma16_ordered(x + (t == 0 ? 0u : 16u * t + hh), ring + q * GW_SLOT + t * 1024);
+    };
+    // activation copies of the item being staged (as in pf_gateup_kernel)
+    const uint8_t *sp[4] = {nullptr, nullptr, nullptr, nullptr}, *sump = nullptr;
+    int s_nc = 0;
+    bool s_sum = false;
+    auto set_sp = [&](const PfItem &it, int buf) {
+        s_nc = it.M;
+        s_sum = wave * 32 < 16 * it.M;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = wave + PF_WAVES * i, tr = 2 * q + (lane >> 5), p = (lane >> 4) & 1, c16 = (lane & 15) ^ (tr & 15);
+            if (i < it.M) sp[i] = (const uint8_t *)(A.xp + ((size_t)s_src[buf][tr] * 2 + p) * A.D + c16 * 8);
+        }
+        if (s_sum) {
             const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
-            dma16_ordered(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32 + (size_t)(c >> 1) * 8, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
+            sump = (const uint8_t *)(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32);
         }
     };
-    auto copy_step = [&](int q, StepPos p) {
-        const PfItem it = R.at(p.k);
-        const uint8_t *bg = it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb;
-        const uint8_t *bu = it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb;
-        const size_t f0 = (size_t)(it.blk * GW_FB + wave * 32) * A.rb;
-        gw_copy(ring + q * GW_SLOT, bg + f0, bu + f0, A.rb, p.c >> 1, p.c & 1, lane);
+    auto stage_at = [&](int s, int c) {
+        uint8_t *st = lds + (s & 1) * IQ_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < s_nc) dma16_ordered(sp[i] + (size_t)c * 256, st + (wave + PF_WAVES * i) * 1024);
+        if ((c & 1) == 0 && s_sum) dma16_ordered(sump + (size_t)(c >> 1) * 16, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
     };
     // prologue: item 0's rows, its first stage and the weights of step 0
     PfItem cur = R.at(0);
     item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
     wait_vmem();
     __syncthreads();
-    stage(cur, 0, 0, 0);
-    StepPos pos{0, 0};
-    copy_step(0, pos);
-    qg_f4 y0[4][2], y1[4][2];   // pair 0, pair 1: [row tile][gate, up]
+    set_sp(cur, 0);
+    stage_at(0, 0);
+    set_wp(cur);
+    copy_w(0, 0);
+    int s = 0;
+    auto run_item = [&](const int k, auto MC) {
+        constexpr int M = decltype(MC)::value;
+        qg_f4 y0[M][2], y1[M][2];   // pair 0, pair 1: [row tile][gate, up]
 #pragma unroll
-    for (int m = 0; m < 4; m++)
+        for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s = 0; s < steps; s++) {
-        const int k = pos.k, c = pos.c;
-        const StepPos p1 = next_pos(pos, NH);
-        wait_vmem();  // this step's stage and weights (and every earlier copy)
-        __syncthreads();
-        if (c == 0) {
-            if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
-            if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+            for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < NH; c++, s++) {
+            wait_vmem();  // this step's stage and weights (and every earlier copy)
+            __syncthreads();
+            if (c == 0) {
+                if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
+                if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
+            }
+            if (s + 1 < steps) {
+                if (c == NH - 1) {
+                    set_sp(R.at(k + 1), (k + 1) & 1);
+                    set_wp(R.at(k + 1));
+                }
+                stage_at(s + 1, c + 1 < NH ? c + 1 : 0);
+                copy_w((s + 1) & 1, c + 1 < NH ? c + 1 : 0);  // slot (s + 1) % 2 was read by step s - 1
+            }
+            const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + (s & 1) * GW_SLOT;
+            const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
+            gq_chunk<M, 2, 16, 1024>(y0, slot, st, ss, c & 1, j, kq);
+            __builtin_amdgcn_sched_barrier(0);
+            gq_chunk<M, 2, 16, 1024>(y1, slot + 32 * 16, st, ss, c & 1, j, kq);
         }
-        if (s + 1 < steps) {
-            stage(p1.k != k ? R.at(p1.k) : cur, p1.k & 1, p1.c, s + 1);
-            copy_step((s + 1) & 1, p1);  // slot (s + 1) % 2 was read by step s - 1
-        }
-        const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + (s & 1) * GW_SLOT;
-        const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
-        const uint8_t *slot1 = slot + 32 * GQ_ROWB;
-        switch (cur.M) {  // block-uniform
-        case 1: gq_chunk<1, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<1, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
-        case 2: gq_chunk<2, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<2, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
-        case 3: gq_chunk<3, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<3, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
-        default: gq_chunk<4, 2>(y0, slot, st, ss, c & 1, j, kq); __builtin_amdgcn_sched_barrier(0); gq_chunk<4, 2>(y1, slot1, st, ss, c & 1, j, kq); break;
-        }
-        if (c == NH - 1) {
-            // SwiGLU: pair t, F row f0 + 16 t + j
-            const int fmt = cur.shared ? A.sh_down_fmt : A.down_fmt, f0 = cur.blk * GW_FB + wave * 32;
+        // SwiGLU: pair t, F row f0 + 16 t + j
+        const PfItem it = R.at(k);
+        const int fmt = it.shared ? A.sh_down_fmt : A.down_fmt, f0 = it.blk * GW_FB + wave * 32;
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                if (m >= cur.M) break;
+        for (int m = 0; m < M; m++) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tr = m * 16 + 4 * kq + i;
-                    float sp = 0.0f;
+            for (int i = 0; i < 4; i++) {
+                const int tr = m * 16 + 4 * kq + i;
+                float sp2 = 0.0f;
 #pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const float ma = t ? qg_swiglu_fast(y1[m][0][i], y1[m][1][i]) : qg_swiglu_fast(y0[m][0][i], y0[m][1][i]);
-                        if (tr < cur.nv) {
-                            const int pa = plane_pos(fmt, f0 + 16 * t + j);
-                            _Float16 *hp = A.midp + (size_t)mrow(cur, tr) * 2 * F;
-                            const _Float16 ha = (_Float16)ma;
-                            hp[pa] = ha;
-                            hp[F + pa] = (_Float16)(ma - (float)ha);
-                        }
-                        sp += ma;
+                for (int t = 0; t < 2; t++) {
+                    const float ma = t ? qg_swiglu_fast(y1[m][0][i], y1[m][1][i]) : qg_swiglu_fast(y0[m][0][i], y0[m][1][i]);
+                    if (tr < it.nv) {
+                        const int pa = plane_pos(fmt, f0 + 16 * t + j);
+                        _Float16 *hp = A.midp + (size_t)mrow(it, tr) * 2 * F;
+                        const _Float16 ha = (_Float16)ma;
+                        hp[pa] = ha;
+                        hp[F + pa] = (_Float16)(ma - (float)ha);
                     }
-                    if (fmt == QT_Q4_K) {
-                        // the wave's 32 rows are one group: sum over the 16 j (lanes of one kq)
-                        sp += __shfl_xor(sp, 1);
-                        sp += __shfl_xor(sp, 2);
-                        sp += __shfl_xor(sp, 4);
-                        sp += __shfl_xor(sp, 8);
-                        if (j == 0 && tr < cur.nv) {
-                            _Float16 *spp = A.msp + (size_t)mrow(cur, tr) * 2 * (F / 32) + f0 / 32;
-                            const _Float16 hs = (_Float16)sp;
-                            spp[0] = hs;
-                            spp[F / 32] = (_Float16)(sp - (float)hs);
-                        }
+                    sp2 += ma;
+                }
+                if (fmt == QT_Q4_K) {
+                    // the wave's 32 rows are one group: sum over the 16 j (lanes of one kq)
+                    sp2 += __shfl_xor(sp2, 1);
+                    sp2 += __shfl_xor(sp2, 2);
+                    sp2 += __shfl_xor(sp2, 4);
+                    sp2 += __shfl_xor(sp2, 8);
+                    if (j == 0 && tr < it.nv) {
+                        _Float16 *gp = A.msp + (size_t)mrow(it, tr) * 2 * (F / 32) + f0 / 32;
+                        const _Float16 hs = (_Float16)sp2;
+                        gp[0] = hs;
+                        gp[F / 32] = (_Float16)(sp2 - (float)hs);
                     }
                 }
             }
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (s + 1 < steps) cur = R.at(k + 1);
         }
-        pos = p1;
+    };
+    for (int k = 0; k < nitems; k++) {
+        switch (R.at(k).M) {  // block-uniform
+        case 1: run_item(k, std::integral_constant<int, 1>{}); break;
+        case 2: run_item(k, std::integral_constant<int, 2>{}); break;
+        case 3: run_item(k, std::integral_constant<int, 3>{}); break;
+        default: run_item(k, std::integral_constant<int, 4>{}); break;
+        }
     }
 }
 
