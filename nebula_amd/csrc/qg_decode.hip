@@ -465,7 +465,6 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     copy_item(i0, 0);
     int cur = -1;
     qg_half8 af[2][8], sf[2];
-    const int gA = 2 * (kq >> 1), gB = gA + 4;
     for (int k = 0; i0 + k < i1; k++) {
         const int item = i0 + k, ti = item / RBK - T0, rb = item % RBK, b = k & 1;
         const int e = s_te[ti][0], n = s_te[ti][1];
@@ -498,11 +497,14 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
             for (int sb = 0; sb < 2; sb++) {
                 const Q4kHeader h = q4k_header(piece(9 * sb));
                 const uint4 ch0 = piece(9 * sb + 1 + kq), ch1 = piece(9 * sb + 5 + kq);
+                qg_half2 scA, ofA, scB, ofB;  // scales of groups gA, gA + 1 and gB, gB + 1
+                gq_scales(h.S[0], kq, scA, ofA);
+                gq_scales(h.S[1], kq, scB, ofB);
                 qg_f4 p0 = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, p1 = p0, mm = p0;
 #pragma unroll
                 for (int f = 0; f < 4; f++) {
-                    p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][f], q4k_chunk_frag(ch0, f, q4k_sh(h, gA + (f >> 1))), p0, 0, 0, 0);
-                    p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][4 + f], q4k_chunk_frag(ch1, f, q4k_sh(h, gB + (f >> 1))), p1, 0, 0, 0);
+                    p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][f], gq_frag(ch0, f, scA[f >> 1], ofA[f >> 1]), p0, 0, 0, 0);
+                    p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb][4 + f], gq_frag(ch1, f, scB[f >> 1], ofB[f >> 1]), p1, 0, 0, 0);
                 }
                 mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf[sb], q4k_min_frag(h), mm, 0, 0, 0);
 #pragma unroll
@@ -674,18 +676,20 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
         // the min-term product takes its 8 group sums from lanes kq = 0; the
         // other lanes read zeros
         const _Float16 *ap = act + (size_t)r * LY.arow + kq * 8, *sp = kq ? (const _Float16 *)s_zero : acts + (size_t)r * LY.srow;
-        const int gA = 2 * (kq >> 1), gB = gA + 4;
         qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int sb = 0; sb < NSB; sb++) {
             const Q4kHeader h = q4k_header(hd[sb]);
+            qg_half2 scA, ofA, scB, ofB;  // scales of groups gA, gA + 1 and gB, gB + 1
+            gq_scales(h.S[0], kq, scA, ofA);
+            gq_scales(h.S[1], kq, scB, ofB);
             qg_f4 p0 = qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, p1 = p0, mm = p0;
 #pragma unroll
             for (int f = 0; f < 4; f++) {
                 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + f * 32),
-                                                            q4k_chunk_frag(c0[sb], f, q4k_sh(h, gA + (f >> 1))), p0, 0, 0, 0);
+                                                            gq_frag(c0[sb], f, scA[f >> 1], ofA[f >> 1]), p0, 0, 0, 0);
                 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(ap + sb * 256 + (4 + f) * 32),
-                                                            q4k_chunk_frag(c1[sb], f, q4k_sh(h, gB + (f >> 1))), p1, 0, 0, 0);
+                                                            gq_frag(c1[sb], f, scB[f >> 1], ofB[f >> 1]), p1, 0, 0, 0);
             }
             mm = __builtin_amdgcn_mfma_f32_16x16x32_f16(ld_frag(sp + sb * 8), q4k_min_frag(h), mm, 0, 0, 0);
 #pragma unroll
@@ -756,14 +760,16 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
             const uint8_t *p = wr + sb * 144;
             const Q4kHeader h = q4k_header(*(const uint4 *)p);
             const uint4 ca = *(const uint4 *)(p + 16 + 16 * kq), cb = *(const uint4 *)(p + 16 + 16 * (kq + 4));
-            const int gA = 2 * (kq >> 1), gB = gA + 4;
+            qg_half2 scA, ofA, scB, ofB;  // scales of groups 2 (kq / 2) + {0, 1} and 4 + the same
+            gq_scales(h.S[0], kq, scA, ofA);
+            gq_scales(h.S[1], kq, scB, ofB);
             qg_f4 acc = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int f = 0; f < 4; f++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[f], q4k_chunk_frag(ca, f, (_Float16)q4k_s(h, gA + (f >> 1))), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[f], gq_frag(ca, f, scA[f >> 1], ofA[f >> 1]), acc, 0, 0, 0);
 #pragma unroll
             for (int f = 0; f < 4; f++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[4 + f], q4k_chunk_frag(cb, f, (_Float16)q4k_s(h, gB + (f >> 1))), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[4 + f], gq_frag(cb, f, scB[f >> 1], ofB[f >> 1]), acc, 0, 0, 0);
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++) {
                 // group sums of mid: 4 partial sums of 8 rows per 32-group
@@ -1060,14 +1066,16 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
                     const uint8_t *p = wb + sb * 144;
                     const Q4kHeader h = q4k_header(*(const uint4 *)p);
                     const uint4 ca = *(const uint4 *)(p + 16 + 16 * kq), cb = *(const uint4 *)(p + 16 + 16 * (kq + 4));
-                    const int gA = 2 * (kq >> 1), gB = gA + 4;
+                    qg_half2 scA, ofA, scB, ofB;  // scales of groups 2 (kq / 2) + {0, 1} and 4 + the same
+                    gq_scales(h.S[0], kq, scA, ofA);
+                    gq_scales(h.S[1], kq, scB, ofB);
                     qg_f4 acc = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int f = 0; f < 4; f++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + f], q4k_chunk_frag(ca, f, (_Float16)q4k_s(h, gA + (f >> 1))), acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + f], gq_frag(ca, f, scA[f >> 1], ofA[f >> 1]), acc, 0, 0, 0);
 #pragma unroll
                     for (int f = 0; f < 4; f++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + 4 + f], q4k_chunk_frag(cb, f, (_Float16)q4k_s(h, gB + (f >> 1))), acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[sb * 8 + 4 + f], gq_frag(cb, f, scB[f >> 1], ofB[f >> 1]), acc, 0, 0, 0);
                     float M = 0.0f;
 #pragma unroll
                     for (int g = 0; g < 8; g++) M = __builtin_fmaf((float)q4k_m(h, g), xg[sb * 8 + g], M);

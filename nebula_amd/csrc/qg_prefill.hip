@@ -1146,38 +1146,6 @@ QG_DEV void gq_chunk_i8(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const uint8_t 
 struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
-// The lane's two group scales of a half superblock as fp16 pairs: sc = {s_a,
-// s_b / 16}, of = {-1024 s_a, -64 s_b}, where s_a is byte 2 (kq >> 1) of the
-// half's scale word (the group of the lane's low nibbles) and s_b the next
-// byte (the group of its high nibbles); a byte permute puts both under the
-// exponent byte 0x64 (1024 + s, exact) and one packed add removes the 1024.
-QG_DEV void gq_scales(uint32_t S, int kq, qg_half2 &sc, qg_half2 &of) {
-    const uint32_t b = 2u * (uint32_t)(kq >> 1);
-    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, S, b | (4u << 8) | ((b + 1u) << 16) | (4u << 24));
-    const qg_half2 sv = __builtin_bit_cast(qg_half2, u) + qg_half2{(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
-    sc = sv * qg_half2{(_Float16)1.0f, (_Float16)0.0625f};
-    of = sv * qg_half2{(_Float16)(-1024.0f), (_Float16)(-64.0f)};
-}
-// 8 Q4_K nibbles of fragment f of a 16-byte qs chunk as s * q in fp16: the
-// nibbles go under the exponent byte 0x64 (1024 + q, or 1024 + 16 q for the
-// high nibbles) and one packed fma per pair applies the scale and removes the
-// offset, exactly (s * q <= 945).
-QG_DEV qg_half8 gq_frag(uint4 c, int f, _Float16 sc, _Float16 of) {
-    uint32_t E;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(E));
-    const uint32_t m = (f & 2) ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t x = (f & 1) ? c.z : c.x, y = (f & 1) ? c.w : c.y;
-    const uint32_t u[4] = {(x & m) | E, ((x >> 8) & m) | E, (y & m) | E, ((y >> 8) & m) | E};
-    const qg_half2 sv = {sc, sc}, ov = {of, of};
-    qg_half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const qg_half2 v = __builtin_elementwise_fma(__builtin_bit_cast(qg_half2, u[i]), sv, ov);
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
-    }
-    return r;
-}
 // One half superblock for the first M row tiles: per K step f (4 of them)
 // the two weight fragments, then every row tile's products (fragment f + 1
 // is built while step f's products run); y += d * acc per half, and with the
