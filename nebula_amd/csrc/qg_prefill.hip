@@ -511,57 +511,6 @@ QG_DEV void q4_chunk(qg_f4 (&y)[4][NCT], const Q4Ops &o, const uint8_t *st, cons
     }
 }
 
-// IQ4_NL operands of one K chunk (8 blocks) for the wave's column tiles: the
-// block scale and the lane's 4 qs bytes per block and tile (the blocks are 18
-// bytes, 2-byte aligned).
-// Blocks past the chunk's nb load block 0 again, so every chunk issues the
-// same number of loads.
-// Vector-memory instructions of one iq_load, counted low: the compiler may
-// fuse a block's two 2-byte qs loads into one 4-byte load, never fewer than
-// one load per block scale and one per qs word (waiting for at most this many
-// outstanding operations is then at least as strict as intended).
-constexpr int IQ_LOADS = 2 * 8 * NCT;
-struct IqOps { uint32_t q[NCT][8], d[NCT][4]; };   // d: the 8 fp16 block scales, two per word
-QG_DEV void iq_load(IqOps &o, const uint8_t *const *wrow, int kc, int nb, int kq) {
-#pragma unroll
-    for (int n = 0; n < NCT; n++)
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const uint16_t *p16 = (const uint16_t *)(wrow[n] + (size_t)(kc * 8 + (b < nb ? b : 0)) * 18);
-            const uint32_t d = p16[0];
-            if (b & 1) o.d[n][b >> 1] |= d << 16;
-            else o.d[n][b >> 1] = d;
-            o.q[n][b] = (uint32_t)p16[1 + 2 * kq] | ((uint32_t)p16[2 + 2 * kq] << 16);
-        }
-}
-
-// y[m][n] += d_b * (lut[q] . x) for the nb blocks of one K chunk.
-QG_DEV void iq_chunk(qg_f4 (&y)[4][NCT], const IqOps &o, const uint8_t *st, int j, int kq, int nb, int M) {
-#pragma unroll
-    for (int b = 0; b < 8; b++) {
-        if (b >= nb) break;  // uniform
-        qg_half8 bf[NCT];
-#pragma unroll
-        for (int n = 0; n < NCT; n++) bf[n] = iq4_frag4(o.q[n][b]);
-        float d[NCT];
-#pragma unroll
-        for (int n = 0; n < NCT; n++) d[n] = qg_half_u16((o.d[n][b >> 1] >> (16 * (b & 1))) & 0xffffu);
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            if (m < M) {  // uniform
-                const qg_half8 a0 = stage_frag(st, m * 16 + j, 0, 4 * b + kq), a1 = stage_frag(st, m * 16 + j, 1, 4 * b + kq);
-#pragma unroll
-                for (int n = 0; n < NCT; n++) {
-                    qg_f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[n], qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[n], acc, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
-                }
-            }
-        }
-    }
-}
-
 // Items of a persistent launch, XCD-aware: workgroup b runs on XCD b % 8
 // (round-robin dispatch), and XCD x takes the contiguous range of items
 // [x*C, (x+1)*C), C = ceil(total/8), so that the items running together on
@@ -671,10 +620,9 @@ struct DnArgs {
     float *slots;                    // [rows][D]: slot t*10+k, shared rows at nt*10+t
 };
 
-// Item = (group, 64-row tile, 256 D rows); wave w: D rows 32 w .. +31 of the
-// block as two column tiles.  Steps are the item's K chunks of 256 (F / 256
-// superblocks for Q4_K, 8 blocks per chunk for IQ4_NL).
-template <int FMT>
+// Q4_K down.  Item = (group, 64-row tile, 256 D rows); wave w: D rows 32 w ..
+// +31 of the block as two column tiles, their weights in registers loaded two
+// steps ahead.  Steps are the item's K chunks of 256 (F / 256 superblocks).
 __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     uint8_t *lds = (uint8_t *)s_dyn;
@@ -708,21 +656,15 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
 #pragma unroll
         for (int n = 0; n < NCT; n++) wrow[n] = bw + (size_t)(d + 16 * n) * rb;
     };
-    auto nblocks = [&](int kc) { return min(8, (F - kc * KC) / 32); };
     auto stage = [&](const PfItem &it, int buf, int kc, int b) {
-        if (FMT == QT_Q4_K)
-            stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src[buf], kc, 32,
-                       16 * it.M, wave, lane);
-        else
-            stage_rows(lds + b * STAGE_BYTES, nullptr, A.midp, F, nullptr, 0, s_src[buf], kc, 4 * nblocks(kc), 16 * it.M, wave,
-                       lane);
+        stage_rows(lds + b * STAGE_BYTES, lds + 2 * STAGE_BYTES + b * SUMS_BYTES, A.midp, F, A.msp, F32, s_src[buf], kc, 32,
+                   16 * it.M, wave, lane);
     };
-    using Ops = typename std::conditional<FMT == QT_Q4_K, Q4Ops, IqOps>::type;
+    using Ops = Q4Ops;
     const uint8_t *wrow[NCT];
     auto load_step = [&](Ops &o, StepPos p) {
         weight_rows(R.at(p.k), wrow);
-        if constexpr (FMT == QT_Q4_K) q4_load(o, wrow, p.c, kq);
-        else iq_load(o, wrow, p.c, nblocks(p.c), kq);
+        q4_load(o, wrow, p.c, kq);
     };
     PfItem cur = R.at(0);
     set_rows(cur, 0);
@@ -741,7 +683,7 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     auto step = [&](int s, const Ops &wc, Ops &wn) {
         const int k = pos.k, kc = pos.c;
         const StepPos p1 = next_pos(pos, nkc), p2 = next_pos(p1, nkc);
-        if (s + 1 < steps) wait_vmem_but<FMT == QT_Q4_K ? Q4_LOADS : IQ_LOADS>();
+        if (s + 1 < steps) wait_vmem_but<Q4_LOADS>();
         else wait_vmem();
         __syncthreads();
         if (kc == 0) {
@@ -761,13 +703,8 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
             }
         }
         if (s + 2 < steps) load_step(wn, p2);
-        const uint8_t *st = lds + (s & 1) * STAGE_BYTES;
-        if constexpr (FMT == QT_Q4_K) {
-            const uint8_t *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
-            q4_chunk(y, wc, st, ss, j, kq, cur.M);
-        } else {
-            iq_chunk(y, wc, st, j, kq, nblocks(kc), cur.M);
-        }
+        const uint8_t *st = lds + (s & 1) * STAGE_BYTES, *ss = lds + 2 * STAGE_BYTES + (s & 1) * SUMS_BYTES;
+        q4_chunk(y, wc, st, ss, j, kq, cur.M);
         if (kc == nkc - 1) {
             const int d0 = cur.blk * DN_DB + wave * 32;
 #pragma unroll
@@ -1753,7 +1690,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
         DnArgs DA{nt, D, F, offsets, tt, seg_lo, seg_hi, row_slot, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr,
                   qg_row_bytes_host(L->down_type, F), sh ? qg_row_bytes_host(L->sh_down_type, F) : 0, midp, msp, slots};
-        if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel<QT_Q4_K>, dim3(grid), dim3(512), PF_LDS, s, DA);
+        if (fmt == QT_Q4_K) pf_launch(slot, pf_down_kernel, dim3(grid), dim3(512), PF_LDS, s, DA);
         else pf_launch(slot, pf_down_iq_kernel, dim3(grid), dim3(512), PF_IQ_LDS, s, DA);
         return hipGetLastError();
     };
