@@ -137,6 +137,29 @@ def test_prefill_config3_routing_dispatch_outputs(layer3):
     check_outputs(fw, L, H, x, rows, "config3 B=2048")
 
 
+def test_prefill_wide_hidden_item_ring_refill(qgl):
+    """D = 8192 (the widest accepted width) at 8192 tokens: each persistent
+    workgroup of the down pass runs about 250 items, so its ring of decoded
+    items (128 entries, refilled 64 at a time) is refilled and reread several
+    times.  Routing of sampled rows bit-exact, their outputs within the bars."""
+    spec = synth.LayerSpec(seed=8192, width=8192, ff=512, gate_type=12, up_type=12, down_type=20)
+    say("building a 8192/512 layer on device")
+    L, H = synth.build_layer(spec), host_layer(spec)
+    nt = 8192
+    x = synth.inputs(8193, nt, 8192)
+    fw = forward(L, x)
+    rows = sample_rows(nt, 12, 13)
+    ids, w = O.route(H.logits(x[rows]))
+    np.testing.assert_array_equal(fw.ids.get()[rows], ids, err_msg="routing ids")
+    np.testing.assert_array_equal(fw.w.get()[rows].view('u4'), w.view('u4'), err_msg="routing weights")
+    all_ids = fw.ids.get()[:nt]
+    n = np.bincount(all_ids.ravel(), minlength=512)
+    tiles = int(np.sum((n + 63) // 64))
+    say(f"  tiles {tiles}: about {tiles * 32 // 256} down items per workgroup on 256 CUs")
+    assert tiles * 32 > 128 * 256, "the item ring must be refilled and reread"
+    check_outputs(fw, L, H, x, rows, "8192/512 B=8192")
+
+
 def test_prefill_int8_dense_pass(layer3, layer1):
     """The int8 variant of the dense gate/up pass (qg_prefill_int8_dense):
     config 3's dense experts, and the shared expert of a 300-token batch
