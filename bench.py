@@ -16,8 +16,10 @@ before the timed region.
             coverage flags.
 --config 3: the 2048-token prefill (Zipf(1.1)-biased router, Q4_K gate/up,
             IQ4_NL down): value = tokens/s of the layer; roofline = the
-            matrix-core utilisation of the dense pass (experts with >= 256
-            rows) of the grouped gate/up GEMM against the int8 peak.
+            matrix-core utilisation of the grouped gate/up GEMM (one launch
+            over every expert) against the int8 peak; the dense experts
+            (>= 256 rows) are also timed in a launch of their own, on fp16
+            and on int8 matrix cores.
 --matmul:   qg_matmul (exact reference order) on the D = 2560 dense
             projections in Q4_K at --batch tokens (default 1): value = weight
             GB/s; cpu_baseline = the reference's qc_matmul.
@@ -55,11 +57,11 @@ ROUTER_BYTES = EXPERTS * D * 4
 HBM_PEAK_GBS = 8000.0
 METRIC = "routed-MoE tokens/s + % HBM peak at B=1/17; int8 MFMA util at 2048-tok prefill"
 KERNELS = ["router", "route", "gate_up", "down", "combine"]
-PF_KERNELS = ["router", "route", "scan", "fill", "gate_up_dense", "gate_up_other", "down_dense", "down_other",
+PF_KERNELS = ["router", "route", "scan", "fill", "gate_up_dense", "gate_up", "down_dense", "down",
               "down_shared", "combine", "count"]
 INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 MFMA (POP/s x 1e3)
 FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 MFMA
-DENSE_MIN = 256                   # rows from which an expert runs in the dense pass
+DENSE_MIN = 256                   # rows from which an expert is dense
 
 
 def layer_bytes(nt: int, unique: float, shared: bool) -> float:
@@ -382,21 +384,23 @@ def bench_prefill(args, data: str) -> dict:
     ms = qg.elapsed_ms(b, e) / args.steps
     qg.lib().qg_graph_destroy(g)
     kern = kernel_times(wl.step, PF_KERNELS, args.steps)
-    # the int8 variant of the dense gate/up pass, timed the same way
-    prev = qg.lib().qg_prefill_int8_dense(1)
-    try:
-        kern_i8 = kernel_times(wl.step, PF_KERNELS, args.steps)
-    finally:
-        qg.lib().qg_prefill_int8_dense(prev)
+    # the dense experts' gate/up in a launch of their own, on fp16 (mode 2)
+    # and on int8 matrix cores (mode 1), timed the same way
+    split = {}
+    for mode in () if getattr(args, "no_split", False) else (2, 1):
+        prev = qg.lib().qg_prefill_int8_dense(mode)
+        try:
+            split[mode] = kernel_times(wl.step, PF_KERNELS, args.steps).get("gate_up_dense")
+        finally:
+            qg.lib().qg_prefill_int8_dense(prev)
     # algorithmic matrix-core work: 2 ops per multiply-add of the useful products
     ops_gu = lambda rows: 2.0 * rows * 2 * D * FF
     ops_dn = lambda rows: 2.0 * rows * D * FF
     rows_dense, rows_all = int(n_e[dense].sum()), int(n_e.sum())
-    t_gu = kern.get("gate_up_dense")
-    achieved = ops_gu(rows_dense) / (t_gu * 1e-3) / 1e12 if t_gu and rows_dense else None
-    t_dense = (kern.get("gate_up_dense", 0) + kern.get("down_dense", 0)) or None
-    util_dense = (ops_gu(rows_dense) + ops_dn(rows_dense)) / (t_dense * 1e-3) / 1e12 / INT8_PEAK_TOPS if t_dense and rows_dense else None
-    t_experts = sum(kern.get(k, 0) for k in ("gate_up_dense", "gate_up_other", "down_dense", "down_other", "down_shared"))
+    t_gu = kern.get("gate_up")
+    achieved = ops_gu(rows_all) / (t_gu * 1e-3) / 1e12 if t_gu else None
+    t_experts = sum(kern.get(k, 0) for k in ("gate_up", "down"))
+    util = lambda ops, t: round(ops / (t * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4) if t and ops else None
     touched = int(np.count_nonzero(n_e))
     layer_b = ROUTER_BYTES + touched * EXPERT_BYTES + nt * (2 * D * 4 + 80)
     line = {
@@ -408,21 +412,23 @@ def bench_prefill(args, data: str) -> dict:
                    "batch_tokens": nt, "experts_touched": touched, "dense_experts": int(dense.sum()),
                    "dense_rows": rows_dense, "rows": rows_all, "max_rows": int(n_e.max()),
                    "matrix_cores": "fp16 16x16x32 MFMA, exact integer weights x fp16 hi/lo activation planes, fp32 accumulate",
-                   "dense_pass_int8_util_algorithmic": round(util_dense, 4) if util_dense else None,
-                   "dense_pass_fp16_util_issued": round(2 * util_dense * INT8_PEAK_TOPS / FP16_PEAK_TFLOPS, 4) if util_dense else None,
-                   "dense_gate_up_int8_variant": {
-                       "arithmetic": "int8 16x16x32 MFMA per Q4_K group and activation plane (two int8 planes, row scale), "
-                                     "per-group int32->fp32 scaling",
-                       "us_fp16": round(t_gu * 1000, 2) if t_gu else None,
-                       "us_int8": round(kern_i8["gate_up_dense"] * 1000, 2) if kern_i8.get("gate_up_dense") else None,
-                       "int8_util_algorithmic": round(ops_gu(rows_dense) / (kern_i8["gate_up_dense"] * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)
-                       if kern_i8.get("gate_up_dense") and rows_dense else None},
+                   "expert_gemms_int8_util_algorithmic": util(ops_gu(rows_all) + ops_dn(rows_all), t_experts),
+                   "expert_gemms_fp16_util_issued": round(2 * (ops_gu(rows_all) + ops_dn(rows_all)) / (t_experts * 1e-3) / 1e12
+                                                          / FP16_PEAK_TFLOPS, 4) if t_experts else None,
+                   "dense_experts_gate_up": {
+                       "rows": rows_dense,
+                       "us_fp16": round(split[2] * 1000, 2) if split.get(2) else None,
+                       "int8_util_algorithmic_fp16": util(ops_gu(rows_dense), split.get(2)),
+                       "us_int8_variant": round(split[1] * 1000, 2) if split.get(1) else None,
+                       "int8_util_algorithmic_int8_variant": util(ops_gu(rows_dense), split.get(1)),
+                       "int8_variant_arithmetic": "int8 16x16x32 MFMA per Q4_K group and activation plane (two int8 "
+                                                  "planes, row scale), per-group int32->fp32 scaling"},
                    "expert_gemm_TOPS_all": round((ops_gu(rows_all) + ops_dn(rows_all)) / (t_experts * 1e-3) / 1e12, 1) if t_experts else None,
                    "layer_bytes": int(layer_b), "layer_hbm_frac": round(layer_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                    "kernel_us": {k: round(v * 1000, 2) for k, v in kern.items()}},
-        "roofline": {"bound": "mfma", "kernel": "gate_up_dense", "achieved": round(achieved, 1) if achieved else None,
+        "roofline": {"bound": "mfma", "kernel": "gate_up", "achieved": round(achieved, 1) if achieved else None,
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4) if achieved else None,
-                     **load_traffic(f"gate_up_dense_config3_B{nt}", 1), "algorithmic_ops": ops_gu(rows_dense)},
+                     **load_traffic(f"gate_up_config3_B{nt}", 1), "algorithmic_ops": ops_gu(rows_all)},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
@@ -524,8 +530,12 @@ def main() -> int:
                          "the 48-layer stack, the prefill)")
     ap.add_argument("--matmul", action="store_true",
                     help="measure qg_matmul on the dense projections instead of the MoE layer (--batch tokens, default 1)")
+    ap.add_argument("--no-split", action="store_true",
+                    help="--config 3: skip the timings of the dense experts in launches of their own")
     ap.add_argument("--int8-dense", action="store_true",
-                    help="with --counter-pass: run the prefill dense gate/up pass in its int8 variant")
+                    help="with --counter-pass: the prefill dense experts' gate/up in a launch of their own on int8")
+    ap.add_argument("--dense-split", action="store_true",
+                    help="with --counter-pass: the prefill dense experts' gate/up in a launch of their own on fp16")
     ap.add_argument("--counter-pass", type=int, default=0, metavar="P",
                     help="for rocprofv3 counter runs: build the workload, print each layer's routing and algorithmic "
                          "bytes as one JSON line, then run P eager passes over the layers in order (dispatch k of a "
@@ -631,18 +641,18 @@ def main() -> int:
 
 def counter_pass(args) -> int:
     """Eager passes over the workload's layers in order, for counter runs."""
-    if args.int8_dense:
-        qg.lib().qg_prefill_int8_dense(1)
+    if args.int8_dense or args.dense_split:
+        qg.lib().qg_prefill_int8_dense(1 if args.int8_dense else 2)
     if args.config == 3:
         nt = args.batch if args.batch is not None else 2048
         wl = PrefillWorkload(nt, seed=9300)
         ids, _ = wl.routing()
         n_e = np.bincount(ids[ids >= 0].ravel(), minlength=EXPERTS)
         dense = n_e >= DENSE_MIN
-        info = {"config": 3, "batch": nt, "layers": [{"layer": 0, "dense_experts": int(dense.sum()),
-                                                       "dense_rows": int(n_e[dense].sum()),
-                                                       "gate_up_dense_algorithmic_bytes": int(dense.sum()) * GATEUP_BYTES
-                                                       + int(n_e[dense].sum()) * D * 4}]}
+        touched = int(np.count_nonzero(n_e))
+        info = {"config": 3, "batch": nt, "layers": [{"layer": 0, "experts_touched": touched, "dense_experts": int(dense.sum()),
+                                                       "rows": int(n_e.sum()),
+                                                       "gate_up_algorithmic_bytes": touched * GATEUP_BYTES + nt * D * 4}]}
     else:
         batch = args.batch if args.batch is not None else (17 if args.config in (1, 4) else 1)
         wl = Workload(args.config, batch, args.layers, seed=9000)
@@ -763,9 +773,9 @@ def sections(wl1: Workload, args) -> dict:
     pc = p["config"]
     out["config3_prefill_B2048"] = {
         "tokens_per_s": p["value"], "ms_per_layer": p["ms_per_step"],
-        "dense_pass_int8_util_algorithmic": pc["dense_pass_int8_util_algorithmic"],
-        "dense_pass_fp16_util_issued": pc["dense_pass_fp16_util_issued"],
-        "gate_up_dense_TOPS": p["roofline"]["achieved"], "gate_up_dense_int8_frac": p["roofline"]["frac"],
+        "gate_up_TOPS": p["roofline"]["achieved"], "gate_up_int8_frac": p["roofline"]["frac"],
+        "expert_gemms_int8_util_algorithmic": pc["expert_gemms_int8_util_algorithmic"],
+        "dense_experts_gate_up": pc["dense_experts_gate_up"],
         "dense_experts": pc["dense_experts"], "layer_hbm_frac": pc["layer_hbm_frac"], "kernel_us": pc["kernel_us"]}
     return out
 

@@ -203,13 +203,16 @@ int qg_synth_matrix(void *out, int type, uint64_t seed, uint64_t stream, int row
  * out, the per-tensor expert layout of a layer. */
 int qg_synth_experts(void *out, int type, uint64_t seed, int tensor, int experts, int rows, int cols, float sigma);
 
-/* No reference counterpart: for the calling thread, run the prefill dense
- * gate/up pass (experts with 256 or more rows) on int8 matrix cores (two
- * int8 activation planes per token row with a row scale, the Q4_K nibbles as
- * int8, per-group int32 -> fp32 scaling) instead of fp16 hi/lo planes; on != 0
- * enables.  Returns the previous setting.  A measurement switch for the
- * benchmark and its parity test; the default (0) is the faster fp16 pass. */
-int qg_prefill_int8_dense(int on);
+/* No reference counterpart: how the calling thread's prefill layers launch
+ * gate/up.  mode 0 (the default): one launch over every expert group.
+ * mode 1: the dense experts (256 or more rows) in a launch of their own on
+ * int8 matrix cores (two int8 activation planes per token row with a row
+ * scale, the Q4_K nibbles as int8, per-group int32 -> fp32 scaling), then the
+ * rest on fp16.  mode 2: the same split with both launches on fp16 hi/lo
+ * planes.  Other values select mode 0.  Returns the previous mode.  A
+ * measurement switch for the benchmark's int8-vs-fp16 comparison of the dense
+ * experts and its parity test. */
+int qg_prefill_int8_dense(int mode);
 
 #ifdef __cplusplus
 }

@@ -19,25 +19,25 @@
 //                 plus the rank of its token in the chunk's mask, so each
 //                 expert's rows are in ascending token order (the order of
 //                 moe_map_kernel, gpu.cu:489-500).
-//   P5 gate/up  : persistent grouped GEMM, two launches (the dense experts,
-//                 then the others and the shared expert); item = (group,
-//                 64-row tile, 128 F rows), or 256 F rows in the dense pass
-//                 when F is a multiple of 256; SwiGLU; mid rows as fp16 hi/lo
-//                 planes.
-//   P6 down     : persistent grouped GEMM, the same two passes; item =
-//                 (group, 64-row tile, 256 D rows); y rows written to the
-//                 selection's slot.
+//   P5 gate/up  : persistent grouped GEMM, one launch over every group
+//                 (the int8 variant: the dense experts in a launch of their
+//                 own); item = (group, 64-row tile, 128 F rows); SwiGLU; mid
+//                 rows as fp16 hi/lo planes.
+//   P6 down     : persistent grouped GEMM, one launch (three when the shared
+//                 expert's down format differs); item = (group, 64-row tile,
+//                 256 D rows); y rows written to the selection's slot.
 //   P7 combine  : out[t] = sum over ranks k of w[t,k]*y[t,k] in rank order,
 //                 + sigmoid-gated shared expert, + optional residual.
 // Groups are the 512 experts plus the shared expert (group 512, every token).
 //
 // GEMM tiles (operand conventions of qg_frag.h): a workgroup is 8 waves, one
-// per CU; each workgroup runs a contiguous range of (item, K step) steps.  The
-// tile's activation rows (64 rows x 2 planes x one K step) are staged in
-// shared memory by direct global->shared copies, double-buffered over steps;
-// each wave owns 32 weight rows (gate/up: 16 gate + 16 up, or two such pairs)
-// whose quantised bytes it copies, one step ahead, into a ring of its own in
-// shared memory (the Q4_K down launch keeps them in registers instead).  A
+// per CU; each workgroup streams the (item, K step) steps of its items, the
+// items cut between XCDs by estimated cost (balanced_items).  The tile's
+// activation rows (64 rows x 2 planes x one K step) are staged in shared
+// memory by direct global->shared copies, double-buffered over steps; each
+// wave owns 32 weight rows (gate/up: 16 gate + 16 up) whose quantised bytes
+// it copies, two steps ahead, into a ring of its own in shared memory (the
+// Q4_K down launch keeps them in registers instead).  A
 // 16x16x32 MFMA pair (hi and lo plane) per (row tile, column tile, 32-element
 // group); row tiles past the group's last row are skipped.  16-byte chunk c of
 // a staged row r sits at chunk c ^ (r & 15), so the 16 rows one MFMA reads
@@ -56,15 +56,19 @@ constexpr int KC = 256;                      // K elements per staged chunk
 constexpr int GU_FB = 128;                   // F rows per gate/up item (16 per wave)
 constexpr int DN_DB = 256;                   // D rows per down item (32 per wave)
 constexpr int NG = QG_EXPERTS + 1;           // groups: experts + shared expert
-constexpr int DENSE_MIN = 256;               // rows from which an expert runs in the dense pass
+constexpr int DENSE_MIN = 256;               // rows from which an expert is dense (pass order; the int8 variant)
 constexpr int STAGE_BYTES = PT * 2 * KC * 2; // [64 rows][2 planes][256] fp16
 constexpr int SUMS_BYTES = PT * 2 * 16;      // [64 rows][2 planes][8 group sums] fp16
 constexpr int PF_LDS = 2 * (STAGE_BYTES + SUMS_BYTES);
 
-// Groups in pass order (dense experts, the other experts, the shared expert);
-// tiles bounds[s] .. bounds[s+1]-1 form segment s (0 dense, 1 sparse, 2 shared);
-// order position p holds group gorder[p], whose tiles start at tbase[p].
-struct TileTable { int bounds[4]; int tbase[NG + 1]; int gorder[NG]; };
+// Groups in pass order: the dense experts (>= DENSE_MIN rows), the shared
+// expert, the other experts; experts by row count, largest first (ties by
+// expert id), so a pass's big tiles come first.  Order position p holds
+// group gorder[p], whose tiles start at tbase[p]; tiles bounds[s] ..
+// bounds[s+1]-1 form segment s (0 dense, 1 shared, 2 the others).  mbase /
+// mbounds: the same prefixes of the row-tile counts M (a group of n rows has
+// ceil(n / 16) of them over its tiles).
+struct TileTable { int bounds[4]; int tbase[NG + 1]; int gorder[NG]; int mbase[NG + 1]; int mbounds[4]; };
 
 struct PfLayout {
     size_t logits, flag, missing, mass, xp, xsp, counts, offsets, tbase, row_token, row_slot, midp, msp, slots, xn, xi8, xsc,
@@ -297,8 +301,8 @@ QG_DEV int scan512(int v, int *s_tmp) {
 __global__ __launch_bounds__(512) void pf_scan_kernel(int *counts, int nch, int *offsets, TileTable *tt, int shared_rows,
                                                       const int *bad, int *status) {
     __shared__ int s_tmp[8];
-    __shared__ int s_tiles[NG];
-    __shared__ int s_nd;
+    __shared__ int s_tiles[NG], s_m16[NG];
+    __shared__ int s_wh[8][64], s_above[64];
     const int e = threadIdx.x;
     if (status) {
         int b = 0;
@@ -331,30 +335,81 @@ __global__ __launch_bounds__(512) void pf_scan_kernel(int *counts, int nch, int 
         }
     }
     if (!tt) return;  // block-uniform
-    // pass order: dense experts, then the others (each in expert order), then shared
-    const int dense = n >= DENSE_MIN;
-    const int dincl = scan512(dense, s_tmp);
-    if (e == QG_EXPERTS - 1) s_nd = dincl;
+    // pass order: experts by row-count bucket, largest first, ties by id (a
+    // counting sort); buckets 0..16 hold ceil(n / 16) of the others, 17..63
+    // the dense experts by 32-row steps, so the dense ones lead; the shared
+    // expert follows them
+    const int lane = e & 63, wave = e >> 6;
+    const int bk = n >= DENSE_MIN ? 17 + min((n - DENSE_MIN) >> 5, 46) : (n + 15) >> 4;
+    unsigned long long same = ~0ull;  // lanes of this wave in the same bucket
+#pragma unroll
+    for (int bit = 0; bit < 6; bit++) {
+        const unsigned long long m = __ballot((bk >> bit) & 1);
+        same &= ((bk >> bit) & 1) ? m : ~m;
+    }
+    const int below = __popcll(same & ((1ull << lane) - 1ull));
+    s_wh[wave][lane] = 0;
+    const int nd = __syncthreads_count(n >= DENSE_MIN);
+    if (below == 0) s_wh[wave][bk] = __popcll(same);
     __syncthreads();
-    const int nd = s_nd, pos = dense ? dincl - 1 : nd + e - (dincl - dense);
-    s_tiles[pos] = (n + PT - 1) / PT;
-    tt->gorder[pos] = e;
-    if (e == 0) {
-        s_tiles[QG_EXPERTS] = (shared_rows + PT - 1) / PT;
-        tt->gorder[QG_EXPERTS] = QG_EXPERTS;
+    if (wave == 0) {  // experts in buckets above each bucket
+        int t = 0;
+        for (int w = 0; w < 8; w++) t += s_wh[w][63 - lane];
+        int incl = t;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
+        }
+        s_above[63 - lane] = incl - t;
     }
     __syncthreads();
+    int rank = s_above[bk] + below;
+    for (int w = 0; w < wave; w++) rank += s_wh[w][bk];
+    const int pos = rank < nd ? rank : rank + 1;
+    s_tiles[pos] = (n + PT - 1) / PT;
+    s_m16[pos] = (n + 15) / 16;
+    tt->gorder[pos] = e;
+    if (e == 0) {
+        s_tiles[nd] = (shared_rows + PT - 1) / PT;
+        s_m16[nd] = (shared_rows + 15) / 16;
+        tt->gorder[nd] = QG_EXPERTS;
+    }
+    __syncthreads();
+    // prefixes over positions 0..511 (thread e: position e), then position 512
     const int v = s_tiles[e], tincl = scan512(v, s_tmp);
+    const int m = s_m16[e], mincl = scan512(m, s_tmp);
     tt->tbase[e] = tincl - v;
-    if (e == nd) tt->bounds[1] = tincl - v;
+    tt->mbase[e] = mincl - m;
+    if (e == nd) {
+        tt->bounds[1] = tincl - v;
+        tt->mbounds[1] = mincl - m;
+    }
+    if (e == nd + 1) {
+        tt->bounds[2] = tincl - v;
+        tt->mbounds[2] = mincl - m;
+    }
     if (e == QG_EXPERTS - 1) {
-        const int all = tincl + s_tiles[QG_EXPERTS];
+        const int all = tincl + s_tiles[QG_EXPERTS], mall = mincl + s_m16[QG_EXPERTS];
         tt->tbase[QG_EXPERTS] = tincl;
+        tt->mbase[QG_EXPERTS] = mincl;
         tt->tbase[NG] = all;
+        tt->mbase[NG] = mall;
         tt->bounds[0] = 0;
-        if (nd == QG_EXPERTS) tt->bounds[1] = tincl;
-        tt->bounds[2] = tincl;
+        tt->mbounds[0] = 0;
+        if (nd == QG_EXPERTS) {  // position 512 (the shared expert) starts segment 1
+            tt->bounds[1] = tincl;
+            tt->mbounds[1] = mincl;
+        }
+        if (nd + 1 == QG_EXPERTS) {
+            tt->bounds[2] = tincl;
+            tt->mbounds[2] = mincl;
+        } else if (nd == QG_EXPERTS) {
+            tt->bounds[2] = all;
+            tt->mbounds[2] = mall;
+        }
         tt->bounds[3] = all;
+        tt->mbounds[3] = mall;
     }
 }
 
@@ -512,16 +567,57 @@ QG_DEV void q4_chunk(qg_f4 (&y)[4][NCT], const Q4Ops &o, const uint8_t *st, cons
 }
 
 // Items of a persistent launch, XCD-aware: workgroup b runs on XCD b % 8
-// (round-robin dispatch), and XCD x takes the contiguous range of items
-// [x*C, (x+1)*C), C = ceil(total/8), so that the items running together on
-// one XCD share expert weights and activation rows in that XCD's L2.
-struct ItemRange { int next, end, step; };
-QG_DEV ItemRange xcd_items(int total) {
+// (round-robin dispatch) and takes its XCD's share xs .. xe-1 of the items
+// in rounds of nx (the XCD's workgroups), position slot of each round, so
+// neighbouring items (the row blocks of one tile, the tiles of one expert)
+// run at the same time on one XCD and share its L2.
+struct ItemRange { int xs, xe, nx, slot; };
+QG_DEV int range_count(const ItemRange &r) { return r.xe - r.xs > r.slot ? (r.xe - r.xs - r.slot + r.nx - 1) / r.nx : 0; }
+
+// The XCDs' shares of a pass, of equal estimated cost.  An item of a tile
+// with M row tiles is priced CA + CB M (its fixed per-step costs plus its
+// products, fitted to per-workgroup durations on config 3); the pass's items
+// are cut at item granularity into 8 parts of equal total price.  The pass
+// order lists groups by row count, largest first, so the cut gives each XCD
+// items of like size, which its workgroups share evenly.  All threads of the
+// block call it (s_tb: the tile table's tbase, filled before the call).
+template <int CA, int CB>
+QG_DEV ItemRange balanced_items(const TileTable *tt, const int *s_tb, int seg_lo, int seg_hi, int nblk) {
+    __shared__ int s_res[2];
+    const int t_lo = tt->bounds[seg_lo], t_hi = tt->bounds[seg_hi], m_lo = tt->mbounds[seg_lo];
+    const long long total_cost = (long long)nblk * (CA * (long long)(t_hi - t_lo) + CB * (long long)(tt->mbounds[seg_hi] - m_lo));
     const int x = blockIdx.x & 7, slot = blockIdx.x >> 3, n_x = (gridDim.x - x + 7) >> 3;
-    const int C = (total + 7) >> 3;
-    return ItemRange{x * C + slot, min(total, (x + 1) * C), n_x};
+    constexpr int parts = 8;
+    // first item of parts x and x + 1: the first item whose price prefix
+    // reaches ceil(total_cost * q / 8)
+    long long Q[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) Q[k] = (total_cost * (x + k) + parts - 1) / parts;
+    if (threadIdx.x < 2) s_res[threadIdx.x] = Q[threadIdx.x] >= total_cost ? (t_hi - t_lo) * nblk : 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < NG; e += blockDim.x) {
+        const int tb0 = s_tb[e], tb1 = s_tb[e + 1];
+        if (tb1 == tb0 || tb0 < t_lo || tb1 > t_hi) continue;
+        const int mb0 = tt->mbase[e], mb1 = tt->mbase[e + 1];
+        const long long g0 = (long long)nblk * (CA * (long long)(tb0 - t_lo) + CB * (long long)(mb0 - m_lo));
+        const long long g1 = (long long)nblk * (CA * (long long)(tb1 - t_lo) + CB * (long long)(mb1 - m_lo));
+        const int T = tb1 - tb0, m_last = mb1 - mb0 - 4 * (T - 1);
+        const long long full = (long long)nblk * (CA + 4 * CB);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            if (!(g0 < Q[k] && Q[k] <= g1) || Q[k] >= total_cost) continue;
+            const int j = (int)min((long long)(T - 1), (Q[k] - g0 - 1) / full);
+            const long long ct = g0 + j * full;
+            const int w = CA + CB * (j < T - 1 ? 4 : m_last);
+            const int blk = (int)((Q[k] - ct + w - 1) / w);
+            s_res[k] = (tb0 + j - t_lo) * nblk + blk;
+        }
+    }
+    __syncthreads();
+    const int n_items = (t_hi - t_lo) * nblk, i0 = min(max(s_res[0], 0), n_items), i1 = min(max(s_res[1], i0), n_items);
+    __syncthreads();
+    return ItemRange{i0, i1, n_x, slot};
 }
-QG_DEV int range_count(const ItemRange &r) { return r.next < r.end ? (r.end - r.next + r.step - 1) / r.step : 0; }
 
 // Tile -> order position (block-uniform): the largest p with tb[p] <= tile_idx
 // (empty groups share their successor's start).
@@ -567,15 +663,15 @@ QG_DEV PfItem pf_unpack(int2 v) {
 
 // The workgroup's items, decoded ahead into a ring in shared memory (the
 // search over the tile table stays out of the step stream): items k .. k+63
-// are written by threads 0..63 when item k - 64 starts (k a multiple of 64),
-// into the slots of items k - 128 .. k - 65, all finished by then; the next
-// reader of the new slots is two steps or more (and a barrier) away.
+// are written when item k - 64 starts (k a multiple of 64), into the slots of
+// items k - 128 .. k - 65, all finished by then; the next reader of the new
+// slots is two steps or more (and a barrier) away.
 constexpr int IT_RING = 128, IT_BATCH = 64;
 struct ItemRing {
     int2 *ring; const int *tb, *go, *off; int nt, t_lo, nblk, nitems; ItemRange ir;
     __device__ __forceinline__ void fill(int k0, int n, int tid) const {
         const int k = k0 + tid;
-        if (tid < n && k < nitems) ring[k & (IT_RING - 1)] = pf_item_packed(tb, go, off, nt, t_lo, nblk, ir.next + k * ir.step);
+        if (tid < n && k < nitems) ring[k & (IT_RING - 1)] = pf_item_packed(tb, go, off, nt, t_lo, nblk, ir.xs + ir.slot + k * ir.nx);
     }
     __device__ __forceinline__ PfItem at(int k) const { return pf_unpack(ring[k & (IT_RING - 1)]); }
 };
@@ -637,7 +733,7 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
     }
     const int ndb = A.D / DN_DB, F = A.F, F32 = A.F / 32, nkc = (F + KC - 1) / KC;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
-    const ItemRange ir = xcd_items(total);
+    const ItemRange ir = balanced_items<10, 3>(A.tt, s_tb, A.seg_lo, A.seg_hi, ndb);
     const int nitems = range_count(ir), steps = nitems * nkc;
     if (steps == 0) return;  // block-uniform
     const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, ndb, nitems, ir};
@@ -820,7 +916,7 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
     }
     const int ndb = A.D / DN_DB, F = A.F, nkc = (F + IQ_KC - 1) / IQ_KC;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
-    const ItemRange ir = xcd_items(total);
+    const ItemRange ir = balanced_items<10, 3>(A.tt, s_tb, A.seg_lo, A.seg_hi, ndb);
     const int nitems = range_count(ir), steps = nitems * nkc;
     if (steps == 0) return;  // block-uniform
     const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, ndb, nitems, ir};
@@ -979,13 +1075,10 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
 // ---- gate/up: the Q4_K weights through each wave's own shared-memory ring ----
 // A step is half a superblock (128 K elements, groups 4h .. 4h+3): per weight
 // row the superblock's 16-byte header (piece 0) and the half's 64 qs bytes
-// (pieces 1..4).  The sparse pass keeps a slot row-major (row r's pieces at
-// 80 r, 160 pieces in 3 copies, so each copy's lanes read whole runs of few
-// rows; lanes past them copy the last piece again into the slot's padding);
-// the dense pass keeps its slots piece-major (piece p of row r at p * 16 x
-// rows + 16 r: one row address per lane serves every copy).  The 8 group
-// sums of a superblock are staged with its first half, into their own double
-// buffer.
+// (pieces 1..4).  A slot is row-major (row r's pieces at 80 r, 160 pieces in
+// 3 copies, so each copy's lanes read whole runs of few rows; lanes past them
+// copy the last piece again into the slot's padding).  The 8 group sums of a
+// superblock are staged with its first half, into their own double buffer.
 constexpr int GQ_PIECES = 5;
 constexpr int GQ_ROWB = GQ_PIECES * 16;
 constexpr int GQ_COPIES = 3;
@@ -1176,7 +1269,7 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     }
     const int nfb = A.F / GU_FB, NH = A.D / 128, D32 = A.D / 32, F = A.F;   // NH steps per item (even)
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
-    const ItemRange ir = xcd_items(total);
+    const ItemRange ir = balanced_items<7, 3>(A.tt, s_tb, A.seg_lo, A.seg_hi, nfb);
     const int nitems = range_count(ir), steps = nitems * NH;
     if (steps == 0) return;  // block-uniform
     const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
@@ -1361,169 +1454,6 @@ __global__ __launch_bounds__(512, 1) void pf_gateup_kernel(GuArgs A) {
     }
 }
 
-// ---- gate/up, wide items (F a multiple of 256): 256 F rows per item ----
-// Wave w takes F rows f0 = 32 w .. +31 of the block as two pairs of column
-// tiles (pair p: gate and up rows f0 + 16 p .. +15), so a tile's activations
-// are staged half as often as with 128-row items and each step's fixed
-// costs (barrier, copy issue) cover twice the weights.  The wave's 64 weight
-// rows of a step (slot row 32 p + 16 u + r: pair p, gate (u = 0) or up, row
-// r) go piece-major to one of two slots of its ring, copy t taking piece t of
-// every row, one step ahead; its 32 rows are one 32-row group of a Q4_K down
-// format, whose sums it forms alone.
-constexpr int GW_FB = 256;
-constexpr int GW_COPIES = 5;
-constexpr int GW_SLOT = GW_COPIES * 64 * 16;
-constexpr int PF_GW_LDS = 2 * IQ_STAGE + 2 * GQ_SUMS + PF_WAVES * 2 * GW_SLOT;
-static_assert(GQ_PIECES == GW_COPIES, "one copy per piece");
-
-__global__ __launch_bounds__(512, 1) void pf_gateup_w_kernel(GuArgs A) {
-    extern __shared__ uint4 s_dyn[];
-    uint8_t *lds = (uint8_t *)s_dyn;
-    __shared__ int s_tb[NG + 1], s_go[NG], s_off[QG_EXPERTS + 1];
-    __shared__ int2 s_it[IT_RING];
-    __shared__ int s_src[2][PT];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    for (int i = tid; i <= NG; i += 512) {
-        s_tb[i] = A.tt->tbase[i];
-        if (i < NG) s_go[i] = A.tt->gorder[i];
-        if (i <= QG_EXPERTS) s_off[i] = A.offsets[i];
-    }
-    const int nfb = A.F / GW_FB, NH = A.D / 128, D32 = A.D / 32, F = A.F;   // NH steps per item (even)
-    const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * nfb;
-    const ItemRange ir = xcd_items(total);
-    const int nitems = range_count(ir), steps = nitems * NH;
-    if (steps == 0) return;  // block-uniform
-    const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, nfb, nitems, ir};
-    __syncthreads();
-    R.fill(0, IT_RING, tid);
-    __syncthreads();
-    uint8_t *sums = lds + 2 * IQ_STAGE;                                         // two superblock sum buffers
-    uint8_t *ring = lds + 2 * IQ_STAGE + 2 * GQ_SUMS + (size_t)wave * 2 * GW_SLOT;  // this wave's two slots
-    auto mrow = [&](const PfItem &it, int tr) { return it.shared ? A.nt * QG_TOP + it.base + tr : it.base + tr; };
-    // Weight copies: lane l takes slot row l (pair l / 32, the up rows for
-    // bit 4); copy t takes piece t of every row, at 16 t + 64 h from the
-    // superblock (the header, t = 0, at 0).
-    const uint8_t *wp = nullptr;  // the lane's row in the item being copied
-    auto set_wp = [&](const PfItem &it) {
-        const uint8_t *b = (lane & 16) ? (it.shared ? A.sh_up : A.up + (size_t)it.g * F * A.rb)
-                                       : (it.shared ? A.sh_gate : A.gate + (size_t)it.g * F * A.rb);
-        wp = b + (size_t)(it.blk * GW_FB + wave * 32 + 16 * (lane >> 5) + (lane & 15)) * A.rb;
-    };
-    auto copy_w = [&](int q, int c) {  // step c of the item being copied into slot q
-        const uint8_t *x = wp + (size_t)(c >> 1) * 144;
-        const uint32_t hh = (c & 1) ? 64u : 0u;
-#pragma unroll
-        for (int t = 0; t < GW_COPIES; t++) dma16_ordered(x + (t == 0 ? 0u : 16u * t + hh), ring + q * GW_SLOT + t * 1024);
-    };
-    // activation copies of the item being staged (as in pf_gateup_kernel)
-    const uint8_t *sp[4] = {nullptr, nullptr, nullptr, nullptr}, *sump = nullptr;
-    int s_nc = 0;
-    bool s_sum = false;
-    auto set_sp = [&](const PfItem &it, int buf) {
-        s_nc = it.M;
-        s_sum = wave * 32 < 16 * it.M;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int q = wave + PF_WAVES * i, tr = 2 * q + (lane >> 5), p = (lane >> 4) & 1, c16 = (lane & 15) ^ (tr & 15);
-            if (i < it.M) sp[i] = (const uint8_t *)(A.xp + ((size_t)s_src[buf][tr] * 2 + p) * A.D + c16 * 8);
-        }
-        if (s_sum) {
-            const int C = wave * 64 + lane, tr = C >> 1, p = C & 1;
-            sump = (const uint8_t *)(A.xsp + ((size_t)s_src[buf][tr] * 2 + p) * D32);
-        }
-    };
-    auto stage_at = [&](int s, int c) {
-        uint8_t *st = lds + (s & 1) * IQ_STAGE;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (i < s_nc) dma16_ordered(sp[i] + (size_t)c * 256, st + (wave + PF_WAVES * i) * 1024);
-        if ((c & 1) == 0 && s_sum) dma16_ordered(sump + (size_t)(c >> 1) * 16, sums + ((s >> 1) & 1) * GQ_SUMS + wave * 1024);
-    };
-    // prologue: item 0's rows, its first stage and the weights of step 0
-    PfItem cur = R.at(0);
-    item_rows(s_src[0], cur, A.row_token, 0, wave, lane);
-    wait_vmem();
-    __syncthreads();
-    set_sp(cur, 0);
-    stage_at(0, 0);
-    set_wp(cur);
-    copy_w(0, 0);
-    int s = 0;
-    auto run_item = [&](const int k, auto MC) {
-        constexpr int M = decltype(MC)::value;
-        qg_f4 y0[M][2], y1[M][2];   // pair 0, pair 1: [row tile][gate, up]
-#pragma unroll
-        for (int m = 0; m < M; m++)
-#pragma unroll
-            for (int n = 0; n < 2; n++) y0[m][n] = y1[m][n] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < NH; c++, s++) {
-            wait_vmem();  // this step's stage and weights (and every earlier copy)
-            __syncthreads();
-            if (c == 0) {
-                if (k > 0 && (k & (IT_BATCH - 1)) == 0) R.fill(k + IT_BATCH, IT_BATCH, tid);
-                if (k + 1 < nitems) item_rows(s_src[(k + 1) & 1], R.at(k + 1), A.row_token, 0, wave, lane);
-            }
-            if (s + 1 < steps) {
-                if (c == NH - 1) {
-                    set_sp(R.at(k + 1), (k + 1) & 1);
-                    set_wp(R.at(k + 1));
-                }
-                stage_at(s + 1, c + 1 < NH ? c + 1 : 0);
-                copy_w((s + 1) & 1, c + 1 < NH ? c + 1 : 0);  // slot (s + 1) % 2 was read by step s - 1
-            }
-            const uint8_t *st = lds + (s & 1) * IQ_STAGE, *slot = ring + (s & 1) * GW_SLOT;
-            const uint8_t *ss = (c & 1) == 0 ? sums + ((s >> 1) & 1) * GQ_SUMS : nullptr;
-            gq_chunk<M, 2, 16, 1024>(y0, slot, st, ss, c & 1, j, kq);
-            __builtin_amdgcn_sched_barrier(0);
-            gq_chunk<M, 2, 16, 1024>(y1, slot + 32 * 16, st, ss, c & 1, j, kq);
-        }
-        // SwiGLU: pair t, F row f0 + 16 t + j
-        const PfItem it = R.at(k);
-        const int fmt = it.shared ? A.sh_down_fmt : A.down_fmt, f0 = it.blk * GW_FB + wave * 32;
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tr = m * 16 + 4 * kq + i;
-                float sp2 = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const float ma = t ? qg_swiglu_fast(y1[m][0][i], y1[m][1][i]) : qg_swiglu_fast(y0[m][0][i], y0[m][1][i]);
-                    if (tr < it.nv) {
-                        const int pa = plane_pos(fmt, f0 + 16 * t + j);
-                        _Float16 *hp = A.midp + (size_t)mrow(it, tr) * 2 * F;
-                        const _Float16 ha = (_Float16)ma;
-                        hp[pa] = ha;
-                        hp[F + pa] = (_Float16)(ma - (float)ha);
-                    }
-                    sp2 += ma;
-                }
-                if (fmt == QT_Q4_K) {
-                    // the wave's 32 rows are one group: sum over the 16 j (lanes of one kq)
-                    sp2 += __shfl_xor(sp2, 1);
-                    sp2 += __shfl_xor(sp2, 2);
-                    sp2 += __shfl_xor(sp2, 4);
-                    sp2 += __shfl_xor(sp2, 8);
-                    if (j == 0 && tr < it.nv) {
-                        _Float16 *gp = A.msp + (size_t)mrow(it, tr) * 2 * (F / 32) + f0 / 32;
-                        const _Float16 hs = (_Float16)sp2;
-                        gp[0] = hs;
-                        gp[F / 32] = (_Float16)(sp2 - (float)hs);
-                    }
-                }
-            }
-        }
-    };
-    for (int k = 0; k < nitems; k++) {
-        switch (R.at(k).M) {  // block-uniform
-        case 1: run_item(k, std::integral_constant<int, 1>{}); break;
-        case 2: run_item(k, std::integral_constant<int, 2>{}); break;
-        case 3: run_item(k, std::integral_constant<int, 3>{}); break;
-        default: run_item(k, std::integral_constant<int, 4>{}); break;
-        }
-    }
-}
-
 // ---------------- P7: combine ----------------
 struct CombArgs {
     int nt, D;
@@ -1609,12 +1539,15 @@ __global__ __launch_bounds__(1024) void pf_stats_kernel(qg_prune_stats *stats, c
 
 }  // namespace
 
-// The dense gate/up pass in int8 (two int8 activation planes, per-group
-// int32 -> fp32 scaling) instead of fp16 hi/lo planes, for the calling thread.
-static thread_local int tl_pf_i8 = 0;
-extern "C" int qg_prefill_int8_dense(int on) {
-    const int prev = tl_pf_i8;
-    tl_pf_i8 = on ? 1 : 0;
+// Gate/up launches of the calling thread's prefill layers: 0 one launch over
+// every group; 1 the dense experts in a launch of their own in int8 (two int8
+// activation planes, per-group int32 -> fp32 scaling), then the rest; 2 the
+// same split with both launches in fp16 (the like-for-like timing of the
+// dense experts).  Other values are taken as 0.
+static thread_local int tl_pf_split = 0;
+extern "C" int qg_prefill_int8_dense(int mode) {
+    const int prev = tl_pf_split;
+    tl_pf_split = mode == 1 || mode == 2 ? mode : 0;
     return prev;
 }
 
@@ -1661,7 +1594,8 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, L->router_bias, logits};
     pf_launch(0, pf_router_kernel, dim3((nt + RT_TOK - 1) / RT_TOK, (rows + RT_ROWS - 1) / RT_ROWS), dim3(512), RT_LDS, s, R);
     if ((rc = hipGetLastError())) return rc;
-    const bool i8 = tl_pf_i8 != 0;
+    const int split = tl_pf_split;
+    const bool i8 = split == 1;
     int8_t *xi8 = i8 ? (int8_t *)(ws + lay.xi8) : nullptr;
     float *xsc = i8 ? (float *)(ws + lay.xsc) : nullptr, *row_sx = i8 ? (float *)(ws + lay.row_sx) : nullptr;
     RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, flag,
@@ -1676,16 +1610,22 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     pf_launch(3, pf_fill_kernel, dim3(nch), dim3(512), 0, s, row_token, row_slot, (const int *)counts, (const int *)ids,
               (const int *)flag, nt, row_sx, (const float *)xsc);
     if ((rc = hipGetLastError())) return rc;
-    // grouped GEMMs: the dense pass (experts with >= 256 rows), then the rest
+    // grouped GEMMs: one launch over every group (dense experts, the shared
+    // expert, the others); qg_prefill_int8_dense splits the dense experts off
     const int grid = qg_cu_count();
-    for (int pass = 0; pass < 2; pass++) {
-        GuArgs G{nt, D, F, offsets, tt, pass ? 1 : 0, pass ? 3 : 1, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
+    auto gate_up = [&](int seg_lo, int seg_hi, bool int8, int slot) {
+        GuArgs G{nt, D, F, offsets, tt, seg_lo, seg_hi, row_token, (const uint8_t *)L->gate, (const uint8_t *)L->up,
                  sh ? (const uint8_t *)L->sh_gate : nullptr, sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D),
                  xp, xsp, midp, msp, L->down_type, sh ? L->sh_down_type : L->down_type, xi8, xsc, row_sx};
-        if (i8 && pass == 0) pf_launch(4 + pass, pf_gateup_kernel<true>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
-        else if (pass == 0 && F % GW_FB == 0) pf_launch(4 + pass, pf_gateup_w_kernel, dim3(grid), dim3(512), PF_GW_LDS, s, G);
-        else pf_launch(4 + pass, pf_gateup_kernel<false>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
-        if ((rc = hipGetLastError())) return rc;
+        if (int8) pf_launch(slot, pf_gateup_kernel<true>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
+        else pf_launch(slot, pf_gateup_kernel<false>, dim3(grid), dim3(512), PF_GQ_LDS, s, G);
+        return hipGetLastError();
+    };
+    if (split) {
+        if ((rc = gate_up(0, 1, i8, 4))) return rc;
+        if ((rc = gate_up(1, 3, false, 5))) return rc;
+    } else if ((rc = gate_up(0, 3, false, 5))) {
+        return rc;
     }
     auto down = [&](int seg_lo, int seg_hi, int fmt, int slot) {
         DnArgs DA{nt, D, F, offsets, tt, seg_lo, seg_hi, row_slot, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr,
@@ -1694,12 +1634,12 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
         else pf_launch(slot, pf_down_iq_kernel, dim3(grid), dim3(512), PF_IQ_LDS, s, DA);
         return hipGetLastError();
     };
-    if ((rc = down(0, 1, L->down_type, 6))) return rc;
     if (!sh || L->sh_down_type == L->down_type) {
-        if ((rc = down(1, 3, L->down_type, 7))) return rc;
-    } else {
-        if ((rc = down(1, 2, L->down_type, 7))) return rc;
-        if ((rc = down(2, 3, L->sh_down_type, 8))) return rc;
+        if ((rc = down(0, 3, L->down_type, 7))) return rc;
+    } else {  // the shared expert's down in its own format
+        if ((rc = down(0, 1, L->down_type, 6))) return rc;
+        if ((rc = down(2, 3, L->down_type, 7))) return rc;
+        if ((rc = down(1, 2, L->sh_down_type, 8))) return rc;
     }
     CombArgs CA{nt, D, ids, weights, flag, slots, sh ? logits + QG_EXPERTS : nullptr, rows, out, resid};
     pf_launch(9, pf_combine_kernel, dim3((D / 4 + 255) / 256, nt), dim3(256), 0, s, CA);

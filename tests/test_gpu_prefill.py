@@ -160,11 +160,14 @@ def test_prefill_wide_hidden_item_ring_refill(qgl):
     check_outputs(fw, L, H, x, rows, "8192/512 B=8192")
 
 
-def test_prefill_int8_dense_pass(layer3, layer1):
-    """The int8 variant of the dense gate/up pass (qg_prefill_int8_dense):
-    config 3's dense experts, and the shared expert of a 300-token batch
-    (300 rows: in the dense pass), against the oracle at the same bars."""
-    prev = qg.lib().qg_prefill_int8_dense(1)
+@pytest.mark.parametrize("mode", [1, 2])
+def test_prefill_dense_split_launches(layer3, layer1, mode):
+    """The dense experts' gate/up in a launch of their own
+    (qg_prefill_int8_dense: mode 1 on int8 matrix cores, mode 2 on fp16):
+    config 3's dense experts, and a 300-token config-1 batch with correlated
+    routing (dense experts next to the shared expert), against the oracle at
+    the same bars."""
+    prev = qg.lib().qg_prefill_int8_dense(mode)
     try:
         L, H = layer3
         x = synth.inputs(3003, 2048, 2048)
@@ -173,12 +176,12 @@ def test_prefill_int8_dense_pass(layer3, layer1):
         n = np.bincount(ids.ravel(), minlength=512)
         dense = np.flatnonzero(n >= 256)
         rows_dense = np.flatnonzero(np.isin(ids, dense).any(axis=1))
-        check_outputs(fw, L, H, x, rows_dense[:: max(1, len(rows_dense) // 24)], "config3 int8 dense pass")
+        check_outputs(fw, L, H, x, rows_dense[:: max(1, len(rows_dense) // 24)], f"config3 dense launch, mode {mode}")
         L1, H1 = layer1
         x1 = synth.inputs(3101, 300, L1.spec.width, correlated=True)
         fw1 = forward(L1, x1)
         check_routing(fw1, H1, x1)
-        check_outputs(fw1, L1, H1, x1, sample_rows(300, 24, 5), "shared expert in the int8 dense pass")
+        check_outputs(fw1, L1, H1, x1, sample_rows(300, 24, 5), f"300 correlated tokens, mode {mode}")
     finally:
         qg.lib().qg_prefill_int8_dense(prev)
 
