@@ -131,18 +131,21 @@ __global__ __launch_bounds__(256) void pf_norm_kernel(float *xn, const float *x,
 // ---------------- P1: router logits ----------------
 // logits[t][r] = sum_k R[r][k] x[t][k] in the order of cpu.c:122-139: chain j
 // (0..31) accumulates k = j, j+32, ... ascending with fused multiply-add,
-// then the tree 16/8/4/2/1 of gpu.cu:154-180 (qg_tree32).  Block = 8 waves =
-// 64 tokens x 32 rows; half-wave h of wave w owns 16 tokens (w & 3) x 8 rows
-// ((w >> 2) * 2 + h), lane j of the half-wave owns chain j of all 128 of its
-// outputs.  K chunks of 128 columns of both operands are staged in shared
-// memory (direct global->shared copies, double-buffered); the two half-waves
-// of a wave read the same token rows (broadcast) and different router rows.
-// The final tree runs as an exchange butterfly: at offset s the lanes with
-// bit s clear keep the lower half of their outputs, the others the upper half,
-// and each adds its partner's value; float addition is commutative, so every
+// then the tree 16/8/4/2/1 of gpu.cu:154-180 (qg_tree32).  Block = 16 waves
+// = 64 tokens x 32 rows; half-wave h of wave w owns 8 tokens (w % 8) x 8 rows
+// ((w / 8) * 2 + h), lane j of the half-wave owns chain j of all 64 of its
+// outputs (112 registers: four waves per SIMD hide the shared-memory reads).
+// K chunks of 128 columns of both operands are staged in shared memory
+// (direct global->shared copies, double-buffered); the two half-waves of a
+// wave read the same token rows (broadcast) and different router rows.  The
+// final tree runs as an exchange butterfly: at offset s the lanes with bit s
+// clear keep the lower half of their outputs, the others the upper half, and
+// each adds its partner's value; float addition is commutative, so every
 // output is the same sum, paired the same way, as lane 0's of qg_tree32.
-// Lane j ends with outputs 4j..4j+3 = token j/2, rows 4(j&1)..4(j&1)+3.
+// Lane j ends with outputs 2j, 2j+1 = token j/4, rows 2(j&3), 2(j&3)+1.
 constexpr int RT_TOK = 64, RT_ROWS = 32, RT_KC = 128;
+constexpr int RT_TT = 8;                          // tokens per half-wave (x 8 rows: RT_TT * 8 chains per lane)
+constexpr int RT_WAVES = (RT_TOK / RT_TT) * (RT_ROWS / 8) / 2;
 constexpr int RT_LDS = 2 * (RT_ROWS + RT_TOK) * RT_KC * 4;
 
 struct RouterArgs {
@@ -152,15 +155,16 @@ struct RouterArgs {
     float *logits;                   // [nt][rows]
 };
 
-__global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
+__global__ __launch_bounds__(64 * RT_WAVES) void pf_router_kernel(RouterArgs A) {
+    constexpr int NTG = RT_TOK / RT_TT, V = RT_TT / 4;  // token groups; outputs per lane after the tree
     extern __shared__ uint4 s_dyn[];
     float *sw = (float *)s_dyn;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, j = lane & 31;
-    const int tg = wave & 3, rg = (wave >> 2) * 2 + h;
+    const int tg = wave % NTG, rg = (wave / NTG) * 2 + h;
     const int t0 = blockIdx.x * RT_TOK, r0 = blockIdx.y * RT_ROWS, nch = A.D / RT_KC;
     auto stage = [&](int c, int b) {
         // 32 router rows then 64 token rows, 512 B each: 48 copies of two rows
-        for (int q = wave; q < (RT_ROWS + RT_TOK) / 2; q += 8) {
+        for (int q = wave; q < (RT_ROWS + RT_TOK) / 2; q += RT_WAVES) {
             const int R = 2 * q + h;
             const float *src;
             if (R < RT_ROWS) {
@@ -172,9 +176,9 @@ __global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
             dma16(src + (size_t)c * RT_KC + 4 * j, sw + (size_t)b * (RT_ROWS + RT_TOK) * RT_KC + q * 2 * RT_KC);
         }
     };
-    float acc[16][8];
+    float acc[RT_TT][8];
 #pragma unroll
-    for (int t = 0; t < 16; t++)
+    for (int t = 0; t < RT_TT; t++)
 #pragma unroll
         for (int r = 0; r < 8; r++) acc[t][r] = 0.0f;
     stage(0, 0);
@@ -183,16 +187,16 @@ __global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
         __syncthreads();
         if (c + 1 < nch) stage(c + 1, (c + 1) & 1);
         const float *W = sw + (size_t)(c & 1) * (RT_ROWS + RT_TOK) * RT_KC + rg * 8 * RT_KC;
-        const float *X = sw + (size_t)(c & 1) * (RT_ROWS + RT_TOK) * RT_KC + (RT_ROWS + tg * 16) * RT_KC;
+        const float *X = sw + (size_t)(c & 1) * (RT_ROWS + RT_TOK) * RT_KC + (RT_ROWS + tg * RT_TT) * RT_KC;
 #pragma unroll
         for (int i = 0; i < RT_KC / 32; i++) {
-            float wv[8], xv[16];
+            float wv[8], xv[RT_TT];
 #pragma unroll
             for (int r = 0; r < 8; r++) wv[r] = W[r * RT_KC + 32 * i + j];
 #pragma unroll
-            for (int t = 0; t < 16; t++) xv[t] = X[t * RT_KC + 32 * i + j];
+            for (int t = 0; t < RT_TT; t++) xv[t] = X[t * RT_KC + 32 * i + j];
 #pragma unroll
-            for (int t = 0; t < 16; t++)
+            for (int t = 0; t < RT_TT; t++)
 #pragma unroll
                 for (int r = 0; r < 8; r++) acc[t][r] = __builtin_fmaf(wv[r], xv[t], acc[t][r]);
         }
@@ -200,7 +204,7 @@ __global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
     // exchange butterfly over the 32 lanes of the half-wave; v[o], o = 8t + r
     float *v = &acc[0][0];
 #pragma unroll
-    for (int s = 16, n = 128; s >= 1; s >>= 1, n >>= 1) {
+    for (int s = 16, n = 8 * RT_TT; s >= 1; s >>= 1, n >>= 1) {
         const bool up = (j & s) != 0;
 #pragma unroll
         for (int q = 0; q < n / 2; q++) {
@@ -209,11 +213,12 @@ __global__ __launch_bounds__(512, 1) void pf_router_kernel(RouterArgs A) {
             v[q] = (up ? v[q + n / 2] : v[q]) + recv;
         }
     }
-    const int t = t0 + tg * 16 + (j >> 1);
+    // lane j holds outputs o = V j .. V j + V - 1
+    const int t = t0 + tg * RT_TT + (V * j) / 8;
     if (t < A.nt) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int r = r0 + rg * 8 + 4 * (j & 1) + q;
+        for (int q = 0; q < V; q++) {
+            const int r = r0 + rg * 8 + (V * j) % 8 + q;
             if (r < A.rows) A.logits[(size_t)t * A.rows + r] = A.bias && r < QG_EXPERTS ? v[q] + A.bias[r] : v[q];
         }
     }
@@ -586,10 +591,11 @@ QG_DEV ItemRange balanced_items(const TileTable *tt, const int *s_tb, int seg_lo
     __shared__ int s_res[2];
     const int t_lo = tt->bounds[seg_lo], t_hi = tt->bounds[seg_hi], m_lo = tt->mbounds[seg_lo];
     const long long total_cost = (long long)nblk * (CA * (long long)(t_hi - t_lo) + CB * (long long)(tt->mbounds[seg_hi] - m_lo));
-    const int x = blockIdx.x & 7, slot = blockIdx.x >> 3, n_x = (gridDim.x - x + 7) >> 3;
-    constexpr int parts = 8;
+    // one part per XCD (a grid of fewer than 8 workgroups: one per workgroup)
+    const int parts = min(8, (int)gridDim.x);
+    const int x = blockIdx.x % parts, slot = blockIdx.x / parts, n_x = (gridDim.x - x + parts - 1) / parts;
     // first item of parts x and x + 1: the first item whose price prefix
-    // reaches ceil(total_cost * q / 8)
+    // reaches ceil(total_cost * q / parts)
     long long Q[2];
 #pragma unroll
     for (int k = 0; k < 2; k++) Q[k] = (total_cost * (x + k) + parts - 1) / parts;
@@ -1592,7 +1598,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     }
     // P1: router logits in the reference's order (+ shared gate row, + bias)
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, L->router_bias, logits};
-    pf_launch(0, pf_router_kernel, dim3((nt + RT_TOK - 1) / RT_TOK, (rows + RT_ROWS - 1) / RT_ROWS), dim3(512), RT_LDS, s, R);
+    pf_launch(0, pf_router_kernel, dim3((nt + RT_TOK - 1) / RT_TOK, (rows + RT_ROWS - 1) / RT_ROWS), dim3(64 * RT_WAVES), RT_LDS, s, R);
     if ((rc = hipGetLastError())) return rc;
     const int split = tl_pf_split;
     const bool i8 = split == 1;
