@@ -258,13 +258,20 @@ QG_DEV void token_planes_i8(const float *xr, int D, int lane, int8_t *hi, int8_t
     }
 }
 
-// One wave per token: top-10 of the (biased) logits, coverage/prune, flags;
-// then the token's fp16 hi/lo planes and 32-group sum planes.
-__global__ __launch_bounds__(256) void pf_route_kernel(RouteArgs A) {
+// Two waves per token (block = 4 tokens): wave w < 4 routes token 4b + w
+// (top-10 of the (biased) logits, coverage/prune, flags) while wave w + 4
+// writes its fp16 hi/lo planes and 32-group sum planes.
+__global__ __launch_bounds__(512) void pf_route_kernel(RouteArgs A) {
     __shared__ float s_rv[4][64];
     __shared__ int s_ri[4][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + wave;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + (wave & 3);
     if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
+    if (wave >= 4) {  // the token's activation planes, beside its routing
+        _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
+        token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
+        if (A.xi8) token_planes_i8(A.x + (size_t)t * A.D, A.D, lane, A.xi8 + (size_t)t * 2 * A.D, A.xi8 + (size_t)t * 2 * A.D + A.D, A.xsc + t);
+        return;
+    }
     int id, missing;
     float wv;
     double mass;
@@ -280,9 +287,6 @@ __global__ __launch_bounds__(256) void pf_route_kernel(RouteArgs A) {
         A.mass[t] = mass;
         if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
     }
-    _Float16 *hi = A.xp + (size_t)t * 2 * A.D, *shi = A.xsp + (size_t)t * 2 * (A.D / 32);
-    token_planes(A.x + (size_t)t * A.D, A.D, false, 1.0f, lane, hi, hi + A.D, shi, shi + A.D / 32, nullptr);
-    if (A.xi8) token_planes_i8(A.x + (size_t)t * A.D, A.D, lane, A.xi8 + (size_t)t * 2 * A.D, A.xi8 + (size_t)t * 2 * A.D + A.D, A.xsc + t);
 }
 
 // ---------------- P3: offsets, chunk bases, tile table ----------------
@@ -1606,7 +1610,7 @@ int qg_prefill_forward(float *out, float *resid, int *ids, float *weights, unsig
     float *xsc = i8 ? (float *)(ws + lay.xsc) : nullptr, *row_sx = i8 ? (float *)(ws + lay.row_sx) : nullptr;
     RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, flag,
                  (int *)(ws + lay.missing), (double *)(ws + lay.mass), x, D, xp, xsp, xi8, xsc};
-    pf_launch(1, pf_route_kernel, dim3((nt + 3) / 4), dim3(256), 0, s, RA);
+    pf_launch(1, pf_route_kernel, dim3((nt + 3) / 4), dim3(512), 0, s, RA);
     if ((rc = hipGetLastError())) return rc;
     pf_launch(10, pf_count_kernel, dim3(nch), dim3(512), 0, s, counts, (int *)nullptr, (const int *)ids, (const int *)flag, nt);
     if ((rc = hipGetLastError())) return rc;
