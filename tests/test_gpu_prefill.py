@@ -186,6 +186,34 @@ def test_prefill_dense_split_launches(layer3, layer1, mode):
         qg.lib().qg_prefill_int8_dense(prev)
 
 
+def test_prefill_concentrated_routing(qgl):
+    """A router bias that sends nearly every token to the same few experts:
+    six experts take over 2000 of the 2048 tokens (32 tiles each, the same
+    row-count bucket, so their pass order falls back to expert id), ten more
+    share most of the remaining selections and the tail reaches the other
+    experts; the shared expert sits after the dense ones, and the XCD shares
+    are cut inside such groups.  Routing bit-exact, sampled rows against the
+    oracle."""
+    spec = synth.LayerSpec(seed=207, gate_type=12, up_type=12, down_type=20, shared=True, sh_types=(12, 12, 12))
+    bias = np.zeros(512, np.float32)
+    rng = np.random.default_rng(207)
+    hot = rng.choice(512, 16, replace=False)
+    bias[hot[:6]] = 6.0
+    bias[hot[6:]] = 3.0
+    L = synth.build_layer(spec)
+    L.bufs["router_bias"] = Device(bias)
+    L.desc.router_bias = L.bufs["router_bias"].p
+    H = O.HostLayer(spec.seed, width=spec.width, ff=spec.ff, gt=spec.gate_type, ut=spec.up_type, dt=spec.down_type,
+                    shared=spec.shared, sh_types=spec.sh_types, router_bias=bias)
+    x = synth.inputs(3207, 2048, spec.width)
+    fw = forward(L, x)
+    ids, _, _ = check_routing(fw, H, x)
+    n = np.bincount(ids.ravel(), minlength=512)
+    say(f"  per-expert rows: top {np.sort(n)[::-1][:8].tolist()}, >=256: {(n >= 256).sum()}, touched {(n > 0).sum()}")
+    assert (n >= 2000).sum() == 6 and (n >= 256).sum() >= 16, "six hot experts, ten warm ones"
+    check_outputs(fw, L, H, x, sample_rows(2048, 32, 11), "concentrated routing, B=2048")
+
+
 @pytest.mark.parametrize("nt", [18, 33, 100])
 def test_prefill_q4k_down_every_token(layer0, nt):
     """Config-0 formats (Q4_K down, min terms in both products), every row checked;
