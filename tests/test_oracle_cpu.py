@@ -461,3 +461,24 @@ def test_tensor_bytes_host_logic():
     assert tb(12, (2560, 0, 1, 1)) is None          # zero dim
     assert tb(0, (1 << 30, 1 << 30, 1 << 30, 1)) is None  # overflow
     assert tb(99, (256, 1, 1, 1)) is None           # unknown type
+
+
+def test_prefill_launch_mode_switch_host_logic():
+    """qg_prefill_int8_dense: a per-thread setting (0 one gate/up launch, 1
+    the dense experts split off on int8, 2 split off on fp16; other values
+    select 0) that returns the previous mode.  Host state only, so it runs
+    without a GPU."""
+    gpu = ROOT / "nebula_amd" / "lib" / "libqwen_gpu.so"
+    if not gpu.exists():
+        pytest.skip("native libraries not built")
+    from nebula_amd import qg
+    lib = qg.lib()
+    prev = lib.qg_prefill_int8_dense(0)
+    try:
+        assert lib.qg_prefill_int8_dense(2) == 0
+        assert lib.qg_prefill_int8_dense(1) == 2
+        assert lib.qg_prefill_int8_dense(7) == 1
+        assert lib.qg_prefill_int8_dense(-1) == 0
+        assert lib.qg_prefill_int8_dense(0) == 0
+    finally:
+        lib.qg_prefill_int8_dense(prev)
