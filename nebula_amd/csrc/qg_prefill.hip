@@ -850,13 +850,13 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
 // 72 bytes of it start at byte offset delta = address % 16 (an even value)
 // of its first piece, so 6 pieces hold them.
 constexpr int IQ_KC = 128;                          // K elements per step
-constexpr int IQ_PIECES = 6;                        // 16-byte pieces per weight row and step
-constexpr int IQ_ROWB = IQ_PIECES * 16;
-constexpr int IQ_COPIES = 32 * IQ_PIECES / 64;      // direct copies per wave and step
-constexpr int IQ_SLOT = 32 * IQ_ROWB;               // bytes per wave and slot
+constexpr int IQ_PIECES = 5;                        // 16-byte pieces per weight row and step (72 bytes from an even offset)
+constexpr int IQ_ROWB = IQ_PIECES * 16;             // 20 dwords: the 16 rows of a fragment read hit distinct banks
+constexpr int IQ_COPIES = 3;                        // direct copies per wave and step
+constexpr int IQ_SLOT = IQ_COPIES * 64 * 16;        // bytes per wave and slot (rows use 32 x 80)
 constexpr int IQ_STAGE = PT * 2 * IQ_KC * 2;        // [64 rows][2 planes][128] fp16
 constexpr int PF_IQ_LDS = 2 * IQ_STAGE + PF_WAVES * 3 * IQ_SLOT;
-static_assert(IQ_COPIES * 64 == 32 * IQ_PIECES, "the copies cover the slot exactly");
+static_assert(32 * IQ_PIECES <= IQ_COPIES * 64, "the copies cover the slot");
 
 // Activation stage of one 128-element K chunk: [row][plane][16 chunks of 16
 // bytes], chunk position c ^ (row & 15); one copy covers two rows.
@@ -950,12 +950,12 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
     int w_p[IQ_COPIES];
     const uint8_t *wrow[IQ_COPIES];
 #pragma unroll
-    for (int t = 0; t < IQ_COPIES; t++) w_p[t] = (t * 64 + lane) % IQ_PIECES;
+    for (int t = 0; t < IQ_COPIES; t++) w_p[t] = min(t * 64 + lane, 32 * IQ_PIECES - 1) % IQ_PIECES;
     auto set_wc = [&](const PfItem &it) {
         size_t rb;
         const uint8_t *w = wave_rows(it, rb);
 #pragma unroll
-        for (int t = 0; t < IQ_COPIES; t++) wrow[t] = w + (size_t)((t * 64 + lane) / IQ_PIECES) * rb;
+        for (int t = 0; t < IQ_COPIES; t++) wrow[t] = w + (size_t)(min(t * 64 + lane, 32 * IQ_PIECES - 1) / IQ_PIECES) * rb;
     };
     // step kc of the item being copied into slot q: piece p of a row is the
     // p-th 16-byte piece from the row's first aligned one; pieces past its
