@@ -847,10 +847,11 @@ __global__ __launch_bounds__(512, 1) void pf_down_kernel(DnArgs A) {
 // its 32 weight rows' bytes of a step as whole 16-byte pieces (three direct
 // copies of 64 lanes) into one of three slots of its own ring and reads them
 // back from shared memory.  A step is 128 K elements (4 blocks); a row's
-// 72 bytes of it start at byte offset delta = address % 16 (an even value)
-// of its first piece, so 6 pieces hold them.
+// 72 bytes of it start at byte offset delta = address % 16 of its first
+// piece, and delta is 0 or 8 (rows are 72 k bytes for F = 128 k, the tensors
+// 16-byte aligned), so 5 pieces hold them.
 constexpr int IQ_KC = 128;                          // K elements per step
-constexpr int IQ_PIECES = 5;                        // 16-byte pieces per weight row and step (72 bytes from an even offset)
+constexpr int IQ_PIECES = 5;                        // 16-byte pieces per weight row and step (72 bytes from offset 0 or 8)
 constexpr int IQ_ROWB = IQ_PIECES * 16;             // 20 dwords: the 16 rows of a fragment read hit distinct banks
 constexpr int IQ_COPIES = 3;                        // direct copies per wave and step
 constexpr int IQ_SLOT = IQ_COPIES * 64 * 16;        // bytes per wave and slot (rows use 32 x 80)
