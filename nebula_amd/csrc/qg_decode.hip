@@ -820,13 +820,14 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
 // the 4 waves takes 16 rows (MFMA columns).  Results go to the selection's
 // slot, weighted by its routing weight (shared rows unweighted); the combine
 // kernel sums the slots in router-rank order.
-template <int FMT, int SFMT>
+template <int FMT, int SFMT, int FF>
 __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     __shared__ int s_e, s_n;
     __shared__ int s_list[MB];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
-    const int F = A.F, sh = A.sh_down != nullptr ? 1 : 0;
+    constexpr int F = FF;  // the layer's F (512 or 640): a constant, so the staging splits need no division
+    const int sh = A.sh_down != nullptr ? 1 : 0;
     const int dblocks = A.D / DN_ROWS;
     const int rbmax = (int)(A.rb > A.sh_rb ? A.rb : A.sh_rb);
     const int slab = (DN_ROWS * rbmax + 1023) & ~1023;
@@ -1137,12 +1138,18 @@ bool dec_ok(const qg_moe_layer *L) {
     return true;
 }
 
-void launch_down(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStream_t s) {
+template <int FF>
+void launch_down_f(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStream_t s) {
     const dim3 block(256);
-    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_IQ4_NL>, grid, block, lds, s, DA);
-    else if (fr == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_Q4_K>, grid, block, lds, s, DA);
-    else if (fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_Q4_K, QT_IQ4_NL>, grid, block, lds, s, DA);
-    else dec_launch(3, dec_down_kernel<QT_Q4_K, QT_Q4_K>, grid, block, lds, s, DA);
+    if (fr == QT_IQ4_NL && fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_IQ4_NL, FF>, grid, block, lds, s, DA);
+    else if (fr == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_IQ4_NL, QT_Q4_K, FF>, grid, block, lds, s, DA);
+    else if (fs == QT_IQ4_NL) dec_launch(3, dec_down_kernel<QT_Q4_K, QT_IQ4_NL, FF>, grid, block, lds, s, DA);
+    else dec_launch(3, dec_down_kernel<QT_Q4_K, QT_Q4_K, FF>, grid, block, lds, s, DA);
+}
+// F is 512 or 640 on this path (dec_ok)
+void launch_down(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStream_t s) {
+    if (DA.F == 512) launch_down_f<512>(DA, fr, fs, grid, lds, s);
+    else launch_down_f<640>(DA, fr, fs, grid, lds, s);
 }
 
 template <int DW>
