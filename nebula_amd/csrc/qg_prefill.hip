@@ -945,7 +945,10 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
         const uint8_t *bw = it.shared ? A.sh_down : A.down + (size_t)it.g * A.D * A.rb;
         return bw + (size_t)(it.blk * DN_DB + wave * 32) * rb;
     };
-    auto nblocks = [&](int kc) { return min(4, F / 32 - 4 * kc); };
+    // F is a multiple of 128 (checked at launch), so every 128-wide step holds
+    // 4 blocks; a constant count lets the block loops unroll without exits
+    constexpr int NB = IQ_KC / 32;
+    auto nblocks = [&](int) { return NB; };
     // Weight copies: piece i = 64 t + lane of a slot is piece p of the wave's
     // row r; wrow[t] is that row in the item being copied.
     int w_p[IQ_COPIES];
