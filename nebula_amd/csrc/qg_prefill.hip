@@ -1051,8 +1051,8 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
             }
             if (s + 2 < steps) {
                 // step s + 2 is step kc + 2 of this item or of the next one(s)
-                const int kc2 = (kc + 2) % nkc;
-                if (kc2 == 0) set_wc(R.at(k + (kc + 2) / nkc));  // it starts a later item
+                const int kr = kc + 2 - nkc, kc2 = kr < 0 ? kc + 2 : nkc == 1 ? 0 : kr;
+                if (kc2 == 0) set_wc(R.at(k + (kr < 0 ? 0 : nkc == 1 ? 2 : 1)));  // it starts a later item
                 copy_w(qn, kc2);
             }
             int del[NCT];
