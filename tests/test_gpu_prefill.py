@@ -225,6 +225,23 @@ def test_prefill_q4k_down_every_token(layer0, nt):
     check_outputs(fw, L, H, x, np.arange(nt), f"config0 B={nt}")
 
 
+@pytest.mark.parametrize("ff,shared", [(128, False), (256, True)])
+def test_prefill_narrow_ff_step_counts(ff, shared):
+    """F = 128 and 256 at D = 1024: the down items have one or two K steps, so
+    the weight copies two steps ahead belong to the next item or the one after
+    (F = 128), and the Q4_K shared down (F = 256) has a single superblock step;
+    every row checked."""
+    spec = synth.LayerSpec(seed=430 + ff, width=1024, ff=ff, gate_type=12, up_type=12, down_type=20, shared=shared,
+                           sh_types=(12, 12, 12))
+    say(f"building a 1024/{ff} layer on device")
+    L, H = synth.build_layer(spec), host_layer(spec)
+    nt = 150
+    x = synth.inputs(440 + ff, nt, 1024, correlated=True)
+    fw = forward(L, x)
+    check_routing(fw, H, x)
+    check_outputs(fw, L, H, x, np.arange(nt), f"1024/{ff} B={nt}")
+
+
 def test_prefill_shared_expert_mixed_formats(layer1):
     """Config-1 formats: IQ4_NL routed down, Q4_K shared down (its own down
     launch), sigmoid-gated shared expert on every token; correlated rows give
