@@ -927,7 +927,7 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
     }
     const int ndb = A.D / DN_DB, F = A.F, nkc = (F + IQ_KC - 1) / IQ_KC;
     const int t_lo = A.tt->bounds[A.seg_lo], total = (A.tt->bounds[A.seg_hi] - t_lo) * ndb;
-    const ItemRange ir = balanced_items<10, 3>(A.tt, s_tb, A.seg_lo, A.seg_hi, ndb);
+    const ItemRange ir = balanced_items<7, 3>(A.tt, s_tb, A.seg_lo, A.seg_hi, ndb);
     const int nitems = range_count(ir), steps = nitems * nkc;
     if (steps == 0) return;  // block-uniform
     const ItemRing R{s_it, s_tb, s_go, s_off, A.nt, t_lo, ndb, nitems, ir};
