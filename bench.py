@@ -560,7 +560,8 @@ def main() -> int:
         return counter_pass(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the layer; --gpus {args.gpus} is not supported "
-              "(this build runs on one MI355X; the multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+              "(this build runs on one MI355X; sharding the layer over several GPUs is designed, not built)",
+              file=sys.stderr)
         return 2
     data = "synthetic (seeded N(0,0.02) weights quantised to Q4_K/IQ4_NL on the device; seeded RMS-normed inputs)"
     if args.matmul:
