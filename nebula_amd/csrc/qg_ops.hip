@@ -118,10 +118,10 @@ template <> struct MmTile<8> { static constexpr int KC = 1024; };
 template <> struct MmTile<16> { static constexpr int KC = 512; };
 template <> struct MmTile<20> { static constexpr int KC = 512; };
 
-template <int TYPE, int TT, int RPL>
+template <int TYPE, int TT, int RPL, int KCO = 0>
 __global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, const uint8_t *__restrict__ w, int rows,
                                                      int cols, const float *__restrict__ x, int nt, size_t stride) {
-    constexpr int KC = MmTile<TT>::KC, RB = 8 * RPL;  // chunk columns; rows per block
+    constexpr int KC = KCO ? KCO : MmTile<TT>::KC, RB = 8 * RPL;  // chunk columns; rows per block
     constexpr int WB = KC / 256 * 144;                                       // chunk bytes of a row
     constexpr int NS = TYPE == QT_Q4_K ? RB * (KC / 256) * 8 : RB * (KC / 32);  // scale entries per chunk
     __shared__ __attribute__((aligned(16))) float xs[TT * KC];    // [token][k], row stride kc
@@ -237,6 +237,10 @@ void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const floa
     const int ty = (nt + TT - 1) / TT;
     if (TT >= 16 && ((rows + 15) / 16) * ty >= 512)
         mm_tile_kernel<TYPE, TT, 2><<<dim3((rows + 15) / 16, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    else if (TT == 1 && cols <= 2560)
+        // one chunk of at most 2560 columns: a third less shared memory than
+        // the 4096-column chunk, so 5 blocks per CU stay resident instead of 3
+        mm_tile_kernel<TYPE, 1, 1, 2560><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
     else
         mm_tile_kernel<TYPE, TT, 1><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
 }
