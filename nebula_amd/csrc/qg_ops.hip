@@ -241,6 +241,9 @@ void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const floa
         // one chunk of at most 2560 columns: a third less shared memory than
         // the 4096-column chunk, so 5 blocks per CU stay resident instead of 3
         mm_tile_kernel<TYPE, 1, 1, 2560><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    else if (TT == 1 && cols > 4096 && cols <= 6144)
+        // one chunk instead of two (one copy round trip per block)
+        mm_tile_kernel<TYPE, 1, 1, 6144><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
     else
         mm_tile_kernel<TYPE, TT, 1><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
 }
