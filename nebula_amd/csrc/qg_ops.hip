@@ -237,6 +237,10 @@ void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const floa
     const int ty = (nt + TT - 1) / TT;
     if (TT >= 16 && ((rows + 15) / 16) * ty >= 512)
         mm_tile_kernel<TYPE, TT, 2><<<dim3((rows + 15) / 16, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    else if ((TT == 4 || TT == 8) && cols <= 2560)
+        // two 1280-column chunks: 5 (4 tokens) or 3 (8 tokens) blocks per CU
+        // instead of 3 or 4, at the same or fewer copy rounds
+        mm_tile_kernel<TYPE, TT, 1, 1280><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
     else if (TT == 1 && cols <= 2560)
         // one chunk of at most 2560 columns: a third less shared memory than
         // the 4096-column chunk, so 5 blocks per CU stay resident instead of 3
