@@ -235,21 +235,33 @@ __global__ __launch_bounds__(256) void mm_tile_kernel(float *__restrict__ out, c
 template <int TYPE, int TT>
 void launch_mm_tile(float *out, const uint8_t *w, int rows, int cols, const float *x, int nt, size_t stride, hipStream_t s) {
     const int ty = (nt + TT - 1) / TT;
-    if (TT >= 16 && ((rows + 15) / 16) * ty >= 512)
-        mm_tile_kernel<TYPE, TT, 2><<<dim3((rows + 15) / 16, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
-    else if ((TT == 4 || TT == 8) && cols <= 2560)
-        // two 1280-column chunks: 5 (4 tokens) or 3 (8 tokens) blocks per CU
-        // instead of 3 or 4, at the same or fewer copy rounds
-        mm_tile_kernel<TYPE, TT, 1, 1280><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
-    else if (TT == 1 && cols <= 2560)
-        // one chunk of at most 2560 columns: a third less shared memory than
-        // the 4096-column chunk, so 5 blocks per CU stay resident instead of 3
-        mm_tile_kernel<TYPE, 1, 1, 2560><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
-    else if (TT == 1 && cols > 4096 && cols <= 6144)
-        // one chunk instead of two (one copy round trip per block)
-        mm_tile_kernel<TYPE, 1, 1, 6144><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
-    else
-        mm_tile_kernel<TYPE, TT, 1><<<dim3((rows + 7) / 8, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+    const dim3 g8((rows + 7) / 8, ty);
+    if constexpr (TT >= 16) {
+        if (((rows + 15) / 16) * ty >= 512) {
+            mm_tile_kernel<TYPE, TT, 2><<<dim3((rows + 15) / 16, ty), 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+            return;
+        }
+    } else if constexpr (TT == 1) {
+        if (cols <= 2560) {
+            // one chunk of at most 2560 columns: a third less shared memory than
+            // the 4096-column chunk, so 5 blocks per CU stay resident instead of 3
+            mm_tile_kernel<TYPE, 1, 1, 2560><<<g8, 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+            return;
+        }
+        if (cols > 4096 && cols <= 6144) {
+            // one chunk instead of two (one copy round trip per block)
+            mm_tile_kernel<TYPE, 1, 1, 6144><<<g8, 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+            return;
+        }
+    } else {
+        if (cols <= 2560) {
+            // two 1280-column chunks: 5 (4 tokens) or 3 (8 tokens) blocks per CU
+            // instead of 3 or 4, at the same or fewer copy rounds
+            mm_tile_kernel<TYPE, TT, 1, 1280><<<g8, 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
+            return;
+        }
+    }
+    mm_tile_kernel<TYPE, TT, 1><<<g8, 256, 0, s>>>(out, w, rows, cols, x, nt, stride);
 }
 
 template <int TYPE>
