@@ -25,7 +25,8 @@ before the timed region.
             GB/s; cpu_baseline = the reference's qc_matmul.
 
 Printed: one JSON line.  value = tokens/s (batch / step time), the step being
-one replay of the layer's captured graph; roofline = the gate/up kernel's
+one layer forward inside a captured graph of the whole 16-layer rotation
+(replayed back to back); roofline = the gate/up kernel's
 algorithmic bytes over its average duration, from HIP events recorded by the
 kernel dispatches themselves on the library's launch stream
 (hipExtLaunchKernelGGL) over the same number of eagerly launched steps; cpu_baseline = the reference's own
@@ -76,22 +77,21 @@ def gateup_bytes(nt: int, unique: float, shared: bool) -> float:
     return (unique + (1 if shared else 0)) * GATEUP_BYTES + nt * D * 4
 
 
-def resident_set(layer: synth.DeviceLayer, seed: int, count: int = 128) -> np.ndarray:
-    """Config 4's resident experts: the `count` with the largest routed-weight
-    mass over 4096 seeded synthetic tokens (ties to the lower id)."""
-    xs = synth.inputs(seed, 4096, D)
+def resident_set(layer: synth.DeviceLayer, batch_seed: int, noise_seed: int, count: int = 128) -> np.ndarray:
+    """Config 4's resident experts: the `count` best-ranked over 4096 seeded
+    synthetic tokens from 8 correlated contexts, one of them the verify
+    batch's own (synth.ranking_inputs), routed on the device, ranked by the
+    reference's rule: activation count, then routed weight, then id
+    (synth.resident_ranking, qwen/README.md:38)."""
+    xs = synth.ranking_inputs(batch_seed, noise_seed, width=D)
+    n = xs.shape[0]
     dx = qg.Device(xs)
-    logits = qg.Device(shape=(4096, EXPERTS), dtype=np.float32)
-    ids = qg.Device(shape=(4096, TOP), dtype=np.int32)
-    w = qg.Device(shape=(4096, TOP), dtype=np.float32)
-    qg.call("matmul", logits.p, layer.bufs["router"].p, 0, EXPERTS, D, dx.p, 4096)
-    qg.call("route", ids.p, w.p, logits.p, 4096)
-    score = np.zeros(EXPERTS)
-    np.add.at(score, ids.get().ravel(), w.get().ravel().astype(np.float64))
-    order = np.lexsort((np.arange(EXPERTS), -score))
-    mask = np.zeros(EXPERTS, np.uint8)
-    mask[order[:count]] = 1
-    return mask
+    logits = qg.Device(shape=(n, EXPERTS), dtype=np.float32)
+    ids = qg.Device(shape=(n, TOP), dtype=np.int32)
+    w = qg.Device(shape=(n, TOP), dtype=np.float32)
+    qg.call("matmul", logits.p, layer.bufs["router"].p, 0, EXPERTS, D, dx.p, n)
+    qg.call("route", ids.p, w.p, logits.p, n)
+    return synth.resident_ranking(ids.get(), w.get(), count)
 
 
 class Workload:
@@ -105,7 +105,7 @@ class Workload:
         for s in self.specs:
             L = synth.build_layer(s)
             if config == 4:
-                mask = resident_set(L, seed=s.seed + 77)
+                mask = resident_set(L, batch_seed=seed + 1000, noise_seed=s.seed + 77)
                 L.bufs["resident"] = qg.Device(mask)
                 L.desc.resident, L.desc.threshold = L.bufs["resident"].p, 0.10
             self.layers.append(L)
@@ -131,38 +131,44 @@ class Workload:
         return len(np.unique(ids[ok]))
 
 
-def capture_graphs(wl: Workload) -> list:
-    """One captured graph per rotated layer: a step replays the layer's kernels
-    with one host call, as a serving loop would (qwen.c captures per batch
-    size, qwen.c:726-734)."""
-    graphs = []
-    for i in range(len(wl.layers)):
-        g = C.c_void_p()
-        qg.call("graph_begin", C.byref(g))
+def capture_steps(wl, layers) -> C.c_void_p:
+    """One captured graph of consecutive layer forwards (rotated layers
+    `layers`, in order): a replay runs them back to back with one host call,
+    as a serving loop replays a whole captured decode step (qwen.c:726-734
+    captures per batch size), so the device time per layer is measured rather
+    than the host's graph-launch rate."""
+    g = C.c_void_p()
+    qg.call("graph_begin", C.byref(g))
+    for i in layers:
         wl.step(i)
-        qg.call("graph_end", g)
-        graphs.append(g)
-    return graphs
+    qg.call("graph_end", g)
+    return g
 
 
 def time_decode(wl: Workload, steps: int, warmup: int):
-    """Step time over `steps` timed graph replays, then the average duration of
-    each kernel of the step from dispatch-timestamped events (qg_moe_kernel_events,
+    """Step time over exactly `steps` timed layer forwards: steps // n replays
+    of one graph of all n rotated layers, then one graph of the first
+    steps % n; then the average duration of each kernel of the step from
+    dispatch-timestamped events (qg_moe_kernel_events,
     hipExtLaunchKernelGGL) over the same number of eagerly launched steps."""
-    graphs = capture_graphs(wl)
-    n = len(graphs)
-    for i in range(warmup):
-        qg.call("graph_launch", graphs[i % n])
+    n = len(wl.layers)
+    full = capture_steps(wl, range(n))
+    part = capture_steps(wl, range(steps % n)) if steps % n else None
+    for _ in range(max(1, -(-warmup // n))):
+        qg.call("graph_launch", full)
     qg.call("sync")
     b, e = qg.Event(), qg.Event()
     b.record()
-    for i in range(steps):
-        qg.call("graph_launch", graphs[i % n])
+    for _ in range(steps // n):
+        qg.call("graph_launch", full)
+    if part is not None:
+        qg.call("graph_launch", part)
     e.record()
     qg.call("sync")
     ms = qg.elapsed_ms(b, e) / steps
-    for g in graphs:
-        qg.lib().qg_graph_destroy(g)
+    for g in (full, part):
+        if g is not None:
+            qg.lib().qg_graph_destroy(g)
     return ms, kernel_times(wl.step, KERNELS, steps)
 
 
@@ -310,8 +316,10 @@ def cpu_baseline(wl, budget_s: float, tokens: int | None = None) -> dict | None:
             "host": hc, "isa": ref.qc_backend_name().decode()}
 
 
-def bench_stack(args) -> dict:
-    """Config 2: 48 seeded config-0 layers, one token, replayed as one graph."""
+def bench_stack(args, cpu_budget: float | None = None) -> dict:
+    """Config 2: 48 seeded config-0 layers, one token, replayed as one graph.
+    With cpu_budget, also the reference's cpu.c on the same stack
+    (cpu_stack_baseline)."""
     n_layers = args.layers if args.layers != 16 else 48
     specs = [synth.LayerSpec(seed=9000 + l) for l in range(n_layers)]
     layers = [synth.build_layer(s) for s in specs]
@@ -338,7 +346,83 @@ def bench_stack(args) -> dict:
     ms = qg.elapsed_ms(b, e) / steps
     h.nm_stack_destroy(stack)
     nbytes = n_layers * layer_bytes(1, 10, False)
-    return {"ms": ms, "layers": n_layers, "bytes": nbytes, "steps": steps}
+    r = {"ms": ms, "layers": n_layers, "bytes": nbytes, "steps": steps}
+    if cpu_budget:
+        r["cpu"] = cpu_stack_baseline(layers, arr, x0, cpu_budget)
+    return r
+
+
+def cpu_stack_baseline(layers, arr, x0: np.ndarray, budget_s: float) -> dict | None:
+    """The reference's cpu.c on the config-2 stack, one token: per layer
+    h <- h + qc_moe(RMSNorm(h)) after the router's qc_matmul, over all 48
+    layers.  Each layer's routing is the GPU stack's own (a recorded eager
+    forward from the same input; the reference's CPU MoE receives its ids
+    from the GPU, qwen.c:665-669), and only the 10 routed experts of a layer
+    are copied to the host, renumbered 0..9 (qc_moe's work depends only on
+    the selected experts)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    try:
+        import oracle as O
+    except Exception:
+        return None
+    ref = O.ref_lib(D)
+    if ref is None:
+        return None
+    n_layers = len(layers)
+    h = qg.host()
+    rec = h.nm_stack_create(arr, n_layers, 1, 1)
+    if not rec:
+        raise RuntimeError(h.nm_last_error().decode())
+    qg.call("write", h.nm_stack_hidden(rec), x0.ctypes.data, x0.nbytes)
+    if h.nm_stack_forward(rec, 1, 0):
+        raise RuntimeError(h.nm_last_error().decode())
+    qg.call("sync")
+    per = {"gate": FF * qg.row_bytes(12, D), "up": FF * qg.row_bytes(12, D), "down": D * qg.row_bytes(12, FF)}
+    cpu_layers = []
+    for l, L in enumerate(layers):
+        pi, pw = C.c_void_p(), C.c_void_p()
+        if h.nm_stack_record(rec, l, None, C.byref(pi), C.byref(pw), None):
+            raise RuntimeError(h.nm_last_error().decode())
+        ids = np.empty((1, TOP), np.int32)
+        w = np.empty((1, TOP), np.float32)
+        qg.call("read", ids.ctypes.data, pi.value, ids.nbytes)
+        qg.call("read", w.ctypes.data, pw.value, w.nbytes)
+        host = {k: np.empty(TOP * v, np.uint8) for k, v in per.items()}
+        for slot, ex in enumerate(ids[0]):
+            for k in host:
+                host[k][slot * per[k]:(slot + 1) * per[k]] = synth.read_expert(L, k, int(ex))
+        router = np.empty(EXPERTS * D * 4, np.uint8)
+        qg.call("read", router.ctypes.data, L.bufs["router"].p, router.nbytes)
+        cpu_layers.append((router, host, np.arange(TOP, dtype=np.int32)[None, :].copy(), w))
+    h.nm_stack_destroy(rec)
+    threads = cpu_threads()
+    ws = ref.qc_create(1, threads)
+    logits = np.empty((1, EXPERTS), np.float32)
+    out = np.empty((1, D), np.float32)
+
+    def run():
+        hs = x0.astype(np.float32).copy()
+        for router, host, ids, w in cpu_layers:
+            xn = synth.rmsnorm(hs)
+            assert ref.qc_matmul(logits.ctypes.data, router.ctypes.data, 0, EXPERTS, D, xn.ctypes.data, 1, threads) == 0
+            assert ref.qc_moe(ws, out.ctypes.data, xn.ctypes.data, ids.ctypes.data, w.ctypes.data, 1,
+                              host["gate"].ctypes.data, 12, host["up"].ctypes.data, 12, host["down"].ctypes.data, 12) == 0
+            hs += out
+    for _ in range(3):
+        run()
+    times, t_end = [], time.time() + budget_s
+    while len(times) < 20 or (time.time() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    ref.qc_destroy(ws)
+    med = float(np.median(times))
+    hc = host_cpus()
+    return {"value": round(1 / med, 2), "unit": "tokens/s", "ms_per_token": round(med * 1e3, 3), "cores": threads,
+            "kind": "reference",
+            "sample": f"cpu.c router qc_matmul + qc_moe per layer over the {n_layers}-layer stack, 1 token, the GPU "
+                      f"stack's routing, isa={ref.qc_backend_name().decode()}; median of {len(times)} runs after 3 "
+                      f"warm-ups; {threads} OpenMP threads on {hc['physical_cores']} physical cores, {hc['model']}"}
 
 
 class PrefillWorkload:
@@ -432,7 +516,7 @@ def bench_prefill(args, data: str) -> dict:
         "cpu_baseline": None,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget, tokens=min(nt, 128))
+        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
     return line
 
 
@@ -583,7 +667,7 @@ def main() -> int:
         return 2
 
     if args.config == 2:
-        r = bench_stack(args)
+        r = bench_stack(args, None if args.no_cpu else args.cpu_budget)
         ms = r["ms"]
         line = {
             "metric": METRIC, "value": round(1 / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
@@ -595,7 +679,7 @@ def main() -> int:
                        "stack_hbm_GBps": round(r["bytes"] / (ms * 1e-3) / 1e9, 1),
                        "stack_hbm_frac": round(r["bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                        "us_per_layer": round(ms * 1000 / r["layers"], 3)},
-            "roofline": None, "cpu_baseline": None,
+            "roofline": None, "cpu_baseline": r.get("cpu"),
         }
         print(json.dumps(line), flush=True)
         return 0
@@ -750,12 +834,14 @@ def sections(wl1: Workload, args) -> dict:
     wl1.x = synth.inputs(9000 + 1000, 17, D, correlated=True)
     wl1.fw.x.set(wl1.x)
     for L in wl1.layers:
-        mask = resident_set(L, seed=L.spec.seed + 77)
+        mask = resident_set(L, batch_seed=9000 + 1000, noise_seed=L.spec.seed + 77)
         L.bufs["resident"] = qg.Device(mask)
         L.desc.resident, L.desc.threshold = L.bufs["resident"].p, 0.10
     flags = np.concatenate([wl1.routing(i)[1] for i in range(len(wl1.layers))])
-    sec = decode_section(wl1, steps, warm, None)
+    sec = decode_section(wl1, steps, warm, cpu)
     sec["flag_counts"] = np.bincount(flags, minlength=4).tolist()
+    sec["resident_ranking"] = ("128 of 512 experts per layer by activation count, then routed weight, then id "
+                               "(qwen/README.md:38), over 4096 tokens from 8 correlated contexts, one of them the batch's")
     out["config4_B17"] = sec
     del wl1.layers[:]
     gc.collect()
@@ -764,12 +850,15 @@ def sections(wl1: Workload, args) -> dict:
     del wl0
     gc.collect()
     a = argparse.Namespace(layers=48, warmup=20, steps=40)
-    r = bench_stack(a)
+    r = bench_stack(a, cpu)
     out["config2_stack48_B1"] = {"tokens_per_s": round(1 / (r["ms"] * 1e-3), 1), "us_per_layer": round(r["ms"] * 1000 / 48, 2),
                                  "stack_bytes": int(r["bytes"]),
                                  "stack_hbm_frac": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if r.get("cpu"):
+        out["config2_stack48_B1"]["cpu_tokens_per_s"] = r["cpu"]["value"]
+        out["config2_stack48_B1"]["cpu_ms_per_token"] = r["cpu"]["ms_per_token"]
     gc.collect()
-    a = argparse.Namespace(batch=2048, warmup=warm, steps=min(args.steps, 50), no_cpu=True, cpu_budget=0)
+    a = argparse.Namespace(batch=2048, warmup=warm, steps=min(args.steps, 50), no_cpu=cpu is None, cpu_budget=cpu or 0)
     p = bench_prefill(a, "")
     pc = p["config"]
     out["config3_prefill_B2048"] = {
@@ -778,6 +867,9 @@ def sections(wl1: Workload, args) -> dict:
         "expert_gemms_int8_util_algorithmic": pc["expert_gemms_int8_util_algorithmic"],
         "dense_experts_gate_up": pc["dense_experts_gate_up"],
         "dense_experts": pc["dense_experts"], "layer_hbm_frac": pc["layer_hbm_frac"], "kernel_us": pc["kernel_us"]}
+    if p.get("cpu_baseline"):
+        out["config3_prefill_B2048"]["cpu_tokens_per_s"] = p["cpu_baseline"]["value"]
+        out["config3_prefill_B2048"]["cpu_sample"] = p["cpu_baseline"]["sample"]
     return out
 
 

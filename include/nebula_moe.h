@@ -14,6 +14,7 @@
 #ifndef NEBULA_MOE_H
 #define NEBULA_MOE_H
 #include "qwen_gpu.h"
+#include <stdint.h>
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -44,9 +45,20 @@ const char *nm_last_error(void);
 typedef int (*nm_cpu_moe_fn)(void *ctx, float *out, const float *x, const int *ids, const float *weights, int tokens);
 /* Device scratch bytes nm_moe_handoff needs for up to `tokens` tokens. */
 size_t nm_handoff_scratch_bytes(int width, int tokens);
+/* Allocates the calling thread's host buffers of nm_moe_handoff (packed
+ * rows, ids, weights, the CPU MoE's rows and a page-locked count word) for
+ * up to `tokens` tokens of `width`, so that later handoffs allocate nothing;
+ * nm_moe_handoff grows them itself when it meets a larger batch. */
+int nm_handoff_reserve(int width, int tokens);
+/* Number of synchronous device-to-host reads (qg_read) this library has
+ * issued in the process: the layer paths' host round trips, for tests and
+ * statistics. */
+uint64_t nm_device_reads(void);
 /* After qg_moe_forward(_residual) with flags: packs the flag-2 tokens on the
- * device, reads their count (4 bytes, synchronous) and then only their
- * input rows, ids and weights, calls cpu_moe, writes its rows back and adds
+ * device, waits for their count, which the device stores into a page-locked
+ * host word (qg_moe_handoff_notify: no device-to-host copy, so a layer with
+ * no flag-2 token makes none), and then reads only their input rows, ids and
+ * weights, calls cpu_moe, writes its rows back and adds
  * them to out (and to out2 when not NULL: the residual stream h) at the
  * tokens' rows, where the device left the shared expert's part.  x is the
  * layer input the forward used (xn_out for the residual form).  Synchronous

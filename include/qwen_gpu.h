@@ -77,9 +77,13 @@ int qg_shared_add(float *out, const float *shared, const float *gate, int tokens
  * shapes and drives the layer from the host, qwen.c:633-735) ---- */
 
 /* Hidden width D and expert FFN width F used by the width-less entry points
- * above, for the calling thread (each thread starts at 2560/640).  D
- * multiple of 256, F multiple of 32, D <= 8192, F <= 4096. */
+ * above: a process-wide setting (initially 2560/640), seen by every thread.
+ * D multiple of 256, F multiple of 32, D <= 8192, F <= 4096. */
 int qg_moe_configure(int width, int ff);
+/* A per-thread override of that setting for the calling thread's width-less
+ * calls (a thread driving a model of its own shape); (0, 0) removes it.
+ * Added entry point, no counterpart in gpu.h. */
+int qg_moe_configure_thread(int width, int ff);
 
 /* Dispatch of routing ids into per-expert contiguous row lists (CSR), the
  * device-side histogram/prefix-sum/permutation replacing qg_moe_map's
@@ -166,6 +170,16 @@ int qg_moe_handoff_pack(int *count, int *rows, float *x_pack, int *ids_pack, flo
                         const unsigned char *flags, const float *x, const int *ids, const float *weights,
                         int tokens, int width);
 int qg_moe_handoff_merge(float *out, const float *y_pack, const int *count, const int *rows, int tokens, int width);
+/* After qg_moe_handoff_pack: count[0] is stored into *host_word, a word of
+ * qg_host_alloc memory, by a kernel on the calling thread's stream, so the
+ * host learns the number of handed-off tokens by polling the word instead of
+ * a device-to-host copy.  Added entry point, no counterpart in gpu.h. */
+int qg_moe_handoff_notify(int *host_word, const int *count);
+/* Page-locked host memory that device code may access through the same
+ * pointer (NULL on failure), and its release.  Added entry points (the
+ * reference allocates its pinned staging inside qg_upload_create). */
+void *qg_host_alloc(size_t bytes);
+void qg_host_free(void *p);
 
 /* Benchmark support: events[2i] and events[2i+1] (qg_event_create handles)
  * are recorded at the start and end of kernel i of this thread's

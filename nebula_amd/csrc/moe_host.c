@@ -1,13 +1,24 @@
 /* Host C driver of stacked routed-MoE layers (declarations and contract in
  * include/nebula_moe.h).  Calls only the qg_* C ABI of libqwen_gpu.so. */
+#define _POSIX_C_SOURCE 200809L
 #include "nebula_moe.h"
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 enum { NM_MAX_TOKENS = 17, NM_TOP = 10 };
+
+/* Every synchronous device-to-host read this library makes goes through
+ * nm_read, which counts them (nm_device_reads). */
+static _Atomic uint64_t nm_reads;
+int nm_read(void *dst, const void *src, size_t n) {
+    nm_reads++;
+    return qg_read(dst, src, n);
+}
+uint64_t nm_device_reads(void) { return nm_reads; }
 
 static _Thread_local char nm_error[256];
 static int fail(const char *fmt, ...) {
@@ -130,6 +141,57 @@ size_t nm_handoff_scratch_bytes(int width, int tokens) {
     return handoff_at(0, width, tokens).bytes;
 }
 
+/* The calling thread's host side of the handoff, allocated once for the
+ * largest (width, tokens) reserved or met and kept for later layers: the
+ * packed rows, ids and weights read from the device, the CPU MoE's output
+ * rows, and the page-locked word the device writes the handed-off count to. */
+typedef struct { float *x, *y, *w; int *ids; int *word; size_t rows_cap, width; } handoff_host;
+static _Thread_local handoff_host hh;
+
+static void handoff_host_free(void) {
+    free(hh.x); free(hh.y); free(hh.w); free(hh.ids);
+    qg_host_free(hh.word);
+    memset(&hh, 0, sizeof hh);
+}
+
+int nm_handoff_reserve(int width, int tokens) {
+    if (width < 1 || tokens < 1 || tokens > 8192) return fail("invalid handoff reservation");
+    if (hh.word && hh.width == (size_t)width && hh.rows_cap >= (size_t)tokens) return 0;
+    const size_t rows = hh.width == (size_t)width && hh.rows_cap > (size_t)tokens ? hh.rows_cap : (size_t)tokens;
+    handoff_host_free();
+    hh.x = malloc(rows * (size_t)width * sizeof(float));
+    hh.y = malloc(rows * (size_t)width * sizeof(float));
+    hh.w = malloc(rows * NM_TOP * sizeof(float));
+    hh.ids = malloc(rows * NM_TOP * sizeof(int));
+    hh.word = qg_host_alloc(sizeof(int));
+    if (!hh.x || !hh.y || !hh.w || !hh.ids || !hh.word) { handoff_host_free(); return fail("handoff host allocation"); }
+    hh.rows_cap = rows;
+    hh.width = (size_t)width;
+    return 0;
+}
+
+/* Waits for the device's store of the handed-off count into the host word
+ * (set to -1 before the notify kernel was queued).  After ~2 ms of polling it
+ * synchronises the device instead, so a failed layer reports its error. */
+static int handoff_wait_count(int *n) {
+    volatile int *word = hh.word;
+    const double t_end = 2e-3;
+    struct timespec t0, t;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    while (*word < 0) {
+        clock_gettime(CLOCK_MONOTONIC, &t);
+        if ((t.tv_sec - t0.tv_sec) + (t.tv_nsec - t0.tv_nsec) * 1e-9 > t_end) {
+            const int rc = qg_sync();
+            if (rc) return fail("handoff count: %s", qg_error(rc));
+            if (*word < 0) return fail("handoff count not delivered");
+            break;
+        }
+    }
+    __atomic_thread_fence(__ATOMIC_ACQUIRE);
+    *n = *word;
+    return 0;
+}
+
 int nm_moe_handoff(float *out, float *out2, const unsigned char *flags, const float *x, const int *ids,
                    const float *weights, int nt, int D, void *scratch, size_t scratch_bytes,
                    nm_cpu_moe_fn cpu_moe, void *ctx, int *handed_off) {
@@ -138,30 +200,22 @@ int nm_moe_handoff(float *out, float *out2, const unsigned char *flags, const fl
         return fail("invalid handoff arguments");
     const handoff_layout L = handoff_at((uintptr_t)scratch, D, nt);
     if (scratch_bytes < L.bytes) return fail("handoff scratch of %zu bytes, %zu needed", scratch_bytes, L.bytes);
+    if (nm_handoff_reserve(D, nt)) return -1;
+    *(volatile int *)hh.word = -1;
     int rc = qg_moe_handoff_pack(L.count, L.rows, L.x, L.ids, L.w, flags, x, ids, weights, nt, D);
-    int n = 0;
-    if (!rc) rc = qg_read(&n, L.count, sizeof n);
+    if (!rc) rc = qg_moe_handoff_notify(hh.word, L.count);
     if (rc) return fail("handoff pack: %s", qg_error(rc));
+    int n = 0;
+    if (handoff_wait_count(&n)) return -1;
     if (n < 0 || n > nt) return fail("handoff count %d out of range", n);
     if (!n) return 0;
     const size_t xb = (size_t)n * D * sizeof(float), sb = (size_t)n * NM_TOP * 4;
-    float *hx = malloc(xb), *hy = malloc(xb), *hw = malloc(sb);
-    int *hi = malloc(sb);
-    int ret = -1;
-    if (!hx || !hy || !hw || !hi) { fail("host allocation"); goto done; }
-    if ((rc = qg_read(hx, L.x, xb)) || (rc = qg_read(hi, L.ids, sb)) || (rc = qg_read(hw, L.w, sb))) {
-        fail("handoff read: %s", qg_error(rc));
-        goto done;
-    }
-    if (cpu_moe(ctx, hy, hx, hi, hw, n)) { fail("CPU MoE of %d handed-off tokens failed", n); goto done; }
-    if ((rc = qg_write(L.y, hy, xb)) || (rc = qg_moe_handoff_merge(out, L.y, L.count, L.rows, nt, D)) ||
-        (out2 && (rc = qg_moe_handoff_merge(out2, L.y, L.count, L.rows, nt, D)))) {
-        fail("handoff merge: %s", qg_error(rc));
-        goto done;
-    }
+    if ((rc = nm_read(hh.x, L.x, xb)) || (rc = nm_read(hh.ids, L.ids, sb)) || (rc = nm_read(hh.w, L.w, sb)))
+        return fail("handoff read: %s", qg_error(rc));
+    if (cpu_moe(ctx, hh.y, hh.x, hh.ids, hh.w, n)) return fail("CPU MoE of %d handed-off tokens failed", n);
+    if ((rc = qg_write(L.y, hh.y, xb)) || (rc = qg_moe_handoff_merge(out, L.y, L.count, L.rows, nt, D)) ||
+        (out2 && (rc = qg_moe_handoff_merge(out2, L.y, L.count, L.rows, nt, D))))
+        return fail("handoff merge: %s", qg_error(rc));
     if (handed_off) *handed_off = n;
-    ret = 0;
-done:
-    free(hx); free(hy); free(hw); free(hi);
-    return ret;
+    return 0;
 }

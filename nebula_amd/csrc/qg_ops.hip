@@ -5,11 +5,16 @@
 #include "qg_internal.h"
 #include "qg_frag.h"
 
-// Per calling thread, like the launch stream: callers on two threads with
-// differently shaped models do not see each other's setting.
-static thread_local int g_width = 2560, g_ff = 640;  // gpu.cu:508-553 hard-code these
-int qg_cfg_width(void) { return g_width; }
-int qg_cfg_ff(void) { return g_ff; }
+// The widths of the width-less entry points: a process-wide setting
+// (qg_moe_configure), which a thread may override for its own calls
+// (qg_moe_configure_thread), so a caller that configures on one thread and
+// launches from another sees its setting, and two threads driving models of
+// different shapes each keep their own.
+#include <atomic>
+static std::atomic<int> g_width{2560}, g_ff{640};  // gpu.cu:508-553 hard-code these
+static thread_local int t_width = 0, t_ff = 0;     // 0: no per-thread override
+int qg_cfg_width(void) { return t_width ? t_width : g_width.load(std::memory_order_relaxed); }
+int qg_cfg_ff(void) { return t_width ? t_ff : g_ff.load(std::memory_order_relaxed); }
 
 namespace {
 
@@ -463,6 +468,12 @@ __global__ __launch_bounds__(256) void handoff_pack_kernel(float *xp, int *idp, 
     }
 }
 
+// count[0] into the host word: a store at system scope, which the host
+// observes by polling the word (page-locked host memory).
+__global__ void handoff_notify_kernel(int *host_word, const int *count) {
+    __hip_atomic_store(host_word, count[0], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Block i < count: out[rows[i]] += y[i] (the host's routed rows onto the
 // device rows, which hold the shared expert's part).
 __global__ __launch_bounds__(256) void handoff_merge_kernel(float *out, const float *y, const int *count, const int *rows, int width) {
@@ -489,10 +500,25 @@ int qg_launch_matmul_exact(float *out, const uint8_t *w, int type, int rows, int
 
 extern "C" {
 
+static bool widths_ok(int width, int ff) {
+    return width >= 256 && width <= 8192 && width % 256 == 0 && ff >= 32 && ff <= 4096 && ff % 32 == 0;
+}
+
 int qg_moe_configure(int width, int ff) {
-    if (width < 256 || width > 8192 || width % 256 || ff < 32 || ff > 4096 || ff % 32) return hipErrorInvalidValue;
-    g_width = width;
-    g_ff = ff;
+    if (!widths_ok(width, ff)) return hipErrorInvalidValue;
+    g_width.store(width, std::memory_order_relaxed);
+    g_ff.store(ff, std::memory_order_relaxed);
+    return hipSuccess;
+}
+
+int qg_moe_configure_thread(int width, int ff) {
+    if (width == 0 && ff == 0) {
+        t_width = t_ff = 0;
+        return hipSuccess;
+    }
+    if (!widths_ok(width, ff)) return hipErrorInvalidValue;
+    t_width = width;
+    t_ff = ff;
     return hipSuccess;
 }
 
@@ -559,25 +585,25 @@ int qg_moe_map(int *map, const int *ids, int nt) {  // gpu.cu:501-505
 
 int qg_moe_gather(float *o, const float *x, const int *map, int selected) {  // gpu.cu:509-512
     if (selected < 1) return selected ? hipErrorInvalidValue : hipSuccess;
-    moe_gather_kernel<<<selected, 256, 0, qg_stream()>>>(o, x, map, g_width);
+    moe_gather_kernel<<<selected, 256, 0, qg_stream()>>>(o, x, map, qg_cfg_width());
     return hipGetLastError();
 }
 
 int qg_moe_scatter(float *o, const float *y, const float *w, const int *ids, const int *map, int expert, int selected) {  // gpu.cu:518-520
     if (selected < 1) return selected ? hipErrorInvalidValue : hipSuccess;
-    moe_scatter_kernel<<<selected, 256, 0, qg_stream()>>>(o, y, w, ids, map, expert, g_width);
+    moe_scatter_kernel<<<selected, 256, 0, qg_stream()>>>(o, y, w, ids, map, expert, qg_cfg_width());
     return hipGetLastError();
 }
 
 int qg_moe_reduce(float *out, const float *slots, int nt) {  // gpu.cu:525-527
     if (nt < 1) return hipErrorInvalidValue;
-    moe_reduce_kernel<<<blocks_for((size_t)nt * g_width, 256), 256, 0, qg_stream()>>>(out, slots, nt, g_width);
+    moe_reduce_kernel<<<blocks_for((size_t)nt * qg_cfg_width(), 256), 256, 0, qg_stream()>>>(out, slots, nt, qg_cfg_width());
     return hipGetLastError();
 }
 
 int qg_shared_add(float *o, const float *x, const float *g, int nt) {  // gpu.cu:553
     if (nt < 1) return hipErrorInvalidValue;
-    shared_add_kernel<<<blocks_for((size_t)nt * g_width, 256), 256, 0, qg_stream()>>>(o, x, g, nt, g_width);
+    shared_add_kernel<<<blocks_for((size_t)nt * qg_cfg_width(), 256), 256, 0, qg_stream()>>>(o, x, g, nt, qg_cfg_width());
     return hipGetLastError();
 }
 
@@ -590,6 +616,12 @@ int qg_moe_handoff_pack(int *count, int *rows, float *x_pack, int *ids_pack, flo
         return hipErrorInvalidValue;
     handoff_rows_kernel<<<1, 1024, 0, qg_stream()>>>(count, rows, flags, nt);
     handoff_pack_kernel<<<nt, 256, 0, qg_stream()>>>(x_pack, ids_pack, w_pack, count, rows, x, ids, weights, width);
+    return hipGetLastError();
+}
+
+int qg_moe_handoff_notify(int *host_word, const int *count) {
+    if (!host_word || !count) return hipErrorInvalidValue;
+    handoff_notify_kernel<<<1, 1, 0, qg_stream()>>>(host_word, count);
     return hipGetLastError();
 }
 

@@ -73,6 +73,14 @@ int qg_zero(void *d, size_t n) {
 }
 int qg_sync(void) { return hipDeviceSynchronize(); }
 
+// Page-locked host memory that kernels may read and write through the same
+// address (a mailbox the host polls without a device-to-host copy).
+void *qg_host_alloc(size_t n) {
+    void *p = nullptr;
+    return hipHostMalloc(&p, n ? n : 1, hipHostMallocDefault) == hipSuccess ? p : nullptr;
+}
+void qg_host_free(void *p) { if (p) (void)hipHostFree(p); }
+
 }  // extern "C"
 
 // Library-owned scratch that grows on demand.  A graph captured earlier may

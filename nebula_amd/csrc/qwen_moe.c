@@ -42,6 +42,7 @@ typedef struct {
     unsigned char *slots;                                     /* cache mode: resident slots, gate|up|down each */
     int *cache_ids;                                           /* slot -> expert or -1 */
     uint64_t *cache_age, clock;
+    unsigned char pinned[512];                                /* hotlist mode: the layer's resident experts */
     qg_moe_layer desc;
 } qm_layer;
 
@@ -93,6 +94,8 @@ static double seconds_now(void) {
 }
 
 #define GPU(call) do { int rc_ = (call); if (rc_) return fail("%s: %s", #call, qg_error(rc_)); } while (0)
+
+int nm_read(void *dst, const void *src, size_t n);  /* moe_host.c: qg_read, counted */
 
 /* ---------------- index (qwen.c:108-146) ---------------- */
 
@@ -221,6 +224,21 @@ static int bind_layer(qwen_model *m, int il) {
     return 0;
 }
 
+/* Whether the device layer's batch kernels (above 17 tokens) take layer il:
+ * Q4_K gate/up (routed and shared), Q4_K (F a multiple of 256) or IQ4_NL
+ * down, D a multiple of 256 and F of 128.  Batches above 17 tokens of the
+ * hotlist target layers and of the MTP layer run there; the cache mode's
+ * grouped qg_* path takes any format. */
+static int batch_formats_ok(const qwen_model *m, int il) {
+    const qm_layer *l = &m->layers[il];
+    const int F = m->F;
+    if (m->D % 256 || F % 128) return 0;
+#define QM_DOWN_OK(t) ((t) == 20 || ((t) == 12 && F % 256 == 0))
+    return l->eg->type == 12 && l->eu->type == 12 && QM_DOWN_OK(l->ed->type) && l->sg->type == 12 && l->su->type == 12 &&
+           QM_DOWN_OK(l->sd->type);
+#undef QM_DOWN_OK
+}
+
 /* Layers present: blk.0 .. blk.(n-1) (n <= 48) and optionally blk.48. */
 static int bind_model(qwen_model *m) {
     const qm_tensor *g0 = layer_tensor(m, 0, "ffn_gate_exps.weight");
@@ -322,6 +340,7 @@ static int open_device(qwen_model *m) {
     m->ws_bytes = qg_moe_workspace_bytes(D, F, T);
     m->handoff_bytes = nm_handoff_scratch_bytes(D, T);
     if (!m->ws_bytes || !m->handoff_bytes) return fail("unsupported MoE shape for %d tokens", T);
+    if (nm_handoff_reserve(D, T)) return fail("handoff host buffers: %s", nm_last_error());
     if (!(m->logits = dev_alloc(m, (size_t)T * QM_EXPERTS * 4)) || !(m->route_w = dev_alloc(m, sel)) ||
         !(m->route_ids = dev_alloc(m, sel)) || !(m->route_map = dev_alloc(m, (size_t)QM_EXPERTS * T * 4)) ||
         !(m->slots = dev_alloc(m, act * QM_TOP)) || !(m->expert_x = dev_alloc(m, act)) ||
@@ -332,7 +351,13 @@ static int open_device(qwen_model *m) {
         !(m->handoff = dev_alloc(m, m->handoff_bytes)))
         return fail("device workspace allocation");
     m->stats.gpu_workspace_bytes = m->stats.gpu_arena_bytes - m->stats.gpu_weight_bytes;
-    m->uploader = qg_upload_create(m->layers[0].expert_bytes);
+    /* the staging buffers hold the largest expert of any target layer, whose
+     * formats may differ from layer to layer (qwen.c:365-367) */
+    size_t largest = 0;
+    for (int il = 0; il < m->n_layers; il++)
+        if (m->layers[il].expert_bytes > largest) largest = m->layers[il].expert_bytes;
+    m->uploader = qg_upload_create(largest);
+    m->stats.host_staging_bytes = 2 * (uint64_t)largest;
     m->h_ids = malloc(sel);
     m->h_w = malloc(sel);
     if (!m->uploader || !m->h_ids || !m->h_w) return fail("expert uploader allocation");
@@ -353,9 +378,15 @@ qwen_model *qwen_open(const char *path, int context, int resident, int capacity)
     m->context = context; m->resident = resident; m->capacity = capacity;
     if (!m->tensors) { fail("host allocation"); free(m); return NULL; }
     if (read_index(m, path, 1) || bind_model(m)) { unmap_files(m); free(m->tensors); free(m); return NULL; }
+    if (capacity > QWEN_MAX_DRAFT + 1 && m->has_mtp && !batch_formats_ok(m, QM_MTP)) {
+        fail("batch capacity %d above %d needs Q4_K gate/up and Q4_K or IQ4_NL down in the MTP layer", capacity,
+             QWEN_MAX_DRAFT + 1);
+        unmap_files(m); free(m->tensors); free(m);
+        return NULL;
+    }
     /* width-less drop-in entry points of this thread use this model's shape */
-    int rc = qg_moe_configure(m->D, m->F);
-    if (rc) { fail("qg_moe_configure: %s", qg_error(rc)); qwen_close(m); return NULL; }
+    int rc = qg_moe_configure_thread(m->D, m->F);
+    if (rc) { fail("qg_moe_configure_thread: %s", qg_error(rc)); qwen_close(m); return NULL; }
     if (open_device(m)) { qwen_close(m); return NULL; }
     for (int il = 0; il < m->n_layers; il++)
         m->stats.host_weight_bytes += m->layers[il].eg->bytes + m->layers[il].eu->bytes + m->layers[il].ed->bytes;
@@ -440,6 +471,11 @@ int qwen_set_hotlist(qwen_model *m, const int *ids, int count, int threads) {
             seen[e] = 1;
         }
     }
+    if (m->capacity > QWEN_MAX_DRAFT + 1)
+        for (int il = 0; il < m->n_layers; il++)
+            if (!batch_formats_ok(m, il))
+                return fail("hotlist with batch capacity %d above %d needs Q4_K gate/up and Q4_K or IQ4_NL down (layer %d)",
+                            m->capacity, QWEN_MAX_DRAFT + 1, il);
     if (m->hotlist_tried) return fail("CPU hotlist initialization already attempted; reopen the model");
     m->hotlist_tried = 1;
     if (!m->cpu_moe) return fail("register the CPU MoE (qwen_set_cpu_moe) before the hotlist");
@@ -459,7 +495,10 @@ int qwen_set_hotlist(qwen_model *m, const int *ids, int count, int threads) {
         /* the cache is empty here: every pinned expert takes a free slot */
         for (int j = 0; j < m->resident; j++)
             if (cache_slot(m, l, ids[il * m->resident + j], keep, 1) < 0) { free(masks); return -1; }
-        for (int j = 0; j < m->resident; j++) masks[(size_t)il * QM_EXPERTS + ids[il * m->resident + j]] = 1;
+        for (int j = 0; j < m->resident; j++) {
+            masks[(size_t)il * QM_EXPERTS + ids[il * m->resident + j]] = 1;
+            l->pinned[ids[il * m->resident + j]] = 1;
+        }
         l->desc.gate = l->d_gate; l->desc.up = l->d_up; l->desc.down = l->d_down;
         l->desc.resident = m->masks + (size_t)il * QM_EXPERTS;
         l->desc.threshold = 0.10;   /* omitted-mass threshold (config.py:9) */
@@ -483,11 +522,21 @@ int qwen_set_cpu_threads(qwen_model *m, int threads) {
 int qwen_cpu_threads(qwen_model *m) { return m ? m->cpu_threads : 0; }
 void qwen_get_cpu_stats(qwen_model *m, qwen_cpu_stats *out) { if (m && out) *out = m->cpu_stats; }
 void qwen_get_handoff_profile(qwen_model *m, qwen_handoff_profile *out) { if (m && out) *out = m->profile; }
-void qwen_get_stats(qwen_model *m, qwen_stats *out) { if (m && out) *out = m->stats; }
+/* In hotlist mode the selections are counted on the device (the prune
+ * counters of qg_moe_forward) instead of reading every layer's ids back
+ * (qwen.c:649-657): a token with a valid routing has 10 - missing resident
+ * selections, so the layers' hits are 10 token_layers - missing_selections. */
+void qwen_get_stats(qwen_model *m, qwen_stats *out) {
+    if (!m || !out) return;
+    *out = m->stats;
+    qg_prune_stats p;
+    if (m->fixed_hotlist && m->prune_device && !nm_read(&p, m->prune_device, sizeof p))
+        out->expert_hits += QM_TOP * p.token_layers - p.missing_selections;
+}
 
 int qwen_get_prune_stats(qwen_model *m, qwen_prune_stats *out) {
     if (!m || !out || !m->prune_device) return fail("hotlist statistics unavailable");
-    GPU(qg_read(out, m->prune_device, sizeof *out));
+    GPU(nm_read(out, m->prune_device, sizeof *out));
     return 0;
 }
 
@@ -513,8 +562,8 @@ int qwen_profile_routes(qwen_model *m, const char *path) {
 static int route_to_host(qwen_model *m, qm_layer *l, const float *x, int nt) {
     GPU(qg_matmul(m->logits, l->d_router, 0, QM_EXPERTS, m->D, x, nt));
     GPU(qg_route(m->route_ids, m->route_w, m->logits, nt));
-    GPU(qg_read(m->h_ids, m->route_ids, (size_t)nt * QM_TOP * 4));
-    GPU(qg_read(m->h_w, m->route_w, (size_t)nt * QM_TOP * 4));
+    GPU(nm_read(m->h_ids, m->route_ids, (size_t)nt * QM_TOP * 4));
+    GPU(nm_read(m->h_w, m->route_w, (size_t)nt * QM_TOP * 4));
     m->stats.metadata_read_bytes += (uint64_t)nt * QM_TOP * 4;
     return 0;
 }
@@ -530,44 +579,43 @@ static int trace_routes(qwen_model *m, int il, int position, int nt) {
 
 /* ---------------- moe() (qwen.c:714-735) ---------------- */
 
-typedef struct { qwen_model *m; qm_layer *l; } cpu_call;
+typedef struct { qwen_model *m; qm_layer *l; uint64_t missing; } cpu_call;
 
+/* The registered CPU MoE on the handed-off rows; compute_seconds counts this
+ * call alone, without the device reads and writes around it (qwen.c:663-668). */
 static int cpu_moe_tokens(void *ctx, float *out, const float *x, const int *ids, const float *weights, int nt) {
-    const cpu_call *c = ctx;
-    return c->m->cpu_moe(c->m->cpu_ctx, out, x, ids, weights, nt, c->l->eg->host, c->l->eg->type, c->l->eu->host,
-                         c->l->eu->type, c->l->ed->host, c->l->ed->type);
+    cpu_call *c = ctx;
+    /* the handed-off tokens' selections of experts not on the device (the
+     * batch's other missing selections were pruned, qwen.c:656) */
+    for (int j = 0; j < nt * QM_TOP; j++)
+        if (ids[j] >= 0 && ids[j] < QM_EXPERTS && !c->l->pinned[ids[j]]) c->missing++;
+    const double begin = seconds_now();
+    const int rc = c->m->cpu_moe(c->m->cpu_ctx, out, x, ids, weights, nt, c->l->eg->host, c->l->eg->type, c->l->eu->host,
+                                 c->l->eu->type, c->l->ed->host, c->l->ed->type);
+    c->m->cpu_stats.compute_seconds += seconds_now() - begin;
+    return rc;
 }
 
 /* Fixed hotlist: the device layer with the resident mask; flag-2 tokens'
- * routed parts come from the host's CPU MoE. */
+ * routed parts come from the host's CPU MoE.  Nothing is read back for a
+ * layer without a flag-2 token (the handoff learns the count from a host
+ * word the device writes); hits are counted on the device. */
 static int moe_hotlist(qwen_model *m, int il, float *out, const float *x, int nt) {
     qm_layer *l = &m->layers[il];
     GPU(qg_moe_forward(out, m->route_ids, m->route_w, m->flags, m->prune_device, x, nt, &l->desc, m->ws, m->ws_bytes));
-    GPU(qg_read(m->h_ids, m->route_ids, (size_t)nt * QM_TOP * 4));
-    m->stats.metadata_read_bytes += (uint64_t)nt * QM_TOP * 4;
-    unsigned char resident[QM_EXPERTS] = {0};
-    for (int j = 0; j < m->resident; j++) if (l->cache_ids[j] >= 0) resident[l->cache_ids[j]] = 1;
-    uint64_t missing = 0;
-    for (int j = 0; j < nt * QM_TOP; j++) {
-        const int e = m->h_ids[j];
-        m->stats.expert_requests++;
-        m->stats.expert_hits += e >= 0 && resident[e];
-        missing += e >= 0 && !resident[e];
-    }
-    double begin = seconds_now();
-    cpu_call c = {m, l};
+    m->stats.expert_requests += (uint64_t)nt * QM_TOP;
+    const double begin = seconds_now();
+    cpu_call c = {m, l, 0};
     int handed = 0;
-    if (missing && nm_moe_handoff(out, NULL, m->flags, x, m->route_ids, m->route_w, nt, m->D, m->handoff, m->handoff_bytes,
-                                  cpu_moe_tokens, &c, &handed))
+    if (nm_moe_handoff(out, NULL, m->flags, x, m->route_ids, m->route_w, nt, m->D, m->handoff, m->handoff_bytes,
+                       cpu_moe_tokens, &c, &handed))
         return fail("CPU MoE handoff: %s", nm_last_error());
     m->profile.layer_calls[il]++;
     if (handed) {
-        const double spent = seconds_now() - begin;
-        m->cpu_stats.handoff_seconds += spent;
-        m->cpu_stats.compute_seconds += spent;
+        m->cpu_stats.handoff_seconds += seconds_now() - begin;
         m->cpu_stats.layer_handoffs++;
         m->cpu_stats.token_layers += (uint64_t)handed;
-        m->cpu_stats.missing_selections += missing;
+        m->cpu_stats.missing_selections += c.missing;
         m->cpu_stats.activation_bytes += (uint64_t)handed * ((uint64_t)m->D * 8 + QM_TOP * 4);
         m->profile.layer_handoffs[il]++;
     }
@@ -635,7 +683,7 @@ int qwen_moe(qwen_model *m, int il, float *out, const float *x, int nt, int posi
     const int mtp = il == QM_MTP;
     if (mtp ? !m->has_mtp : (il < 0 || il >= m->n_layers)) return fail("no MoE layer %d", il);
     if (!mtp && position + nt > m->context) return fail("target batch exceeds context");
-    GPU(qg_moe_configure(m->D, m->F));
+    GPU(qg_moe_configure_thread(m->D, m->F));
     const double begin = seconds_now();
     int rc;
     if (mtp) {
@@ -650,7 +698,9 @@ int qwen_moe(qwen_model *m, int il, float *out, const float *x, int nt, int posi
         rc = m->fixed_hotlist ? moe_hotlist(m, il, out, x, nt) : moe_cached(m, il, out, x, nt);
     }
     if (rc) return rc;
-    GPU(qg_sync());
+    /* no synchronisation: the layer's device work is ordered on the calling
+     * thread's stream, like the reference's moe(); a hotlist layer has
+     * already waited for its handoff decision */
     if (mtp) {
         m->stats.mtp_tokens += (uint64_t)nt;
         m->stats.mtp_seconds += seconds_now() - begin;

@@ -32,7 +32,7 @@ SIGNATURES = {
     "moe_reduce": ([P, P, I], I), "mtp_moe": ([P, P, P, P, P, P, I, P, I, P, I, I], I),
     "dequant": ([P, P, I, I, I], I), "shared_add": ([P, P, P, I], I),
     # additions
-    "moe_configure": ([I, I], I), "moe_dispatch": ([P, P, P, P, P, I], I),
+    "moe_configure": ([I, I], I), "moe_configure_thread": ([I, I], I), "moe_dispatch": ([P, P, P, P, P, I], I),
     "moe_workspace_bytes": ([I, I, I], Z), "moe_phase_events": ([P, I], I), "moe_forward": ([P, P, P, P, P, P, I, P, P, Z], I),
     "moe_forward_noalloc": ([P, P, P, P, P, P, I, P], I),
     "moe_forward_residual": ([P, P, P, P, P, P, P, I, P, P, Z], I), "moe_kernel_events": ([P, I], I),
@@ -40,6 +40,7 @@ SIGNATURES = {
     "device_info": ([P, Z, P, P, P, P], I),
     "synth_matrix": ([P, I, U64, U64, I, I, F], I), "synth_experts": ([P, I, U64, I, I, I, I, F], I), "prefill_int8_dense": ([I], I),
     "moe_handoff_pack": ([P, P, P, P, P, P, P, P, P, I, I], I), "moe_handoff_merge": ([P, P, P, P, I, I], I),
+    "moe_handoff_notify": ([P, P], I), "host_alloc": ([Z], P), "host_free": ([P], None),
 }
 
 # nm_cpu_moe_fn of include/nebula_moe.h: (ctx, out, x, ids, weights, tokens) -> 0 on success
@@ -50,6 +51,7 @@ HOST_SIGNATURES = {
     "stack_forward": ([P, I, I], I), "stack_record": ([P, I, P, P, P, P], I), "last_error": ([], C.c_char_p),
     "handoff_scratch_bytes": ([I, I], Z),
     "moe_handoff": ([P, P, P, P, P, P, I, I, P, Z, CPU_MOE_FN, P, P], I),
+    "handoff_reserve": ([I, I], I), "device_reads": ([], C.c_uint64),
 }
 
 

@@ -39,6 +39,44 @@ def inputs(seed: int, tokens: int, width: int, correlated: bool = False) -> np.n
     return rmsnorm(x)
 
 
+RANKING_TOKENS, RANKING_CONTEXTS = 4096, 8
+
+
+def ranking_inputs(batch_seed: int, noise_seed: int, tokens: int = RANKING_TOKENS, width: int = 2048,
+                   contexts: int = RANKING_CONTEXTS) -> np.ndarray:
+    """Config 4's ranking set: `tokens` rows from `contexts` correlated
+    contexts, RMSNorm(base_c + 0.3*noise), token i in context i % contexts.
+    Context 0's base is the verify batch's own (inputs(batch_seed, ...,
+    correlated=True) draws the same base first); the other bases and all the
+    noise come from `noise_seed`, so no ranking row equals a batch row.  With
+    one context the top 128 experts cover every selection of the batch (every
+    token flag 0); with 8 the batch's frequent experts are resident and some
+    of its rare ones are not, so its tokens mix flags 0, 1 and 2."""
+    base0 = np.random.default_rng(batch_seed).standard_normal(width)
+    rng = np.random.default_rng(noise_seed)
+    bases = np.concatenate([base0[None, :], rng.standard_normal((contexts - 1, width))])
+    x = bases[np.arange(tokens) % contexts] + 0.3 * rng.standard_normal((tokens, width))
+    return rmsnorm(x)
+
+
+def resident_ranking(ids: np.ndarray, weights: np.ndarray, count: int = 128) -> np.ndarray:
+    """The resident mask of the `count` best-ranked experts over routed
+    selections (ids, weights [tokens, 10]): activation count descending, then
+    accumulated router weight descending, then expert id ascending, the
+    reference's expert ranking (qwen/README.md:38).  Ids outside 0..511 are
+    ignored."""
+    ids = np.asarray(ids).ravel()
+    w = np.asarray(weights).ravel().astype(np.float64)
+    ok = (ids >= 0) & (ids < EXPERTS)
+    hits = np.bincount(ids[ok], minlength=EXPERTS)
+    mass = np.zeros(EXPERTS)
+    np.add.at(mass, ids[ok], w[ok])
+    order = np.lexsort((np.arange(EXPERTS), -mass, -hits))
+    mask = np.zeros(EXPERTS, np.uint8)
+    mask[order[:count]] = 1
+    return mask
+
+
 @dataclass
 class LayerSpec:
     seed: int

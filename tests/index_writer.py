@@ -22,8 +22,9 @@ def tensor_line(name, file, offset, nbytes, typ, dims):
 
 def write_index(directory: Path, files: list[list[tuple]], numbers=None, sparse: bool = False) -> Path:
     """files: per file, a list of (name, type, dims, data or byte count);
-    each tensor starts 32-byte aligned.  sparse: data are byte counts and the
-    file is only sized (its contents are zeros)."""
+    each tensor starts 32-byte aligned.  A byte count in place of data (or
+    sparse: every tensor given so) leaves the tensor's bytes zero without
+    writing them (the file is only sized over them)."""
     directory = Path(directory)
     lines = ["COB_QWEN_INDEX_V1\n", "VERIFIED 1\n", " ".join(str(v) for v in (numbers or HEADER_NUMBERS)) + "\n"]
     tensor_lines = []
@@ -32,9 +33,10 @@ def write_index(directory: Path, files: list[list[tuple]], numbers=None, sparse:
         off = 0
         with open(path, "wb") as f:
             for name, typ, dims, data in tensors:
-                nbytes = data if sparse else np.asarray(data).nbytes
+                zero = sparse or isinstance(data, (int, np.integer))
+                nbytes = int(data) if zero else np.asarray(data).nbytes
                 off = (off + 31) // 32 * 32
-                if not sparse:
+                if not zero:
                     f.seek(off)
                     f.write(np.ascontiguousarray(data).tobytes())
                 tensor_lines.append(tensor_line(name, fid, off, nbytes, typ, dims))

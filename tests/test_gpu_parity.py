@@ -415,21 +415,23 @@ def test_layer_config0_multitoken_no_shared(layer0):
 
 @pytest.mark.parametrize("nt", [1, 4, 17])
 def test_layer_partial_residency_flags(layer1, nt):
-    """Config 4: 128 resident experts chosen by routed-weight mass over 4096
-    synthetic tokens; flags and pruning exact, unflagged rows in tolerance
-    (4 tokens run the small-batch kernels, 17 the dispatch kernels)."""
+    """Config 4: 128 resident experts ranked by the reference's rule
+    (activation count, routed weight, id; qwen/README.md:38) over 4096 tokens
+    from 8 correlated contexts, one of them the batch's own.  The batch then
+    mixes covered (flag 0), pruned (1) and handed-off (2) tokens: flags and
+    pruning exact, every unflagged row (resident experts only, pruned weights
+    0) within tolerance of the oracle; 1 token runs the inline-routing
+    kernels, 4 and 17 the routing kernel."""
     L, H = layer1
-    xs = synth.inputs(4242, 4096, 2048, correlated=False)
+    xs = synth.ranking_inputs(77, 4242)
     dx = Device(xs)
-    logits = Device(shape=(4096, 512), dtype=np.float32)
-    ids, w = Device(shape=(4096, 10), dtype=np.int32), Device(shape=(4096, 10), dtype=np.float32)
-    call("matmul", logits.p, L.bufs["router"].p, 0, 512, 2048, dx.p, 4096)
-    call("route", ids.p, w.p, logits.p, 4096)
-    score = np.zeros(512)
-    np.add.at(score, ids.get().ravel(), w.get().ravel().astype(np.float64))
-    order = np.lexsort((np.arange(512), -score))
-    resident = np.zeros(512, np.uint8)
-    resident[order[:128]] = 1
+    n = xs.shape[0]
+    logits = Device(shape=(n, 512), dtype=np.float32)
+    ids, w = Device(shape=(n, 10), dtype=np.int32), Device(shape=(n, 10), dtype=np.float32)
+    call("matmul", logits.p, L.bufs["router"].p, 0, 512, 2048, dx.p, n)
+    call("route", ids.p, w.p, logits.p, n)
+    resident = synth.resident_ranking(ids.get(), w.get(), 128)
+    assert int(resident.sum()) == 128
     desc = qg.MoeLayer.from_buffer_copy(L.desc)
     rdev = Device(resident)
     desc.resident, desc.threshold = rdev.p, 0.10
@@ -438,6 +440,13 @@ def test_layer_partial_residency_flags(layer1, nt):
     try:
         x = synth.inputs(77, nt, 2048, correlated=True)
         fw, st = _check_layer(L, H, x, f"config4 B={nt}", resident=resident)
+        flags = fw.flags.get()[:nt]
+        say(f"  config4 B={nt}: flags {np.bincount(flags, minlength=4).tolist()}")
+        if nt >= 4:
+            # resident-only routed compute is exercised and compared
+            assert np.count_nonzero(flags < 2) > 0
+        if nt == 17:
+            assert np.count_nonzero(flags == 0) > 0 and np.count_nonzero(flags == 1) > 0
         gst = qg.PruneStats.from_buffer_copy(fw.stats.get())
         assert (gst.token_layers, gst.missing_selections, gst.skipped_selections, gst.avoided_token_handoffs) == \
                (st.token_layers, st.missing_selections, st.skipped_selections, st.avoided_token_handoffs)

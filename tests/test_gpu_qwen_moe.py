@@ -239,20 +239,29 @@ def test_hotlist_mode_handoff_and_stats(model_index):
         lib.qwen_get_stats(m, C.byref(st0))
         assert st0.expert_handoffs == R  # the pinning uploads
         total = O.PruneStats()
-        flagged = layers_with = 0
+        flagged = layers_with = hits = missing = 0
         pos = 0
+        host = qg.host()
         for i, (nt, seed) in enumerate(HOT_CALLS):
             x = synth.inputs(8300 + seed, nt, D, correlated=True)
             say(f"qwen_moe hotlist nt={nt}")
             before = len(calls)
+            reads = host.nm_device_reads()
             got = run_moe(m, 0, x, pos)
+            reads = host.nm_device_reads() - reads
             want, ids, w, _, flags, st = H0.forward(x, resident)
+            # the reference's hit count over the pruned ids (qwen.c:656-657)
+            hits += int(((ids >= 0) & (resident[np.clip(ids, 0, 511)] == 1)).sum())
+            missing += int(((ids >= 0) & (resident[np.clip(ids, 0, 511)] == 0)).sum())
             ok = flags < 3
             maxabs, rel = assert_close(got[ok], want[ok], f"hotlist nt={nt}")
             n2 = int((flags == 2).sum())
             assert (len(calls) - before) == (1 if n2 else 0) and (not n2 or calls[-1] == n2)
             say(f"  hotlist nt={nt}: flags {np.bincount(flags, minlength=4).tolist()} max-abs {maxabs:.2e} rel-L2 {rel:.2e}")
             assert (n2 == 0) == (i < 3), flags
+            # no device-to-host read for a layer without a flag-2 token; the
+            # packed rows, ids and weights (three reads) for one with
+            assert reads == (3 if n2 else 0), reads
             flagged += n2
             layers_with += n2 > 0
             for k in ("token_layers", "missing_selections", "skipped_selections", "avoided_token_handoffs"):
@@ -267,14 +276,88 @@ def test_hotlist_mode_handoff_and_stats(model_index):
         lib.qwen_get_cpu_stats(m, C.byref(cs))
         assert cs.token_layers == flagged and cs.layer_handoffs == layers_with
         assert cs.activation_bytes == flagged * (D * 8 + 40) and cs.handoff_seconds > 0
+        # compute_seconds is the CPU MoE call alone (qwen.c:663-668)
+        assert 0 < cs.compute_seconds < cs.handoff_seconds
+        assert cs.missing_selections == missing
         prof = qg.QwenHandoffProfile()
         lib.qwen_get_handoff_profile(m, C.byref(prof))
         assert prof.layer_calls[0] == 4 and prof.layer_handoffs[0] == layers_with
         st = qg.QwenStats()
         lib.qwen_get_stats(m, C.byref(st))
         assert st.expert_handoffs == R and st.expert_requests == 10 * pos  # no uploads after pinning
+        assert st.expert_hits == hits, (st.expert_hits, hits)
         # the MTP layer is unaffected by the hotlist
         x = synth.inputs(8400, 5, D, correlated=True)
         assert_close(run_moe(m, 48, x, 0), HM.forward(x)[0], "MTP after hotlist")
     finally:
         lib.qwen_close(m)
+
+
+def q8_0_random(rows: int, cols: int, experts: int, seed: int) -> np.ndarray:
+    """GGML Q8_0 bytes (34 per 32 columns: fp16 scale, 32 int8) of random
+    rows: scale 0.02/64, values uniform in [-127, 127]."""
+    rng = np.random.default_rng(seed)
+    blocks = experts * rows * (cols // 32)
+    b = np.empty((blocks, 34), np.uint8)
+    b[:, :2] = np.frombuffer(np.float16(0.02 / 64).tobytes(), np.uint8)
+    b[:, 2:] = rng.integers(-127, 128, (blocks, 32), dtype=np.int8).view(np.uint8)
+    return b.ravel()
+
+
+def test_layers_of_different_expert_sizes(qgl, tmp_path):
+    """Cache mode over a 2-layer model whose layer 1 keeps its down experts
+    in Q8_0 (1.89x the IQ4_NL bytes of layer 0): the pinned uploader holds the
+    largest expert of any layer (qwen.c:365-367), so layer 1's uploads go
+    through and its outputs match the oracle.  The same model is refused a
+    hotlist at a batch capacity above 17 (layer 1's format has no batch
+    kernels), and an MTP layer in that format is refused at open."""
+    Dm, Fm = 1024, 256
+    s0 = synth.LayerSpec(seed=610, width=Dm, ff=Fm, down_type=20, shared=True, sh_types=(12, 12, 12))
+    s1 = synth.LayerSpec(seed=611, width=Dm, ff=Fm, down_type=20, shared=True, sh_types=(12, 12, 12))
+    a0, a1 = layer_arrays(s0), layer_arrays(s1)
+    a1 = dict(a1, down=q8_0_random(Dm, Fm, 512, 612))
+    t0 = dict(TYPES)
+    t1 = dict(TYPES, down=8)
+    files = [moe_layer_tensors(0, Dm, Fm, t0, a0, qg.row_bytes) + moe_layer_tensors(1, Dm, Fm, t1, a1, qg.row_bytes)]
+    idx = write_index(tmp_path / "two", files)
+    lib = qg.qwen()
+    m = lib.qwen_open(str(idx).encode(), 4096, 16, 4)
+    assert m, lib.qwen_last_error().decode()
+    try:
+        H1 = O.HostLayer(611, width=Dm, ff=Fm, gt=12, ut=12, dt=8, shared=True, sh_types=(12, 12, 12))
+        per = {"gate": Fm * qg.row_bytes(12, Dm), "up": Fm * qg.row_bytes(12, Dm), "down": Dm * qg.row_bytes(8, Fm)}
+        fetch = lambda name, e: a1[name][e * per[name]:(e + 1) * per[name]]
+        for il, nt in ((1, 4), (0, 3), (1, 1)):
+            x = synth.inputs(700 + il * 10 + nt, nt, Dm, correlated=True)
+            xd, out = Device(x), Device(shape=(nt, Dm), dtype=np.float32)
+            say(f"qwen_moe cache mode, layer {il}, nt={nt}")
+            assert lib.qwen_moe(m, il, out.p, xd.p, nt, 0) == 0, lib.qwen_last_error().decode()
+            if il == 1:
+                want = H1.forward(x, fetch=fetch)[0]
+                assert_close(out.get(), want, f"layer 1 (Q8_0 down) nt={nt}")
+        st = qg.QwenStats()
+        lib.qwen_get_stats(m, C.byref(st))
+        largest = 2 * Fm * qg.row_bytes(12, Dm) + Dm * qg.row_bytes(8, Fm)
+        assert st.host_staging_bytes == 2 * largest, (st.host_staging_bytes, largest)
+    finally:
+        lib.qwen_close(m)
+    # a hotlist at capacity 24 needs the batch kernels' formats in every layer
+    m = lib.qwen_open(str(idx).encode(), 4096, 16, 24)
+    assert m, lib.qwen_last_error().decode()
+    try:
+        hot = np.tile(np.arange(16, dtype=np.int32), 2)
+        assert lib.qwen_set_cpu_moe(m, qg.QWEN_CPU_MOE_FN(lambda *a: -1), None) == 0
+        assert lib.qwen_set_hotlist(m, hot.ctypes.data, 32, 4) == -1
+        assert b"layer 1" in lib.qwen_last_error(), lib.qwen_last_error()
+    finally:
+        lib.qwen_close(m)
+    # an MTP layer (blk.48) with Q8_0 down: refused above 17 tokens at open,
+    # accepted at 17 (its tensors are zero: nothing is computed here)
+    mtp = [(name.replace("blk.1.", "blk.48."), typ, dims, np.asarray(data).nbytes)
+           for name, typ, dims, data in moe_layer_tensors(1, Dm, Fm, t1, a1, qg.row_bytes)]
+    idx2 = write_index(tmp_path / "mtp", [files[0], mtp])
+    assert not lib.qwen_open(str(idx2).encode(), 4096, 16, 24)
+    assert b"MTP" in lib.qwen_last_error(), lib.qwen_last_error()
+    m = lib.qwen_open(str(idx2).encode(), 4096, 16, 17)
+    assert m, lib.qwen_last_error().decode()
+    lib.qwen_close(m)

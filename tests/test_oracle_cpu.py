@@ -292,6 +292,34 @@ def test_zipf_bias_closed_form():
     assert not np.array_equal(synth.zipf_bias(34), synth.zipf_bias(33))
 
 
+def test_resident_ranking_order():
+    """Config 4's resident set: activation count first, then accumulated
+    routed weight, then the lower id (qwen/README.md:38); ids outside 0..511
+    (pruned encodings, invalid routing) are ignored."""
+    from nebula_amd import synth
+    ids = np.array([[5, 7, 9, -1], [7, 5, 3, -7], [9, 3, 600, 2]], np.int32)
+    w = np.array([[0.1, 0.2, 0.3, 0.9], [0.3, 0.1, 0.05, 0.9], [0.1, 0.3, 0.9, 0.01]], np.float32)
+    # counts: 5:2 7:2 9:2 3:2 2:1; weights: 5:.2 7:.5 9:.4 3:.35 2:.01
+    m = synth.resident_ranking(ids, w, 3)
+    assert sorted(np.flatnonzero(m).tolist()) == [3, 7, 9]
+    assert synth.resident_ranking(ids, w, 4)[5] == 1 and synth.resident_ranking(ids, w, 4)[2] == 0
+    # equal count and weight: the lower id
+    m = synth.resident_ranking(np.array([[4, 8]], np.int32), np.array([[0.5, 0.5]], np.float32), 1)
+    assert np.flatnonzero(m).tolist() == [4]
+
+
+def test_ranking_inputs_share_the_batch_base():
+    """Context 0 of the ranking set has the verify batch's base (the batch
+    and the ranking rows differ only by their noise), the others do not."""
+    from nebula_amd import synth
+    batch = synth.inputs(77, 17, 256, correlated=True)
+    rank = synth.ranking_inputs(77, 4242, tokens=64, width=256)
+    c = lambda a, b: float(np.mean(a, 0) @ np.mean(b, 0) / np.linalg.norm(np.mean(a, 0)) / np.linalg.norm(np.mean(b, 0)))
+    assert c(batch, rank[0::8]) > 0.95
+    assert all(abs(c(batch, rank[k::8])) < 0.5 for k in range(1, 8))
+    assert not np.any(np.all(np.isclose(rank[:, None, :], batch[None, :, :]), axis=2))
+
+
 def test_layer_router_bias_changes_routing_as_logits_plus_bias():
     """nbo_layer with a router bias routes exactly as route(matmul(x) + bias)
     and returns those logits; a zero bias changes nothing."""
