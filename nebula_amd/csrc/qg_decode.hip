@@ -16,12 +16,16 @@
 //                coverage/prune, flags), then the plan: the experts in order
 //                of their first eligible selection, each cut into tiles of up
 //                to 8 selections in token order.
-//   K2 gate/up : persistent; item = (tile, 32 rows of F), the shared
-//                expert's tiles first.  B = 1 routes inline (every workgroup
-//                routes the token; workgroup 0 publishes the plan).  Products
-//                on the matrix cores (v_mfma_f32_16x16x32_f16) with exact
-//                integer weights; SwiGLU; mid rows written as fp16 hi/lo
-//                planes with their 8-row sums.
+//   K2 gate/up : B > 1 at D = 2048: one workgroup per CU, each on one
+//                expert's run of 16-row F blocks for all of the expert's
+//                tiles, so every weight row is read once (dec_gateup3).
+//                B = 1: persistent over (tile, 16 F rows) items, routing the
+//                token inline (every workgroup routes it; workgroup 0
+//                publishes the plan) (dec_gateup2).  D = 2560: the
+//                register-weight kernel (dec_gateup).  Products on the
+//                matrix cores (v_mfma_f32_16x16x32_f16) with exact integer
+//                weights; SwiGLU; mid rows written as fp16 hi/lo planes with
+//                their 8-row sums.
 //   K3 down    : persistent; item = (tile, 64 output rows): weight slab and
 //                the tile's mid planes staged in shared memory, products on
 //                the matrix cores, weighted results to per-selection slots.
@@ -396,6 +400,7 @@ constexpr int GU2_SL = 32 * 18;              // 16-byte slots per item and wave:
 constexpr int GU2_NT = 4;                     // tiles a workgroup's item range may touch
 constexpr size_t GU2_LDS = (size_t)4 * 2 * GU2_SL * 16;  // 4 waves x 2 buffers
 
+// One token (INL) at D = 2048.
 // Persistent: the layer's items (tile, 16 F rows) in tile order, split into
 // contiguous ranges, one per workgroup, so a workgroup keeps a tile's
 // activation fragments in registers across its row blocks.  Wave w takes
@@ -547,6 +552,291 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
         }
         __syncthreads();  // buffer b is free for the item after next
     }
+}
+
+// ---- K2 at D = 2048, one expert per workgroup ----
+// Every workgroup (one per CU) owns a contiguous run of one expert's 16-row F
+// blocks and computes each block for all of the expert's token tiles (up to
+// three tiles of 8 tokens) against a single copy of its weights, so an
+// expert's weight rows are read from HBM once.  The experts' blocks are dealt
+// to the workgroups in proportion to their cost (blocks x (GU3_COST + tiles):
+// a block's time is mostly its weight bytes): workgroup g takes the expert
+// whose cost range holds the midpoint of g's equal share.
+// Wave w (of 8, two per SIMD) multiplies superblock w (the K split) of the
+// block's 16 gate and 16 up rows; their bytes come by direct global->shared
+// copies into the wave's own ring of GU3_RING buffers, issued GU3_RING - 1
+// blocks ahead.  Each dequantised weight fragment feeds the MFMAs of every
+// tile.  The tiles' activation fragments are loaded once, before the first
+// copies.  Partial sums (hi and lo planes already added) meet in shared
+// memory; 2M waves apply SwiGLU, one per tile and token of each lane pair.
+constexpr int GU3_W = 8;                                          // waves per workgroup
+constexpr int GU3_RING = 3;
+constexpr int GU3_SLOT = 32 * 9;                                  // 16-byte pieces of one block and wave
+constexpr int GU3_CPB = (GU3_SLOT + 63) / 64;                     // copies per block and wave
+constexpr int GU3_MAXT = 3;                                       // tiles of 8 tokens per expert (17 tokens)
+constexpr size_t GU3_RING_BYTES = (size_t)GU3_W * GU3_RING * GU3_SLOT * 16;
+constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave x gate/up x tile x lane: float2
+constexpr size_t GU3_LDS = GU3_RING_BYTES + GU3_RED_BYTES;
+constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
+constexpr int GU3_COST = 3;                                       // a block's weight cost in units of one tile's compute
+static_assert(GU_PLAN_BYTES <= GU3_RED_BYTES, "plan scratch aliases the reduction area");
+
+// The block's products for the M tiles: y[cb][m] = the wave's partial sums
+// over its superblock for the 16 gate (cb 0) or up (cb 1) rows, column j,
+// as (token 2kq, token 2kq + 1) with the hi and lo plane rows added.
+template <int M>
+QG_DEV void gu3_products(const uint4 *wb, const qg_half8 (&af)[GU3_MAXT][8], const qg_half8 (&sf)[GU3_MAXT], int j,
+                         int kq, float2 (&y)[2][GU3_MAXT]) {
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+        const int row = cb * 16 + j, rot = row >> 3;
+        // piece c of the row (0: header, 1..8: nibbles), rotated by row / 8
+        auto piece = [&](int c) { const int x = c + rot; return wb[9 * row + (x >= 9 ? x - 9 : x)]; };
+        const Q4kHeader h = q4k_header(piece(0));
+        const uint4 ch0 = piece(1 + kq), ch1 = piece(5 + kq);
+        qg_half2 scA, ofA, scB, ofB;  // scales of groups gA, gA + 1 and gB, gB + 1
+        gq_scales(h.S[0], kq, scA, ofA);
+        gq_scales(h.S[1], kq, scB, ofB);
+        qg_f4 p0[M], p1[M], mm[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) p0[m] = p1[m] = mm[m] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int f = 0; f < 4; f++) {
+            const qg_half8 b0 = gq_frag(ch0, f, scA[f >> 1], ofA[f >> 1]), b1 = gq_frag(ch1, f, scB[f >> 1], ofB[f >> 1]);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                p0[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[m][f], b0, p0[m], 0, 0, 0);
+                p1[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[m][4 + f], b1, p1[m], 0, 0, 0);
+            }
+        }
+        const qg_half8 bm = q4k_min_frag(h);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            mm[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf[m], bm, mm[m], 0, 0, 0);
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = __builtin_fmaf(h.d, p0[m][i] + p1[m][i], -h.dmin * mm[m][i]);
+            y[cb][m] = make_float2(v[0] + v[1], v[2] + v[3]);
+        }
+    }
+}
+
+// The workgroup's blocks rb0 .. rb1 - 1 of one expert with M tiles; tn / tq:
+// the tiles' token counts and selections, in shared memory.
+template <int M>
+QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, const int (*tq)[TILE_TOK], uint4 *s_dyn,
+                    int tid) {
+    const int wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
+    const int D = A.D, D32 = D / 32, nb = rb1 - rb0;
+    const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
+    const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
+    uint4 *ring = s_dyn + (size_t)wave * GU3_RING * GU3_SLOT;
+    float2 *red = (float2 *)(s_dyn + GU3_RING_BYTES / 16);
+    // block rb -> this wave's copies into ring slot s: each row's 144 bytes of
+    // the wave's superblock as one run, rotated by row / 8 pieces so that the
+    // 16 rows of a fragment read spread over the banks
+    auto copy_block = [&](int rb, int s) {
+#pragma unroll
+        for (int i = 0; i < GU3_CPB; i++) {
+            const int sl = i * 64 + lane, row = sl / 9, pc = sl - 9 * row, rot = row >> 3;
+            const int c = pc - rot + (pc < rot ? 9 : 0);
+            if (sl < GU3_SLOT)
+                dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 144 + 16 * c,
+                              ring + (size_t)s * GU3_SLOT + i * 64);
+        }
+    };
+    // the first blocks' weights go out first; then the tiles' activation
+    // fragments for this wave's superblock: plane row r = (token r/2, plane
+    // r%2), rows past a tile's tokens repeating its last
+    for (int i = 0; i < GU3_RING - 1 && i < nb; i++) copy_block(rb0 + i, i);
+    qg_half8 af[GU3_MAXT][8], sf[GU3_MAXT];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int r = 2 * min(j >> 1, tn[m] - 1) + (j & 1), sl = tq[m][r >> 1];
+        const int tok = e < 0 ? sl - MS : sl / QG_TOP;
+        const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 256 + kq * 8;
+        const _Float16 *xs = A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)wave * 8;
+#pragma unroll
+        for (int f = 0; f < 8; f++) af[m][f] = ld_frag(xr + f * 32);
+        sf[m] = kq ? qg_half8{} : ld_frag(xs);
+    }
+    const int fmt = e < 0 ? A.sh_fmt : A.fmt;
+    for (int it = 0; it < nb; it++) {
+        // the block GU3_RING - 1 ahead into the slot the previous block used
+        if (it + GU3_RING - 1 < nb) copy_block(rb0 + it + GU3_RING - 1, (it + GU3_RING - 1) % GU3_RING);
+        const int ahead = min(GU3_RING - 1, nb - 1 - it);  // later blocks in flight
+        if (ahead >= 2) wait_vmem_but<2 * GU3_CPB>();
+        else if (ahead == 1) wait_vmem_but<GU3_CPB>();
+        else wait_vmem();
+        float2 y[2][GU3_MAXT];
+        gu3_products<M>(ring + (size_t)(it % GU3_RING) * GU3_SLOT, af, sf, j, kq, y);
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int m = 0; m < M; m++) red[((wave * 2 + cb) * GU3_MAXT + m) * 64 + lane] = y[cb][m];
+        __syncthreads();
+        if (wave < 2 * M) {
+            // tile m = wave / 2, token 2 kq + t2 of lane's pair, F row j of the block
+            const int m = wave >> 1, t2 = wave & 1, n = tn[m];
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int w = 0; w < GU3_W; w++) {
+                const float2 ga = red[((w * 2 + 0) * GU3_MAXT + m) * 64 + lane], ua = red[((w * 2 + 1) * GU3_MAXT + m) * 64 + lane];
+                g += t2 ? ga.y : ga.x;
+                u += t2 ? ua.y : ua.x;
+            }
+            const int rb = rb0 + it, frow = rb * GU2_ROWS + j, pos = plane_pos(fmt, frow);
+            const float mv = qg_swiglu_fast(g, u);
+            float s8 = mv;  // sum over the 8 rows of this lane's group
+            s8 += __shfl_xor(s8, 1);
+            s8 += __shfl_xor(s8, 2);
+            s8 += __shfl_xor(s8, 4);
+            const int idx = 2 * kq + t2;
+            if (idx < n) {
+                const int sl = tq[m][idx];
+                _Float16 *mp = A.midp + (size_t)sl * 2 * A.F;
+                const _Float16 hv = (_Float16)mv;
+                mp[pos] = hv;
+                mp[A.F + pos] = (_Float16)(mv - (float)hv);
+                if ((j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
+            }
+        }
+        __syncthreads();  // the reduction area is free
+    }
+}
+
+template <bool INL>
+__global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
+    extern __shared__ uint4 s_dyn[];
+    __shared__ int s_xe[GU3_MAXX], s_xk[GU3_MAXX], s_xm[GU3_MAXX], s_cum[GU3_MAXX + 1];
+    __shared__ int s_nx;
+    __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
+    __shared__ float s_rv[64];
+    __shared__ int s_ri[64];
+    __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
+    __shared__ int s_nent;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int RBK = A.F / GU2_ROWS;
+    const uint32_t warm = gu_warm(A, tid);
+    const GuPlan P = gu_plan_at(s_dyn + GU3_RING_BYTES / 16);  // scratch in the reduction area
+    if (INL) {
+        if (wave == 0) gu_route_inline(A, lane, s_rv, s_ri, s_rank, s_rid, &s_nent);
+        __syncthreads();
+    } else {
+        gu_build_plan(A, tid, P);
+    }
+    const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    if (wave == 0) {
+        // the expert list: the shared expert, then the routed experts in plan
+        // order (first routed tile index, tile count) and the prefix of their
+        // costs (F blocks x tiles)
+        if (lane == 0 && sh) { s_xe[0] = -1; s_xk[0] = -1; s_xm[0] = sh_tiles; }
+        int nx = sh;
+        const unsigned long long below = (1ULL << lane) - 1ULL;
+        if (INL) {
+            if (lane < s_nent) { s_xe[sh + lane] = s_rid[lane]; s_xk[sh + lane] = lane; s_xm[sh + lane] = 1; }
+            nx += s_nent;
+        } else {
+            const int ntl = *P.ntiles;
+            for (int c0 = 0; c0 < ntl; c0 += 64) {
+                const int k = c0 + lane, te = k < ntl ? P.tile[k] : -1;
+                const bool first = te >= 0 && (te >> 16) == 0;
+                const unsigned long long b = __ballot(first);
+                if (first) {
+                    const int x = nx + __popcll(b & below), ex = te & 0xffff;
+                    s_xe[x] = ex;
+                    s_xk[x] = k;
+                    s_xm[x] = (__popc(P.mask[ex]) + TILE_TOK - 1) / TILE_TOK;
+                }
+                nx += __popcll(b);
+            }
+            if (blockIdx.x == 0 && lane == 0) A.pl->n_tiles = ntl;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // cost prefix, RBK (GU3_COST + M) per expert: a block's time is set by
+        // its weight bytes (the same for every tile count) plus a little
+        // compute per tile; tile counts (1..3) summed by bit-sliced ballots
+        int carry = 0;
+        for (int c0 = 0; c0 < nx; c0 += 64) {
+            const int x = c0 + lane, mx = x < nx ? s_xm[x] : 0;
+            const unsigned long long b0 = __ballot(mx & 1), b1 = __ballot(mx & 2), bv = __ballot(x < nx);
+            const unsigned long long upto = below | (1ULL << lane);
+            if (x < nx)
+                s_cum[x + 1] = RBK * (carry + GU3_COST * __popcll(bv & upto) + __popcll(b0 & upto) + 2 * __popcll(b1 & upto));
+            carry += GU3_COST * __popcll(bv) + __popcll(b0) + 2 * __popcll(b1);
+        }
+        if (lane == 0) { s_cum[0] = 0; s_nx = nx; }
+    }
+    __syncthreads();
+    asm volatile("" ::"v"(warm));  // the warming loads have landed
+    const int nx = s_nx;
+    if (nx == 0) return;  // block-uniform: nothing computed on the device
+    // this workgroup's expert: the one whose cost range holds the midpoint of
+    // its share; its blocks are split evenly over the expert's workgroups
+    // (C <= RBK (GU3_COST + 3) 173 and G <= 1024: 32-bit products suffice)
+    const uint32_t C = (uint32_t)s_cum[nx], G = gridDim.x, g = blockIdx.x;
+    const uint32_t pos = ((2 * g + 1) * C) / (2 * G);
+    int x = 0;
+    for (int c0 = 0; c0 < nx; c0 += 64) {
+        const int xx = c0 + lane;
+        x += __popcll(__ballot(xx < nx && (uint32_t)s_cum[xx + 1] <= pos));
+    }
+    // first workgroup of expert x: the smallest g' with (2g'+1) C >= 2 G cum[x]
+    auto first_wg = [&](int xx) -> uint32_t {
+        if (xx >= nx) return G;
+        const uint32_t t = 2 * G * (uint32_t)s_cum[xx];
+        return t <= C ? 0u : (t - C + 2 * C - 1) / (2 * C);
+    };
+    const uint32_t gA = first_wg(x), gB = first_wg(x + 1), W = gB - gA, kx = g - gA;
+    const int rb0 = (int)(RBK * kx / W), rb1 = (int)(RBK * (kx + 1) / W);
+    const int e = s_xe[x], M = s_xm[x];
+    if (wave == 0) {
+        // the expert's tiles: n tokens each and their selections (shared expert:
+        // MS + token); the expert's first workgroup publishes its routed tiles
+        // for the down kernel
+        const int m = lane >> 3, slot = lane & 7;
+        if (m < M) {
+            int n, q = -1;
+            if (e < 0) {
+                n = min(TILE_TOK, A.nt - TILE_TOK * m);
+                if (slot < n) q = MS + TILE_TOK * m + slot;
+            } else if (INL) {
+                n = 1;
+                if (slot == 0) q = s_rank[s_xk[x]];
+            } else {
+                const uint32_t msk = P.mask[e];
+                n = min(TILE_TOK, __popc(msk) - TILE_TOK * m);
+                if (slot < n) {
+                    // the (8 m + slot)-th token choosing e (the k-th set bit of
+                    // the mask, found by halving), and the rank it gave e
+                    int k = TILE_TOK * m + slot, t = 0;
+#pragma unroll
+                    for (int w = 16; w >= 1; w >>= 1) {
+                        const int c = __popc((msk >> t) & ((1u << w) - 1u));
+                        if (k >= c) { k -= c; t += w; }
+                    }
+                    int r = 0;
+#pragma unroll
+                    for (int rr = 0; rr < QG_TOP; rr++) r = P.ids[t * QG_TOP + rr] == e ? rr : r;
+                    q = t * QG_TOP + r;
+                }
+                if (kx == 0) {
+                    const int k = s_xk[x] + m;
+                    if (slot < n) A.pl->tile[k].q[slot] = q;
+                    if (slot == 0) { A.pl->tile[k].e = e; A.pl->tile[k].n = n; }
+                }
+            }
+            if (slot < n) s_tq[m][slot] = q;
+            if (slot == 0) s_tn[m] = n;
+        }
+    }
+    __syncthreads();  // the plan scratch is read; the reduction area may be reused
+    if (rb1 <= rb0) return;  // block-uniform
+    if (M == 1) gu3_run<1>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
+    else if (M == 2) gu3_run<2>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
+    else gu3_run<3>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
 }
 
 // Shared-memory layout of the gate/up kernel (fp16 units): 16 staged plane
@@ -962,18 +1252,27 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
         }
     }
     if (A.stats && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
-        // counters in token order (deterministic, unlike the reference's atomics)
+        // counters in token order (deterministic, unlike the reference's
+        // atomics), summed in registers and added once
+        uint64_t tl = 0, ms = 0, ss = 0, av = 0;
+        double mass = A.stats->skipped_mass;
         for (int u = 0; u < A.nt; u++) {
-            const int f = A.pl->flag[u];
+            const int f = A.pl->flag[u], mi = A.pl->missing[u];
+            const double mu = A.pl->mass[u];
             if (f == 3) continue;
-            A.stats->token_layers += 1;
-            A.stats->missing_selections += (uint64_t)A.pl->missing[u];
+            tl += 1;
+            ms += (uint64_t)mi;
             if (f == 1) {
-                A.stats->skipped_selections += (uint64_t)A.pl->missing[u];
-                A.stats->avoided_token_handoffs += 1;
-                A.stats->skipped_mass += A.pl->mass[u];
+                ss += (uint64_t)mi;
+                av += 1;
+                mass += mu;
             }
         }
+        A.stats->token_layers += tl;
+        A.stats->missing_selections += ms;
+        A.stats->skipped_selections += ss;
+        A.stats->avoided_token_handoffs += av;
+        A.stats->skipped_mass = mass;
     }
 }
 
@@ -1207,9 +1506,11 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     int nwg2 = items2 < GU_WGS ? items2 : GU_WGS;
     if ((long long)nwg2 * per2 < items2) nwg2 = (items2 + per2 - 1) / per2;
     if (D == 2048) {
-        // F is a multiple of 32 (validate_layer), so of GU2_ROWS
+        // F is a multiple of 32 (validate_layer), so of GU2_ROWS; one
+        // workgroup per CU, each on one expert's run of F blocks
+        // (one token: the per-tile kernel with its finer split, 512 workgroups)
         if (inl) dec_launch(2, dec_gateup2_kernel<true>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
-        else dec_launch(2, dec_gateup2_kernel<false>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
+        else dec_launch(2, dec_gateup3_kernel<false>, dim3(qg_cu_count()), dim3(64 * GU3_W), GU3_LDS, s, G2);
     } else {
         // D = 2560 (dec_ok): the register-weight kernel, 10 superblocks per row
         const size_t gu_bytes = (size_t)gu_lds(D).total * 2;

@@ -23,8 +23,23 @@ def load(name):
     return meta, arrays
 
 
+def fixture_inputs(meta, arrays):
+    """The fixture's input rows: stored, or (production shapes) regenerated
+    from the seed and checked against the stored SHA-256."""
+    import hashlib
+    x = synth.inputs(meta["input_seed"], meta["tokens"], meta["width"], correlated=meta["correlated"])
+    if "x" in arrays:
+        np.testing.assert_array_equal(x.view('u4'), arrays["x"].view('u4'))
+    else:
+        assert hashlib.sha256(np.ascontiguousarray(x).view(np.uint8).tobytes()).hexdigest() == meta["x_sha256"]
+    return x
+
+
 def test_fixtures_present():
-    assert len(CASES) >= 5, CASES
+    assert len(CASES) >= 9, CASES
+    # the production shapes of the benchmark's kernels are among them
+    widths = {load(c)[0]["width"] for c in CASES}
+    assert {256, 2048, 2560} <= widths, widths
 
 
 @pytest.mark.parametrize("name", CASES)
@@ -33,8 +48,7 @@ def test_oracle_reproduces_fixture(name):
     meta, a = load(name)
     H = O.HostLayer(meta["seed"], width=meta["width"], ff=meta["ff"], gt=meta["gate_type"], ut=meta["up_type"],
                     dt=meta["down_type"], shared=meta["shared"], sh_types=tuple(meta["shared_types"]))
-    x = synth.inputs(meta["input_seed"], meta["tokens"], meta["width"], correlated=meta["correlated"])
-    np.testing.assert_array_equal(x.view('u4'), a["x"].view('u4'))
+    x = fixture_inputs(meta, a)
     out, ids, w, logits, flags, st = H.forward(x, a.get("resident"))
     sha = lambda v: hashlib.sha256(np.ascontiguousarray(v).view(np.uint8).tobytes()).hexdigest()
     for key, h in meta["sha256"].items():

@@ -2,7 +2,11 @@
 the device generator writes the recorded bytes (SHA-256), qg_moe_forward
 gives the recorded routing, weights and flags bit for bit and the recorded
 outputs within max-abs 1e-3 / rel-L2 1e-4 (rows computed on the device,
-flag < 2), and qg_moe_dispatch gives the recorded CSR bit for bit."""
+flag < 2), and qg_moe_dispatch gives the recorded CSR bit for bit.  The
+production-shape fixtures run the benchmark's kernels without the oracle
+library: D = 2048 at one token the inline-routing gate/up and the fused
+down+combine, at 17 tokens the one-expert-per-workgroup gate/up, the down and
+the combine; D = 2560 the register-weight gate/up at 1 and 4 tokens."""
 import ctypes as C
 import hashlib
 import sys
@@ -12,7 +16,7 @@ import pytest
 
 from nebula_amd import qg, synth
 from nebula_amd.qg import Device, call
-from test_golden import CASES, load
+from test_golden import CASES, fixture_inputs, load
 
 pytestmark = pytest.mark.gpu
 
@@ -38,7 +42,7 @@ def test_device_matches_fixture(qgl, name):
         assert got == h, key
     nt, D = meta["tokens"], meta["width"]
     fw = synth.Forward(D, meta["ff"], nt)
-    fw.x.set(a["x"])
+    fw.x.set(fixture_inputs(meta, a))
     fw.run(L, nt)
     call("sync")
     np.testing.assert_array_equal(fw.ids.get()[:nt], a["ids"])

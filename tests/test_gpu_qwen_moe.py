@@ -319,6 +319,7 @@ def test_layers_of_different_expert_sizes(qgl, tmp_path):
     t0 = dict(TYPES)
     t1 = dict(TYPES, down=8)
     files = [moe_layer_tensors(0, Dm, Fm, t0, a0, qg.row_bytes) + moe_layer_tensors(1, Dm, Fm, t1, a1, qg.row_bytes)]
+    (tmp_path / "two").mkdir()
     idx = write_index(tmp_path / "two", files)
     lib = qg.qwen()
     m = lib.qwen_open(str(idx).encode(), 4096, 16, 4)
@@ -355,6 +356,7 @@ def test_layers_of_different_expert_sizes(qgl, tmp_path):
     # accepted at 17 (its tensors are zero: nothing is computed here)
     mtp = [(name.replace("blk.1.", "blk.48."), typ, dims, np.asarray(data).nbytes)
            for name, typ, dims, data in moe_layer_tensors(1, Dm, Fm, t1, a1, qg.row_bytes)]
+    (tmp_path / "mtp").mkdir()
     idx2 = write_index(tmp_path / "mtp", [files[0], mtp])
     assert not lib.qwen_open(str(idx2).encode(), 4096, 16, 24)
     assert b"MTP" in lib.qwen_last_error(), lib.qwen_last_error()
