@@ -77,6 +77,14 @@ def gateup_bytes(nt: int, unique: float, shared: bool) -> float:
     return (unique + (1 if shared else 0)) * GATEUP_BYTES + nt * D * 4
 
 
+def down_bytes(nt: int, unique: float, shared: bool) -> float:
+    """The down kernel's algorithmic bytes: each touched expert's down rows
+    once, the mid rows read (fp16 hi and lo planes, one row per selection and
+    shared-expert token) and the weighted rows written to the selection slots."""
+    rows = nt * TOP + (nt if shared else 0)
+    return (unique + (1 if shared else 0)) * (EXPERT_BYTES - GATEUP_BYTES) + rows * FF * 4 + rows * D * 4
+
+
 def resident_set(layer: synth.DeviceLayer, batch_seed: int, noise_seed: int, count: int = 128) -> np.ndarray:
     """Config 4's resident experts: the `count` best-ranked over 4096 seeded
     synthetic tokens from 8 correlated contexts, one of them the verify
@@ -744,7 +752,8 @@ def counter_pass(args) -> int:
         layers = []
         for i in range(len(wl.layers)):
             u = wl.unique_experts(i)
-            layers.append({"layer": i, "unique_experts": u, "gate_up_algorithmic_bytes": int(gateup_bytes(batch, u, wl.shared))})
+            layers.append({"layer": i, "unique_experts": u, "gate_up_algorithmic_bytes": int(gateup_bytes(batch, u, wl.shared)),
+                           "down_algorithmic_bytes": int(down_bytes(batch, u, wl.shared))})
         info = {"config": args.config, "batch": batch, "layers": layers}
     qg.call("sync")
     print(json.dumps(info), flush=True)
