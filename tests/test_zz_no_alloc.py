@@ -2,9 +2,13 @@
 workspace (no allocation) equals qg_moe_forward with a caller workspace bit
 for bit, on two calls in a row (the second with fewer tokens, so the shared
 workspace holds the first call's contents), on the decode and the prefill
-paths; layers whose workspace exceeds the static size are rejected."""
+paths; layers whose workspace exceeds the static size are rejected; the
+entry point captured into a graph (also as its first call in a fresh
+process) replays bit-identical to the eager layer."""
 import ctypes as C
+import subprocess
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -62,3 +66,44 @@ def test_noalloc_rejects_oversize(layer):
     assert lib.qg_moe_forward_noalloc(out.p, ids.p, w.p, None, None, x.p, nt, C.byref(layer.desc)) != 0
     assert lib.qg_moe_forward_noalloc(out.p, ids.p, w.p, None, None, x.p, 0, C.byref(layer.desc)) != 0
     call("sync")
+
+
+@pytest.mark.parametrize("nt", [4, 40])
+def test_noalloc_graph_replays(layer, nt):
+    """qg_moe_forward_noalloc captured (qg_graph_begin/end) and replayed three
+    times, with the program's own eager work and a synchronisation between
+    replays: every replay equals the eager qg_moe_forward bit for bit."""
+    x = synth.inputs(800 + nt, nt, 2048, correlated=True)
+    fw = synth.Forward(2048, 512, nt)
+    fw.x.set(x)
+    fw.run(layer, nt)
+    call("sync")
+    want = [fw.out.get()[:nt].copy(), fw.ids.get()[:nt].copy(), fw.w.get()[:nt].copy()]
+    out = Device(shape=(nt, 2048), dtype=np.float32)
+    ids = Device(shape=(nt, 10), dtype=np.int32)
+    w = Device(shape=(nt, 10), dtype=np.float32)
+    g = C.c_void_p()
+    say(f"capture noalloc nt={nt}")
+    call("graph_begin", C.byref(g))
+    call("moe_forward_noalloc", out.p, ids.p, w.p, None, None, fw.x.p, nt, C.byref(layer.desc))
+    call("graph_end", g)
+    try:
+        for r in range(3):
+            call("graph_launch", g)
+            call("sync")
+            for got, exp in zip((out.get(), ids.get(), w.get()), want):
+                np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32), err_msg=f"replay {r}")
+            fw.run(layer, nt)
+            call("sync")
+    finally:
+        qg.lib().qg_graph_destroy(g)
+
+
+def test_noalloc_first_call_under_capture():
+    """A fresh process whose first qg_moe_forward_noalloc call is made under
+    graph capture (tests/noalloc_capture_child.py), at 4 and 40 tokens."""
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    say("child process: first noalloc call under capture")
+    r = subprocess.run([sys.executable, "-u", str(child), "4", "40"], capture_output=True, text=True, timeout=300)
+    say(r.stdout.strip())
+    assert r.returncode == 0, r.stdout + r.stderr
