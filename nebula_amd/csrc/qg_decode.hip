@@ -1288,14 +1288,14 @@ struct Dn1Args {
 };
 constexpr int DN1_ROWS = 16;             // output rows per workgroup
 constexpr int DN1_SL = DN1_ROWS * 288 / 16;  // 16-byte slots of 16 rows of 288 bytes
-constexpr int DN1_W = 8;                 // waves per workgroup
-constexpr int DN1_EPW = 2;               // entries per wave (10 routed + 1 shared over 8 waves)
+constexpr int DN1_W = 16;                // waves per workgroup
+constexpr int DN1_EPW = 1;               // entries per wave (10 routed + 1 shared, each on its own wave)
 // weight rows per wave and entry, then every entry's mid planes (F = 512) and 8-row sums
 constexpr size_t DN1_LDS = (size_t)DN1_W * DN1_EPW * DN1_SL * 16 + (size_t)(QG_TOP + 1) * 2 * 512 * 2 + (size_t)(QG_TOP + 1) * 64 * 4;
 
 // One token (the plan's entries k = eligible ranks in order, then the shared
-// expert): workgroup b owns output rows 16b .. 16b + 15; wave w (of 8) computes
-// the entries k = w, w + 8 (their 16 weight rows, the entries' mid planes
+// expert): workgroup b owns output rows 16b .. 16b + 15; wave w (of 16)
+// computes entry k = w (its 16 weight rows, the entries' mid planes
 // and 8-row sums all copied into shared memory by direct global->shared
 // copies at once), each weighted by its routing weight; wave 0 then sums them in
 // rank order, adds sigmoid(logit) times the shared expert's row and the
