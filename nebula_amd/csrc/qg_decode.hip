@@ -65,6 +65,7 @@ struct DecTile { int e, n, q[TILE_TOK]; };
 struct DecPlan {
     int flag[MB]; int missing[MB]; double mass[MB];
     int n_tiles;                             // routed tiles
+    uint32_t emask[QG_EXPERTS];              // B > 1: bit t set when token t has an eligible selection of the expert
     DecTile tile[MAX_TILES];
 };
 
@@ -110,6 +111,7 @@ struct RouterArgs {
     _Float16 *xp, *xsp;             // planes [nt][2][D] (Q4_K order); planes of 32-group sums [nt][2][D/32]
     int row_blocks;                 // blockIdx.x < row_blocks: router rows; above: planes
     const float *bias;              // F32 [512] added to the expert logits, or null
+    uint32_t *emask;                // the plan's per-expert token masks, cleared by the first plane block, or null
 };
 
 
@@ -148,6 +150,8 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
     const int nt = A.nt;
     if (blockIdx.x >= A.row_blocks) {
+        if (A.emask && blockIdx.x == A.row_blocks)
+            for (int i = threadIdx.x; i < QG_EXPERTS; i += 256) A.emask[i] = 0u;  // the routing kernel sets them
         const int t = (blockIdx.x - A.row_blocks) * 4 + wave;
         if (t >= nt) return;  // whole wave; the plane blocks have no block barrier
         const float *xr = A.x + (size_t)t * DW;
@@ -237,6 +241,9 @@ __global__ __launch_bounds__(64) void dec_route_kernel(RouteArgs A) {
     if (lane < QG_TOP) {
         A.ids[t * QG_TOP + lane] = id;
         A.w[t * QG_TOP + lane] = wv;
+        // the gate/up kernel's plan: the tokens of each expert's eligible
+        // selections (pruned selections carry -id-2; flag-2/3 tokens have none)
+        if (flag < 2 && id >= 0 && id < QG_EXPERTS) atomicOr(&A.pl->emask[id], 1u << t);
     }
     if (lane == 0) {
         A.pl->flag[t] = flag;
@@ -579,7 +586,6 @@ constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave
 constexpr size_t GU3_LDS = GU3_RING_BYTES + GU3_RED_BYTES;
 constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
 constexpr int GU3_COST = 3;                                       // a block's weight cost in units of one tile's compute
-static_assert(GU_PLAN_BYTES <= GU3_RED_BYTES, "plan scratch aliases the reduction area");
 
 // The block's products for the M tiles: y[cb][m] = the wave's partial sums
 // over its superblock for the 16 gate (cb 0) or up (cb 1) rows, column j,
@@ -621,45 +627,80 @@ QG_DEV void gu3_products(const uint4 *wb, const qg_half8 (&af)[GU3_MAXT][8], con
     }
 }
 
-// The workgroup's blocks rb0 .. rb1 - 1 of one expert with M tiles; tn / tq:
-// the tiles' token counts and selections, in shared memory.
+// This wave's copies of F block rb of an expert (gate rows gm, up rows um)
+// into its ring slot: each row's 144 bytes of the wave's superblock as one
+// run, rotated by row / 8 pieces so that the 16 rows of a fragment read
+// spread over the banks.
+QG_DEV void gu3_copy(const GuArgs &A, const uint8_t *gm, const uint8_t *um, int rb, uint4 *slot, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < GU3_CPB; i++) {
+        const int sl = i * 64 + lane, row = sl / 9, pc = sl - 9 * row, rot = row >> 3;
+        const int c = pc - rot + (pc < rot ? 9 : 0);
+        if (sl < GU3_SLOT)
+            dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 144 + 16 * c,
+                          slot + i * 64);
+    }
+}
+
+// The selection of each of the expert's tile slots (t*10 + the rank token t
+// gave expert e, from the routing ids; shared expert: MS + t), by one wave
+// (lane l: tile l / 8, slot l % 8); with k0 >= 0 the tiles are also published
+// as routed tiles k0 .. k0 + M - 1 of the plan for the down kernel.
+QG_DEV void gu3_selections(const GuArgs &A, int e, int M, const int *tn, const int (*tt)[TILE_TOK], int (*tq)[TILE_TOK], int k0,
+                           int lane) {
+    const int m = lane >> 3, slot = lane & 7;
+    if (m >= M) return;
+    const int n = tn[m];
+    int q = -1;
+    if (slot < n) {
+        const int t = tt[m][slot];
+        if (e < 0) {
+            q = MS + t;
+        } else {
+            const int2 *row = (const int2 *)(A.ids + (size_t)t * QG_TOP);  // 8-byte aligned
+            int r = 0;
+#pragma unroll
+            for (int i = 0; i < QG_TOP / 2; i++) {
+                const int2 v = row[i];
+                r = v.x == e ? 2 * i : v.y == e ? 2 * i + 1 : r;
+            }
+            q = t * QG_TOP + r;
+        }
+        tq[m][slot] = q;
+    }
+    if (k0 >= 0) {
+        if (slot < n) A.pl->tile[k0 + m].q[slot] = q;
+        if (slot == 0) { A.pl->tile[k0 + m].e = e; A.pl->tile[k0 + m].n = n; }
+    }
+}
+
+// The workgroup's blocks rb0 .. rb1 - 1 of one expert with M tiles, whose
+// first GU3_RING - 1 blocks' copies are in flight; tn / tt: the tiles' token
+// counts and tokens, tq: their selections (written by wave 0 here, read after
+// the first block's barrier), all in shared memory.
 template <int M>
-QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, const int (*tq)[TILE_TOK], uint4 *s_dyn,
-                    int tid) {
+QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, const int (*tt)[TILE_TOK], int (*tq)[TILE_TOK],
+                    int k0, uint4 *s_dyn, int tid) {
     const int wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int D = A.D, D32 = D / 32, nb = rb1 - rb0;
     const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
     const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
     uint4 *ring = s_dyn + (size_t)wave * GU3_RING * GU3_SLOT;
     float2 *red = (float2 *)(s_dyn + GU3_RING_BYTES / 16);
-    // block rb -> this wave's copies into ring slot s: each row's 144 bytes of
-    // the wave's superblock as one run, rotated by row / 8 pieces so that the
-    // 16 rows of a fragment read spread over the banks
-    auto copy_block = [&](int rb, int s) {
-#pragma unroll
-        for (int i = 0; i < GU3_CPB; i++) {
-            const int sl = i * 64 + lane, row = sl / 9, pc = sl - 9 * row, rot = row >> 3;
-            const int c = pc - rot + (pc < rot ? 9 : 0);
-            if (sl < GU3_SLOT)
-                dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 144 + 16 * c,
-                              ring + (size_t)s * GU3_SLOT + i * 64);
-        }
-    };
-    // the first blocks' weights go out first; then the tiles' activation
-    // fragments for this wave's superblock: plane row r = (token r/2, plane
-    // r%2), rows past a tile's tokens repeating its last
-    for (int i = 0; i < GU3_RING - 1 && i < nb; i++) copy_block(rb0 + i, i);
+    // the tiles' activation fragments for this wave's superblock: plane row
+    // r = (token r/2, plane r%2), rows past a tile's tokens repeating its last
     qg_half8 af[GU3_MAXT][8], sf[GU3_MAXT];
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        const int r = 2 * min(j >> 1, tn[m] - 1) + (j & 1), sl = tq[m][r >> 1];
-        const int tok = e < 0 ? sl - MS : sl / QG_TOP;
+        const int r = 2 * min(j >> 1, tn[m] - 1) + (j & 1), tok = tt[m][r >> 1];
         const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 256 + kq * 8;
         const _Float16 *xs = A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)wave * 8;
 #pragma unroll
         for (int f = 0; f < 8; f++) af[m][f] = ld_frag(xr + f * 32);
         sf[m] = kq ? qg_half8{} : ld_frag(xs);
     }
+    if (wave == 0) gu3_selections(A, e, M, tn, tt, tq, k0, lane);
+    auto copy_block = [&](int rb, int s) { gu3_copy(A, gm, um, rb, ring + (size_t)s * GU3_SLOT, wave, lane); };
     const int fmt = e < 0 ? A.sh_fmt : A.fmt;
     for (int it = 0; it < nb; it++) {
         // the block GU3_RING - 1 ahead into the slot the previous block used
@@ -705,53 +746,44 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
     }
 }
 
-template <bool INL>
+// B = 2..17 at D = 2048.  The expert list: the shared expert, then the routed
+// experts in ascending id, each with the tokens whose eligible selections
+// chose it (the routing kernel's per-expert masks), cut into tiles of up to 8
+// tokens in token order; the routed tiles are numbered in list order and
+// published by each expert's first workgroup for the down kernel.
 __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
     __shared__ int s_xe[GU3_MAXX], s_xk[GU3_MAXX], s_xm[GU3_MAXX], s_cum[GU3_MAXX + 1];
+    __shared__ uint32_t s_xt[GU3_MAXX];
     __shared__ int s_nx;
-    __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
-    __shared__ float s_rv[64];
-    __shared__ int s_ri[64];
-    __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
-    __shared__ int s_nent;
+    __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tt[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int RBK = A.F / GU2_ROWS;
     const uint32_t warm = gu_warm(A, tid);
-    const GuPlan P = gu_plan_at(s_dyn + GU3_RING_BYTES / 16);  // scratch in the reduction area
-    if (INL) {
-        if (wave == 0) gu_route_inline(A, lane, s_rv, s_ri, s_rank, s_rid, &s_nent);
-        __syncthreads();
-    } else {
-        gu_build_plan(A, tid, P);
-    }
     const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     if (wave == 0) {
-        // the expert list: the shared expert, then the routed experts in plan
-        // order (first routed tile index, tile count) and the prefix of their
-        // costs (F blocks x tiles)
-        if (lane == 0 && sh) { s_xe[0] = -1; s_xk[0] = -1; s_xm[0] = sh_tiles; }
-        int nx = sh;
+        uint32_t em[QG_EXPERTS / 64];
+#pragma unroll
+        for (int i = 0; i < QG_EXPERTS / 64; i++) em[i] = A.pl->emask[64 * i + lane];
+        if (lane == 0 && sh) { s_xe[0] = -1; s_xk[0] = -1; s_xm[0] = sh_tiles; s_xt[0] = 0u; }
         const unsigned long long below = (1ULL << lane) - 1ULL;
-        if (INL) {
-            if (lane < s_nent) { s_xe[sh + lane] = s_rid[lane]; s_xk[sh + lane] = lane; s_xm[sh + lane] = 1; }
-            nx += s_nent;
-        } else {
-            const int ntl = *P.ntiles;
-            for (int c0 = 0; c0 < ntl; c0 += 64) {
-                const int k = c0 + lane, te = k < ntl ? P.tile[k] : -1;
-                const bool first = te >= 0 && (te >> 16) == 0;
-                const unsigned long long b = __ballot(first);
-                if (first) {
-                    const int x = nx + __popcll(b & below), ex = te & 0xffff;
-                    s_xe[x] = ex;
-                    s_xk[x] = k;
-                    s_xm[x] = (__popc(P.mask[ex]) + TILE_TOK - 1) / TILE_TOK;
-                }
-                nx += __popcll(b);
+        int nx = sh, ntl = 0;
+#pragma unroll
+        for (int i = 0; i < QG_EXPERTS / 64; i++) {
+            // tiles per expert (1..3 for up to 17 tokens) as bit-sliced ballots
+            const int mx = em[i] ? (__popc(em[i]) + TILE_TOK - 1) / TILE_TOK : 0;
+            const unsigned long long b = __ballot(em[i] != 0u), b0 = __ballot(mx & 1), b1 = __ballot(mx & 2);
+            if (em[i]) {
+                const int x = nx + __popcll(b & below);
+                s_xe[x] = 64 * i + lane;
+                s_xm[x] = mx;
+                s_xk[x] = ntl + __popcll(b0 & below) + 2 * __popcll(b1 & below);
+                s_xt[x] = em[i];
             }
-            if (blockIdx.x == 0 && lane == 0) A.pl->n_tiles = ntl;
+            nx += __popcll(b);
+            ntl += __popcll(b0) + 2 * __popcll(b1);
         }
+        if (blockIdx.x == 0 && lane == 0) A.pl->n_tiles = ntl;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -791,52 +823,45 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     };
     const uint32_t gA = first_wg(x), gB = first_wg(x + 1), W = gB - gA, kx = g - gA;
     const int rb0 = (int)(RBK * kx / W), rb1 = (int)(RBK * (kx + 1) / W);
-    const int e = s_xe[x], M = s_xm[x];
+    const int e = s_xe[x], M = s_xm[x], k0 = kx == 0 && e >= 0 ? s_xk[x] : -1;
+    // the first blocks' weights go out first
+    {
+        const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
+        const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
+        uint4 *ring = s_dyn + (size_t)wave * GU3_RING * GU3_SLOT;
+        for (int i = 0; i < GU3_RING - 1 && rb0 + i < rb1; i++) gu3_copy(A, gm, um, rb0 + i, ring + (size_t)i * GU3_SLOT, wave, lane);
+    }
     if (wave == 0) {
-        // the expert's tiles: n tokens each and their selections (shared expert:
-        // MS + token); the expert's first workgroup publishes its routed tiles
-        // for the down kernel
+        // the expert's tiles: n tokens each, in token order
         const int m = lane >> 3, slot = lane & 7;
         if (m < M) {
-            int n, q = -1;
+            int n, t = 0;
             if (e < 0) {
                 n = min(TILE_TOK, A.nt - TILE_TOK * m);
-                if (slot < n) q = MS + TILE_TOK * m + slot;
-            } else if (INL) {
-                n = 1;
-                if (slot == 0) q = s_rank[s_xk[x]];
+                t = TILE_TOK * m + slot;
             } else {
-                const uint32_t msk = P.mask[e];
+                const uint32_t msk = s_xt[x];
                 n = min(TILE_TOK, __popc(msk) - TILE_TOK * m);
-                if (slot < n) {
-                    // the (8 m + slot)-th token choosing e (the k-th set bit of
-                    // the mask, found by halving), and the rank it gave e
-                    int k = TILE_TOK * m + slot, t = 0;
+                // the (8 m + slot)-th set bit of the mask, found by halving
+                int k = TILE_TOK * m + slot;
 #pragma unroll
-                    for (int w = 16; w >= 1; w >>= 1) {
-                        const int c = __popc((msk >> t) & ((1u << w) - 1u));
-                        if (k >= c) { k -= c; t += w; }
-                    }
-                    int r = 0;
-#pragma unroll
-                    for (int rr = 0; rr < QG_TOP; rr++) r = P.ids[t * QG_TOP + rr] == e ? rr : r;
-                    q = t * QG_TOP + r;
-                }
-                if (kx == 0) {
-                    const int k = s_xk[x] + m;
-                    if (slot < n) A.pl->tile[k].q[slot] = q;
-                    if (slot == 0) { A.pl->tile[k].e = e; A.pl->tile[k].n = n; }
+                for (int w = 16; w >= 1; w >>= 1) {
+                    const int c = __popc((msk >> t) & ((1u << w) - 1u));
+                    if (k >= c) { k -= c; t += w; }
                 }
             }
-            if (slot < n) s_tq[m][slot] = q;
+            if (slot < n) s_tt[m][slot] = t;
             if (slot == 0) s_tn[m] = n;
         }
     }
-    __syncthreads();  // the plan scratch is read; the reduction area may be reused
-    if (rb1 <= rb0) return;  // block-uniform
-    if (M == 1) gu3_run<1>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
-    else if (M == 2) gu3_run<2>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
-    else gu3_run<3>(A, e, rb0, rb1, s_tn, s_tq, s_dyn, tid);
+    __syncthreads();
+    if (rb1 <= rb0) {  // block-uniform: no blocks here; the first workgroup still publishes
+        if (wave == 0 && k0 >= 0) gu3_selections(A, e, M, s_tn, s_tt, s_tq, k0, lane);
+        return;
+    }
+    if (M == 1) gu3_run<1>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
+    else if (M == 2) gu3_run<2>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
+    else gu3_run<3>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
 }
 
 // Shared-memory layout of the gate/up kernel (fp16 units): 16 staged plane
@@ -1477,7 +1502,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr;
     const int row_blocks = RT_ROWBLOCKS * ngr;
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_blocks,
-                 L->router_bias};
+                 L->router_bias, nt > INLINE_MAX ? pl->emask : nullptr};
     const dim3 rgrid(row_blocks + (nt + 3) / 4), rblock(256);
     const size_t rlds = (size_t)TPB * D * 4;
     if (D == 2048) router_launch<2048>(TPB, rgrid, rblock, rlds, s, R);
@@ -1510,7 +1535,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
         // workgroup per CU, each on one expert's run of F blocks
         // (one token: the per-tile kernel with its finer split, 512 workgroups)
         if (inl) dec_launch(2, dec_gateup2_kernel<true>, dim3(nwg2), dim3(256), GU2_LDS, s, G2);
-        else dec_launch(2, dec_gateup3_kernel<false>, dim3(qg_cu_count()), dim3(64 * GU3_W), GU3_LDS, s, G2);
+        else dec_launch(2, dec_gateup3_kernel, dim3(qg_cu_count()), dim3(64 * GU3_W), GU3_LDS, s, G2);
     } else {
         // D = 2560 (dec_ok): the register-weight kernel, 10 superblocks per row
         const size_t gu_bytes = (size_t)gu_lds(D).total * 2;
