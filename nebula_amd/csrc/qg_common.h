@@ -214,42 +214,57 @@ QG_DEV void qg_route_lane(const float *s, int lane, int &id_out, float &w_out) {
 }
 
 // The same routing as qg_route_lane, faster: a threshold T that every top-10
-// logit reaches (the 10th largest of the 64 lane maxima, counting equal
-// values separately: at least 10 logits reach it, so the 10th largest logit
-// does), then an exact rank by (value desc, index asc) among the candidates
-// >= T, which is the order of the reference's repeated strict-greater argmax.
-// The numerators exp(s - max) are computed in parallel (lane k: rank k) and
-// summed in rank order.  lds_v/lds_i: 64 floats / 64 ints of wave-private
-// shared memory.  More than 64 candidates (heavy ties) falls back to
-// qg_route_lane.
-QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i) {
-    float v[8];
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; i++) { v[i] = s[lane + 64 * i]; bad |= !__builtin_isfinite(v[i]); }
+// logit reaches, then an exact rank by (value desc, index asc) among the
+// candidates >= T, which is the order of the reference's repeated
+// strict-greater argmax.  T: each 16-lane row's three largest distinct lane
+// maxima are 12 values held by 12 different lanes; the third smallest of
+// them has at least 10 of the 12 lanes at or above it, so at least 10 logits
+// reach it and the 10th largest logit does.  (Typically 10-14 candidates; a
+// row with fewer than three distinct lane maxima gives -inf, every logit a
+// candidate, and the fallback.)  The numerators exp(s - max) are computed in
+// parallel (lane k: rank k) and summed in rank order; with weights false they
+// are skipped (w_out 0).  lds_v/lds_i: QG_ROUTE_SCRATCH (128) floats / ints
+// of wave-private shared memory (entries 64 + lane take the lane's
+// non-candidates, so the compaction has no branches).  More than 64
+// candidates (heavy ties) falls back to qg_route_lane.  qg_route_vals takes
+// the lane's 8 logits s[lane + 64 i] already loaded (s itself is read again
+// only by that fallback).
+constexpr int QG_ROUTE_SCRATCH = 128;  // entries of each routing scratch array
+QG_DEV void qg_route_vals(const float (&v)[8], const float *s, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i,
+                          bool weights = true) {
+    auto rl = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
     id_out = -1;
     w_out = 0.0f;
-    if (__any(bad)) return;
+    bool bad = false;
     float lm = v[0];
 #pragma unroll
-    for (int i = 1; i < 8; i++) lm = fmaxf(lm, v[i]);
-    // threshold: walk down the distinct lane maxima until 10 lanes are covered
-    float largest = 0.0f, T = 0.0f, cur = lm;
-    int remaining = QG_TOP;
-    for (int r = 0; r < QG_TOP; r++) {
-        const float m = qg_wave_max(cur);
-        if (r == 0) largest = m;
-        const int cnt = __popcll(__ballot(cur == m));
-        T = m;
-        if (cnt >= remaining) break;
-        remaining -= cnt;
-        cur = cur == m ? -__builtin_inff() : cur;
+    for (int i = 0; i < 8; i++) { bad |= !__builtin_isfinite(v[i]); lm = fmaxf(lm, v[i]); }
+    if (__any(bad)) return;
+    // the rows' three largest distinct lane maxima (-inf where a row has fewer)
+    float cur = lm;
+    const float r1 = qg_row_max(cur);
+    cur = cur == r1 ? -__builtin_inff() : cur;
+    const float r2 = qg_row_max(cur);
+    cur = cur == r2 ? -__builtin_inff() : cur;
+    const float r3 = qg_row_max(cur);
+    float a[12];
+#pragma unroll
+    for (int rw = 0; rw < 4; rw++) { a[3 * rw] = rl(r1, 16 * rw); a[3 * rw + 1] = rl(r2, 16 * rw); a[3 * rw + 2] = rl(r3, 16 * rw); }
+    const float largest = fmaxf(fmaxf(a[0], a[3]), fmaxf(a[6], a[9]));
+    // T = the third smallest of the 12 (the three smallest kept in order)
+    float m0 = a[0], m1 = __builtin_inff(), m2 = __builtin_inff();
+#pragma unroll
+    for (int i = 1; i < 12; i++) {
+        m2 = fminf(m2, fmaxf(m1, a[i]));
+        m1 = fminf(m1, fmaxf(m0, a[i]));
+        m0 = fminf(m0, a[i]);
     }
-    // candidates v >= T, compacted in lane order
+    const float T = m2;
+    // candidates v >= T, compacted in lane order: exclusive prefix sum of the
+    // lane's count (0..8) from bit-sliced ballots
     int c = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) c += v[i] >= T;
-    // exclusive prefix sum of c (0..8) over the lanes from bit-sliced ballots
     int pos = 0, total_c = 0;
 #pragma unroll
     for (int bit = 0; bit < 4; bit++) {
@@ -259,8 +274,13 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     }
     if (total_c > 64) { qg_route_lane(s, lane, id_out, w_out); return; }
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-        if (v[i] >= T) { lds_v[pos] = v[i]; lds_i[pos] = lane + 64 * i; pos++; }
+    for (int i = 0; i < 8; i++) {
+        const bool cand = v[i] >= T;
+        const int at = cand ? pos : 64 + lane;
+        lds_v[at] = v[i];
+        lds_i[at] = lane + 64 * i;
+        pos += cand;
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -269,7 +289,7 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     const int ci = lane < total_c ? lds_i[lane] : 0;
     int rank = 0;
     for (int q = 0; q < total_c; q++) {  // candidate q from its lane's registers (wave-uniform q)
-        const float ov = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), q));
+        const float ov = rl(cv, q);
         const int oi = __builtin_amdgcn_readlane(ci, q);
         rank += (ov > cv) | ((ov == cv) & (oi < ci));
     }
@@ -280,11 +300,19 @@ QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, f
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < QG_TOP) id_out = lds_i[lane];
+    if (!weights) return;  // wave-uniform
     const float num = lane < QG_TOP ? qg_expf(lds_v[lane] - largest) : 0.0f;
     float total = 0.0f;
 #pragma unroll
-    for (int k = 0; k < QG_TOP; k++) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), k));
-    if (lane < QG_TOP) { id_out = lds_i[lane]; w_out = num / total; }
+    for (int k = 0; k < QG_TOP; k++) total += rl(num, k);
+    if (lane < QG_TOP) w_out = num / total;
+}
+QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i, bool weights = true) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = s[lane + 64 * i];
+    qg_route_vals(v, s, lane, id_out, w_out, lds_v, lds_i, weights);
 }
 
 // Two tokens per wave, one per 32-lane half h: the routing of qg_route_fast
@@ -439,9 +467,11 @@ QG_DEV int qg_route_cover(int &id, float &wv, const uint8_t *resident, double th
     const bool bad = __ballot(mine && !valid) != 0;
     missing = __popcll(nb);
     mass = 0.0;
+    if (nb) {  // wave-uniform
 #pragma unroll
-    for (int k = 0; k < QG_TOP; k++)
-        if ((nb >> k) & 1) mass += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), k));
+        for (int k = 0; k < QG_TOP; k++)
+            if ((nb >> k) & 1) mass += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), k));
+    }
     const int flag = bad ? 3 : !missing ? 0 : (thr > 0 && mass < thr) ? 1 : 2;
     if (flag == 1 && nonres) { id = -id - 2; wv = 0.0f; }
     return flag;

@@ -230,8 +230,8 @@ struct RouteArgs {
 // tokens run on separate CUs.  The expert plan is built from these results by
 // every gate/up workgroup (dec_gateup_kernel).
 __global__ __launch_bounds__(64) void dec_route_kernel(RouteArgs A) {
-    __shared__ float s_rv[64];
-    __shared__ int s_ri[64];
+    __shared__ __align__(16) float s_rv[QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_ri[QG_ROUTE_SCRATCH];
     const int t = blockIdx.x, lane = threadIdx.x;
     int id, missing;
     float wv;
@@ -291,7 +291,7 @@ QG_DEV void gu_route_inline(const GuArgs &A, int lane, float *s_rv, int *s_ri, i
     int id, missing;
     float wv;
     double mass;
-    qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri);
+    qg_route_fast(A.logits, lane, id, wv, s_rv, s_ri, blockIdx.x == 0 || A.resident != nullptr);
     const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
     const bool el = lane < QG_TOP && flag < 2 && id >= 0 && id < QG_EXPERTS;
     const unsigned long long b = __ballot(el);
@@ -422,8 +422,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
     __shared__ int s_te[GU2_NT][2];          // per tile of the range: expert, token count
     __shared__ int s_tl[GU2_NT][TILE_TOK];   // and its selections
-    __shared__ float s_rv[64];
-    __shared__ int s_ri[64];
+    __shared__ __align__(16) float s_rv[QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_ri[QG_ROUTE_SCRATCH];
     __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
     __shared__ int s_nent;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
@@ -895,8 +895,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup_kernel(GuArgs A) {
     __shared__ int s_item[GU_NI][2];     // per item: expert (-1: shared), token count (-1: past the plan)
     __shared__ int s_list[GU_NI][TILE_TOK];  // per item: its selections (shared expert: MS + t)
     __shared__ int s_nitems;
-    __shared__ float s_rv[64];
-    __shared__ int s_ri[64];
+    __shared__ __align__(16) float s_rv[QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_ri[QG_ROUTE_SCRATCH];
     __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
     __shared__ int s_nent;
     __shared__ uint4 s_zero[NSB];

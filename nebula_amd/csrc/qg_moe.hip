@@ -151,8 +151,8 @@ __global__ __launch_bounds__(RD_THREADS) void route_dispatch_kernel(int *ids_out
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (xh)  // fp16 hi/lo planes of the inputs for the matrix-core expert kernels
         for (int i = tid; i < nt * (D / 32); i += RD_THREADS) act_planes_group(x, D, i / (D / 32), i % (D / 32), xh, xs);
-    __shared__ float s_rv[RD_THREADS / 64][64];
-    __shared__ int s_ri[RD_THREADS / 64][64];
+    __shared__ __align__(16) float s_rv[RD_THREADS / 64][QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_ri[RD_THREADS / 64][QG_ROUTE_SCRATCH];
     for (int t = wave; t < nt; t += RD_THREADS / 64) route_token(s_ids, s_w, logits + (size_t)t * ld, t, lane, s_rv[wave], s_ri[wave]);
     __syncthreads();
     // Coverage (gpu.cu:470-478): mass of non-resident selections in rank order.

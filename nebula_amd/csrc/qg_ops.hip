@@ -339,8 +339,8 @@ __global__ void binary_kernel(float *o, const float *a, const float *b, int n, i
 // numerators exp(s - max) summed in rank order, then divided by the sum.
 // ------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void route_kernel(int *ids, float *weights, const float *logits, int nt, int ld) {
-    __shared__ float s_v[64];
-    __shared__ int s_i[64];
+    __shared__ __align__(16) float s_v[QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_i[QG_ROUTE_SCRATCH];
     const int ta = 2 * blockIdx.x, tb = min(ta + 1, nt - 1);
     qg_route_wave2(ids, weights, logits, ld, ta, tb, threadIdx.x, s_v, s_i);
 }

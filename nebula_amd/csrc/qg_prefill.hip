@@ -262,8 +262,8 @@ QG_DEV void token_planes_i8(const float *xr, int D, int lane, int8_t *hi, int8_t
 // (top-10 of the (biased) logits, coverage/prune, flags) while wave w + 4
 // writes its fp16 hi/lo planes and 32-group sum planes.
 __global__ __launch_bounds__(512) void pf_route_kernel(RouteArgs A) {
-    __shared__ float s_rv[4][64];
-    __shared__ int s_ri[4][64];
+    __shared__ __align__(16) float s_rv[4][QG_ROUTE_SCRATCH];
+    __shared__ __align__(16) int s_ri[4][QG_ROUTE_SCRATCH];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = blockIdx.x * 4 + (wave & 3);
     if (t >= A.nt) return;  // whole wave; no block barrier in this kernel
     if (wave >= 4) {  // the token's activation planes, beside its routing
