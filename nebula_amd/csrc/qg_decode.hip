@@ -129,30 +129,30 @@ QG_DEV float exact_row_dot(const float *w, const float *x, bool norm, float sc, 
     return qg_tree32(acc);
 }
 
-// Router: grid (64 x token groups of up to 5 + ceil(nt/4) plane blocks), 4
-// waves per block.  Router block b covers expert rows 8(b % 64) .. +7 and the
-// token group b / 64 (TPB tokens), so the blocks sharing a row block sit on
-// one XCD and share its router rows through that L2.  Wave w owns rows
-// 8(b % 64) + 2w + h (32-lane half h), read into registers; the group's token
+// Router: grid (R x token groups of up to 5 + ceil(nt/RW) plane blocks), RW
+// waves per block (4; 1 at one token), R = 512 / (2 RW) row blocks.  Router
+// block b covers expert rows 2RW(b % R) .. +2RW-1 and the token group b / R
+// (TPB tokens), so the blocks sharing a row block sit on one XCD and share its
+// router rows through that L2.  Wave w owns rows 2RW(b % R) + 2w + h (32-lane
+// half h), read into registers; the group's token
 // rows are staged in shared memory by direct global->shared copies, each
 // block starting at its own offset so the CUs do not read the same L2 lines
 // at once.  Lane j accumulates columns k = j (mod 32) in ascending k with fma,
 // then the 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal the
-// reference's qc_matmul bit for bit.  Blocks above 64 x groups: one token per
+// reference's qc_matmul bit for bit.  Blocks above R x groups: one token per
 // wave: the shared-expert gate logit (same order), and the (optionally
 // normalised) row as fp16 hi/lo planes in the Q4_K fragment order plus hi/lo
 // planes of the sums of each 32-group.
-constexpr int RT_ROWBLOCKS = QG_EXPERTS / 8;
-template <int TPB, int DW>
+template <int TPB, int DW, int RW>
 __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
-    constexpr int KS = DW / 32;
+    constexpr int KS = DW / 32, RBLK = QG_EXPERTS / (2 * RW);  // row blocks of 2 RW rows
     extern __shared__ float s_rt[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
     const int nt = A.nt;
     if (blockIdx.x >= A.row_blocks) {
         if (A.emask && blockIdx.x == A.row_blocks)
-            for (int i = threadIdx.x; i < QG_EXPERTS; i += 256) A.emask[i] = 0u;  // the routing kernel sets them
-        const int t = (blockIdx.x - A.row_blocks) * 4 + wave;
+            for (int i = threadIdx.x; i < QG_EXPERTS; i += 64 * RW) A.emask[i] = 0u;  // the routing kernel sets them
+        const int t = (blockIdx.x - A.row_blocks) * RW + wave;
         if (t >= nt) return;  // whole wave; the plane blocks have no block barrier
         const float *xr = A.x + (size_t)t * DW;
         const float sc = A.norm ? row_rms_scale(xr, DW, A.eps, lane) : 1.0f;
@@ -164,14 +164,14 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
         token_planes(xr, DW, A.norm != 0, sc, lane, hi, hi + DW, shi, shi + DW / 32, A.xn ? A.xn + (size_t)t * DW : nullptr);
         return;
     }
-    const int rb = blockIdx.x % RT_ROWBLOCKS, t0 = (blockIdx.x / RT_ROWBLOCKS) * TPB;
+    const int rb = blockIdx.x % RBLK, t0 = (blockIdx.x / RBLK) * TPB;
     const int ntg = min(TPB, nt - t0);  // tokens of this group (>= 1)
-    const int row = rb * 8 + 2 * wave + half;
+    const int row = rb * 2 * RW + 2 * wave + half;
     const float *wr = A.router + (size_t)row * DW;
     // the group's token rows, 1 KB per copy, rotated start
     constexpr int CPT = DW / 256;
     const int ncp = ntg * CPT, rot = (int)((blockIdx.x * 37u) % (unsigned)ncp);
-    for (int q = wave; q < ncp; q += 4) {
+    for (int q = wave; q < ncp; q += RW) {
         int c = q + rot;
         if (c >= ncp) c -= ncp;
         dma16(A.x + (size_t)t0 * DW + c * 256 + lane * 4, s_rt + c * 256);
@@ -773,8 +773,8 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
             // tiles per expert (1..3 for up to 17 tokens) as bit-sliced ballots
             const int mx = em[i] ? (__popc(em[i]) + TILE_TOK - 1) / TILE_TOK : 0;
             const unsigned long long b = __ballot(em[i] != 0u), b0 = __ballot(mx & 1), b1 = __ballot(mx & 2);
-            if (em[i]) {
-                const int x = nx + __popcll(b & below);
+            const int x = nx + __popcll(b & below);
+            if (em[i] && x < GU3_MAXX) {
                 s_xe[x] = 64 * i + lane;
                 s_xm[x] = mx;
                 s_xk[x] = ntl + __popcll(b0 & below) + 2 * __popcll(b1 & below);
@@ -783,6 +783,10 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
             nx += __popcll(b);
             ntl += __popcll(b0) + 2 * __popcll(b1);
         }
+        // at most one tile per eligible selection when the masks are this
+        // layer's; anything larger (masks not cleared) computes nothing
+        // rather than overrun the plan
+        if (nx > GU3_MAXX || ntl > MAX_TILES) nx = ntl = 0;
         if (blockIdx.x == 0 && lane == 0) A.pl->n_tiles = ntl;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -1479,11 +1483,11 @@ void launch_down(const DnArgs &DA, int fr, int fs, dim3 grid, size_t lds, hipStr
 template <int DW>
 void router_launch(int TPB, dim3 grid, dim3 block, size_t lds, hipStream_t s, const RouterArgs &R) {
     switch (TPB) {
-    case 1: dec_launch(0, dec_router_kernel<1, DW>, grid, block, lds, s, R); break;
-    case 2: dec_launch(0, dec_router_kernel<2, DW>, grid, block, lds, s, R); break;
-    case 3: dec_launch(0, dec_router_kernel<3, DW>, grid, block, lds, s, R); break;
-    case 4: dec_launch(0, dec_router_kernel<4, DW>, grid, block, lds, s, R); break;
-    default: dec_launch(0, dec_router_kernel<5, DW>, grid, block, lds, s, R); break;
+    case 1: dec_launch(0, dec_router_kernel<1, DW, 1>, grid, block, lds, s, R); break;
+    case 2: dec_launch(0, dec_router_kernel<2, DW, 4>, grid, block, lds, s, R); break;
+    case 3: dec_launch(0, dec_router_kernel<3, DW, 4>, grid, block, lds, s, R); break;
+    case 4: dec_launch(0, dec_router_kernel<4, DW, 4>, grid, block, lds, s, R); break;
+    default: dec_launch(0, dec_router_kernel<5, DW, 4>, grid, block, lds, s, R); break;
     }
 }
 
@@ -1498,12 +1502,14 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     _Float16 *xp = (_Float16 *)(ws + lay.xp);
     _Float16 *xsp = (_Float16 *)(ws + lay.xsum);
     const int rows = QG_EXPERTS + (sh ? 1 : 0);
-    // token groups of up to 5: 64 row blocks each
-    const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr;
-    const int row_blocks = RT_ROWBLOCKS * ngr;
+    // token groups of up to 5: 64 row blocks of 4 waves each (128 blocks of 2
+    // waves: 6.3 -> 6.7 us at 17 tokens); one token: 256 one-wave row blocks
+    // (fewer rows per CU, so more of the router's 4 MB in flight at once)
+    const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr, RW = TPB == 1 ? 1 : 4;
+    const int row_blocks = QG_EXPERTS / (2 * RW) * ngr;
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_blocks,
                  L->router_bias, nt > INLINE_MAX ? pl->emask : nullptr};
-    const dim3 rgrid(row_blocks + (nt + 3) / 4), rblock(256);
+    const dim3 rgrid(row_blocks + (nt + RW - 1) / RW), rblock(64 * RW);
     const size_t rlds = (size_t)TPB * D * 4;
     if (D == 2048) router_launch<2048>(TPB, rgrid, rblock, rlds, s, R);
     else router_launch<2560>(TPB, rgrid, rblock, rlds, s, R);

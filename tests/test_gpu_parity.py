@@ -376,9 +376,9 @@ def layer1(qgl):
     return L, H
 
 
-def _check_layer(L, H, x, what, resident=None):
+def _check_layer(L, H, x, what, resident=None, fw=None):
     nt = x.shape[0]
-    fw = synth.Forward(2048, 512, nt)
+    fw = fw if fw is not None else synth.Forward(2048, 512, nt)
     fw.x.set(np.concatenate([x, np.zeros((fw.tokens - nt, 2048), np.float32)]) if nt < fw.tokens else x)
     say(f"forward {what} nt={nt}")
     fw.run(L, nt)
@@ -406,6 +406,17 @@ def test_layer_config0_batch1(layer0):
 def test_layer_config1_verify_batches(layer1, nt):
     L, H = layer1
     _check_layer(L, H, synth.inputs(50 + nt, nt, 2048, correlated=True), f"config1 B={nt}")
+
+
+def test_layer_workspace_reused_across_calls(layer1):
+    """One workspace through consecutive verify batches of different sizes:
+    every call's routing and output match the oracle, so nothing of an
+    earlier call's plan (the per-expert token masks among it) leaks into the
+    next one."""
+    L, H = layer1
+    fw = synth.Forward(2048, 512, 17)
+    for i, nt in enumerate((17, 8, 17, 4, 17, 2, 17)):
+        _check_layer(L, H, synth.inputs(70 + i, nt, 2048, correlated=(i % 2 == 0)), f"reused workspace call {i} B={nt}", fw=fw)
 
 
 def test_layer_config0_multitoken_no_shared(layer0):
