@@ -1154,6 +1154,19 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     float *mbuf = (float *)(abuf + 16 * F * 2);
     const int cpr = F / 8;  // 16-byte chunks per staged plane row
     const int sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    // wave 0 holds the plan entry of the workgroup's next item in registers,
+    // loaded while the current item streams (routed tiles only)
+    int p_ntl = 0, p_e = -1, p_n = 0, p_q = 0;
+    auto fetch = [&](int item) {
+        const int k = item / dblocks - sh_tiles;
+        if (wave == 0 && k >= 0 && k < MAX_TILES) {
+            p_ntl = A.pl->n_tiles;
+            p_e = A.pl->tile[k].e;
+            p_n = A.pl->tile[k].n;
+            p_q = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
+        }
+    };
+    fetch(blockIdx.x);
     for (int item = blockIdx.x;; item += gridDim.x) {
         const int T = item / dblocks, d0 = (item - T * dblocks) * DN_ROWS;
         if (wave == 0) {
@@ -1162,18 +1175,16 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
                 n = min(TILE_TOK, A.nt - TILE_TOK * T);
                 if (lane < n) s_list[lane] = MS + TILE_TOK * T + lane;
             } else if (T - sh_tiles < MAX_TILES) {
-                const int k = T - sh_tiles;
-                const int ntl = A.pl->n_tiles, ek = A.pl->tile[k].e, nk = A.pl->tile[k].n;
-                const int qk = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
-                if (k < ntl) {
-                    e = ek;
-                    n = nk;
-                    if (lane < nk) s_list[lane] = qk;
+                if (T - sh_tiles < p_ntl) {
+                    e = p_e;
+                    n = p_n;
+                    if (lane < p_n) s_list[lane] = p_q;
                 }
             }
             if (lane == 0) { s_e = e; s_n = n; }
         }
         __syncthreads();
+        fetch(item + gridDim.x);
         const int e = s_e, n = s_n;
         if (n < 0) break;  // block-uniform; every later item is past the plan too
         const bool shared = e < 0;
