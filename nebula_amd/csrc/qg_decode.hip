@@ -1326,15 +1326,16 @@ struct Dn1Args {
     float *out, *resid;
     qg_prune_stats *stats;
 };
-constexpr int DN1_ROWS = 16;             // output rows per workgroup
-constexpr int DN1_SL = DN1_ROWS * 288 / 16;  // 16-byte slots of 16 rows of 288 bytes
+constexpr int DN1_ROWS = 8;              // output rows per workgroup (MFMA columns 8..15 repeat 0..7)
+constexpr int DN1_SL = DN1_ROWS * 288 / 16;  // 16-byte slots of the rows (288 bytes each)
 constexpr int DN1_W = 16;                // waves per workgroup
 constexpr int DN1_EPW = 1;               // entries per wave (10 routed + 1 shared, each on its own wave)
 // weight rows per wave and entry, then every entry's mid planes (F = 512) and 8-row sums
 constexpr size_t DN1_LDS = (size_t)DN1_W * DN1_EPW * DN1_SL * 16 + (size_t)(QG_TOP + 1) * 2 * 512 * 2 + (size_t)(QG_TOP + 1) * 64 * 4;
 
 // One token (the plan's entries k = eligible ranks in order, then the shared
-// expert): workgroup b owns output rows 16b .. 16b + 15; wave w (of 16)
+// expert): workgroup b owns output rows 8b .. 8b + 7 (256 workgroups at
+// D = 2048, one per CU); wave w (of 16)
 // computes entry k = w (its 16 weight rows, the entries' mid planes
 // and 8-row sums all copied into shared memory by direct global->shared
 // copies at once), each weighted by its routing weight; wave 0 then sums them in
@@ -1398,7 +1399,7 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
                     xg[g] = (m4.x + m4.y) + (m4.z + m4.w);
                 }
             }
-            const uint8_t *wb = (const uint8_t *)(wl + (size_t)x * DN1_SL) + (size_t)j * 288;
+            const uint8_t *wb = (const uint8_t *)(wl + (size_t)x * DN1_SL) + (size_t)(j % DN1_ROWS) * 288;
             qg_f4 y = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
             if (q4k) {
 #pragma unroll
@@ -1443,7 +1444,7 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
             }
             // lanes kq = 0 hold rows 0 (hi) and 1 (lo) of weight row j
             const float v = y[0] + y[1];
-            if (kq == 0) s_v[k][j] = shared ? v : v * A.w[q];
+            if (kq == 0 && j < DN1_ROWS) s_v[k][j] = shared ? v : v * A.w[q];
         }
     }
     __syncthreads();
