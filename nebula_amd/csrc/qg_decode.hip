@@ -1144,6 +1144,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
     __shared__ int s_e, s_n;
     __shared__ int s_list[MB];
+    __shared__ float s_wt[TILE_TOK];  // the tile's routing weights (1 for the shared expert)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     constexpr int F = FF;  // the layer's F (512 or 640): a constant, so the staging splits need no division
     const int sh = A.sh_down != nullptr ? 1 : 0;
@@ -1169,6 +1170,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     fetch(blockIdx.x);
     for (int item = blockIdx.x;; item += gridDim.x) {
         const int T = item / dblocks, d0 = (item - T * dblocks) * DN_ROWS;
+        float wq = 1.0f;  // wave 0: the routing weight of tile slot `lane`, loaded behind the copies
         if (wave == 0) {
             int e = -1, n = -1;
             if (T < sh_tiles) {
@@ -1178,7 +1180,10 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
                 if (T - sh_tiles < p_ntl) {
                     e = p_e;
                     n = p_n;
-                    if (lane < p_n) s_list[lane] = p_q;
+                    if (lane < p_n) {
+                        s_list[lane] = p_q;
+                        wq = A.w[p_q];
+                    }
                 }
             }
             if (lane == 0) { s_e = e; s_n = n; }
@@ -1213,6 +1218,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
             }
         }
         wait_vmem();
+        if (wave == 0 && lane < TILE_TOK) s_wt[lane] = wq;
         __syncthreads();
         const uint8_t *wr = wbuf + (size_t)(16 * wave + j) * rb;
         int mrow[2];
@@ -1225,7 +1231,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
             if (idx < n) {
                 const int sl = s_list[idx];
                 const float v = y[2 * t2] + y[2 * t2 + 1];
-                A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * A.w[sl];
+                A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * s_wt[idx];
             }
         }
         __syncthreads();  // s_list, s_e, s_n, the slab and the stage are rewritten by the next item
