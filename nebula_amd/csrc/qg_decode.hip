@@ -585,7 +585,7 @@ constexpr size_t GU3_RING_BYTES = (size_t)GU3_W * GU3_RING * GU3_SLOT * 16;
 constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave x gate/up x tile x lane: float2
 constexpr size_t GU3_LDS = GU3_RING_BYTES + GU3_RED_BYTES;
 constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
-constexpr int GU3_COST = 2;                                       // a block's weight cost in units of one tile's compute
+constexpr int GU3_COST = 1;                                       // a block's weight cost in units of one tile's compute
 
 // The block's products for the M tiles: y[cb][m] = the wave's partial sums
 // over its superblock for the 16 gate (cb 0) or up (cb 1) rows, column j,
