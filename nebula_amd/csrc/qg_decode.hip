@@ -567,8 +567,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
 // three tiles of 8 tokens) against a single copy of its weights, so an
 // expert's weight rows are read from HBM once.  The experts' blocks are dealt
 // to the workgroups in proportion to their cost (blocks x (GU3_COST + tiles):
-// a block's time is mostly its weight bytes): workgroup g takes the expert
-// whose cost range holds the midpoint of g's equal share.
+// a block's copies, then its products and epilogue once per tile): workgroup
+// g takes the expert whose cost range holds the midpoint of g's equal share.
 // Wave w (of 8, two per SIMD) multiplies superblock w (the K split) of the
 // block's 16 gate and 16 up rows; their bytes come by direct global->shared
 // copies into the wave's own ring of GU3_RING buffers, issued GU3_RING - 1
@@ -585,7 +585,7 @@ constexpr size_t GU3_RING_BYTES = (size_t)GU3_W * GU3_RING * GU3_SLOT * 16;
 constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave x gate/up x tile x lane: float2
 constexpr size_t GU3_LDS = GU3_RING_BYTES + GU3_RED_BYTES;
 constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
-constexpr int GU3_COST = 1;                                       // a block's weight cost in units of one tile's compute
+constexpr int GU3_COST = 1;                                       // a block's copy cost in units of one tile's compute (measured best of 0..8)
 
 // The block's products for the M tiles: y[cb][m] = the wave's partial sums
 // over its superblock for the 16 gate (cb 0) or up (cb 1) rows, column j,
@@ -791,9 +791,9 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // cost prefix, RBK (GU3_COST + M) per expert: a block's time is set by
-        // its weight bytes (the same for every tile count) plus a little
-        // compute per tile; tile counts (1..3) summed by bit-sliced ballots
+        // cost prefix, RBK (GU3_COST + M) per expert: a block's copies (the
+        // same for every tile count) plus its products and epilogue per tile;
+        // tile counts (1..3) summed by bit-sliced ballots
         int carry = 0;
         for (int c0 = 0; c0 < nx; c0 += 64) {
             const int x = c0 + lane, mx = x < nx ? s_xm[x] : 0;
