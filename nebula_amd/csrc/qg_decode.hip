@@ -583,8 +583,9 @@ constexpr int GU3_CPB = (GU3_SLOT + 63) / 64;                     // copies per 
 constexpr int GU3_MAXT = 3;                                       // tiles of 8 tokens per expert (17 tokens)
 constexpr size_t GU3_RING_BYTES = (size_t)GU3_W * GU3_RING * GU3_SLOT * 16;
 constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave x gate/up x tile x lane: float2
-constexpr size_t GU3_LDS = GU3_RING_BYTES + GU3_RED_BYTES;
+constexpr size_t GU3_LDS = GU3_RING_BYTES + 2 * GU3_RED_BYTES;          // rings, two partial-sum buffers
 constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
+static_assert((size_t)(5 * GU3_MAXX + 1) * 4 <= GU3_RED_BYTES, "the expert list fits a partial-sum buffer");
 constexpr int GU3_COST = 1;                                       // a block's copy cost in units of one tile's compute (measured best of 0..8)
 
 // The block's products for the M tiles: y[cb][m] = the wave's partial sums
@@ -686,7 +687,7 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
     const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
     const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
     uint4 *ring = s_dyn + (size_t)wave * GU3_RING * GU3_SLOT;
-    float2 *red = (float2 *)(s_dyn + GU3_RING_BYTES / 16);
+    float2 *red0 = (float2 *)(s_dyn + GU3_RING_BYTES / 16);
     // the tiles' activation fragments for this wave's superblock: plane row
     // r = (token r/2, plane r%2), rows past a tile's tokens repeating its last
     qg_half8 af[GU3_MAXT][8], sf[GU3_MAXT];
@@ -711,6 +712,10 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
         else wait_vmem();
         float2 y[2][GU3_MAXT];
         gu3_products<M>(ring + (size_t)(it % GU3_RING) * GU3_SLOT, af, sf, j, kq, y);
+        // partial sums alternate between two buffers: block it + 2 rewrites
+        // this one only after every wave has passed block it + 1's barrier,
+        // so this block's epilogue needs no barrier of its own
+        float2 *red = red0 + (size_t)(it & 1) * (GU3_RED_BYTES / 8);
 #pragma unroll
         for (int cb = 0; cb < 2; cb++)
 #pragma unroll
@@ -742,7 +747,6 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
                 if ((j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
             }
         }
-        __syncthreads();  // the reduction area is free
     }
 }
 
@@ -753,8 +757,11 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
 // published by each expert's first workgroup for the down kernel.
 __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     extern __shared__ uint4 s_dyn[];
-    __shared__ int s_xe[GU3_MAXX], s_xk[GU3_MAXX], s_xm[GU3_MAXX], s_cum[GU3_MAXX + 1];
-    __shared__ uint32_t s_xt[GU3_MAXX];
+    // the expert list, in the second partial-sum buffer (first written after
+    // the barrier that ends the list's use)
+    int *s_xe = (int *)(s_dyn + (GU3_RING_BYTES + GU3_RED_BYTES) / 16), *s_xk = s_xe + GU3_MAXX, *s_xm = s_xk + GU3_MAXX;
+    int *s_cum = s_xm + GU3_MAXX;
+    uint32_t *s_xt = (uint32_t *)(s_cum + GU3_MAXX + 1);
     __shared__ int s_nx;
     __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tt[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
