@@ -1149,9 +1149,8 @@ QG_DEV qg_f4 dn_tile(const uint8_t *wr, const uint8_t *ast, int F, int j, int kq
 template <int FMT, int SFMT, int FF>
 __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     extern __shared__ uint4 s_dyn[];
-    __shared__ int s_e, s_n;
-    __shared__ int s_list[MB];
-    __shared__ float s_wt[TILE_TOK];  // the tile's routing weights (1 for the shared expert)
+    __shared__ int s_list[TILE_TOK];   // the tile's selections
+    __shared__ float s_wt[TILE_TOK];  // and routing weights (1 for the shared expert)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     constexpr int F = FF;  // the layer's F (512 or 640): a constant, so the staging splits need no division
     const int sh = A.sh_down != nullptr ? 1 : 0;
@@ -1162,12 +1161,13 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     float *mbuf = (float *)(abuf + 16 * F * 2);
     const int cpr = F / 8;  // 16-byte chunks per staged plane row
     const int sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
-    // wave 0 holds the plan entry of the workgroup's next item in registers,
-    // loaded while the current item streams (routed tiles only)
+    // every wave holds the plan entry of the workgroup's next item in
+    // registers (lane l: tile slot l % 8), loaded while the current item
+    // streams (routed tiles only), so no barrier precedes an item's copies
     int p_ntl = 0, p_e = -1, p_n = 0, p_q = 0;
     auto fetch = [&](int item) {
         const int k = item / dblocks - sh_tiles;
-        if (wave == 0 && k >= 0 && k < MAX_TILES) {
+        if (k >= 0 && k < MAX_TILES) {
             p_ntl = A.pl->n_tiles;
             p_e = A.pl->tile[k].e;
             p_n = A.pl->tile[k].n;
@@ -1177,28 +1177,25 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     fetch(blockIdx.x);
     for (int item = blockIdx.x;; item += gridDim.x) {
         const int T = item / dblocks, d0 = (item - T * dblocks) * DN_ROWS;
-        float wq = 1.0f;  // wave 0: the routing weight of tile slot `lane`, loaded behind the copies
-        if (wave == 0) {
-            int e = -1, n = -1;
-            if (T < sh_tiles) {
-                n = min(TILE_TOK, A.nt - TILE_TOK * T);
-                if (lane < n) s_list[lane] = MS + TILE_TOK * T + lane;
-            } else if (T - sh_tiles < MAX_TILES) {
-                if (T - sh_tiles < p_ntl) {
-                    e = p_e;
-                    n = p_n;
-                    if (lane < p_n) {
-                        s_list[lane] = p_q;
-                        wq = A.w[p_q];
-                    }
-                }
-            }
-            if (lane == 0) { s_e = e; s_n = n; }
+        // this item's expert e (-1: shared), token count n (-1: past the
+        // plan) and the selection qs of tile slot lane % 8, alike in every wave
+        int e = -1, n = -1, qs = MS;
+        if (T < sh_tiles) {
+            n = min(TILE_TOK, A.nt - TILE_TOK * T);
+            qs = MS + TILE_TOK * T + (lane & (TILE_TOK - 1));
+        } else if (T - sh_tiles < MAX_TILES && T - sh_tiles < p_ntl) {
+            e = p_e;
+            n = p_n;
+            qs = p_q;
         }
-        __syncthreads();
         fetch(item + gridDim.x);
-        const int e = s_e, n = s_n;
         if (n < 0) break;  // block-uniform; every later item is past the plan too
+        float wq = 1.0f;  // wave 0: the routing weight of tile slot `lane`, loaded behind the copies
+        if (wave == 0 && lane < n) {
+            s_list[lane] = qs;
+            if (e >= 0) wq = A.w[qs];
+        }
+        auto sel = [&](int slot) { return __shfl(qs, slot); };  // the selection of tile slot `slot` (all lanes active)
         const bool shared = e < 0;
         const int rb = (int)(shared ? A.sh_rb : A.rb);
         // the item's weight slab: 64 consecutive rows, one flat copy
@@ -1214,14 +1211,16 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
         // past them are not read into any kept result
         for (int q = wave; q * 64 < 2 * n * cpr; q += 4) {
             const int C = q * 64 + lane, r = C / cpr, pos = C - r * cpr;
-            if (r < 2 * n) dma16(A.midp + ((size_t)s_list[r >> 1] * 2 + (r & 1)) * F + (size_t)(pos ^ (r & 15)) * 8, abuf + (size_t)q * 1024);
+            const int sq = sel(min(r, 2 * n - 1) >> 1);
+            if (r < 2 * n) dma16(A.midp + ((size_t)sq * 2 + (r & 1)) * F + (size_t)(pos ^ (r & 15)) * 8, abuf + (size_t)q * 1024);
         }
         if ((shared ? SFMT : FMT) == QT_Q4_K) {
             // the tile tokens' 8-row sums of mid (Q4_K min terms), padded rows
             const int cpm = F / 32;  // 16-byte chunks per row
             for (int q = wave; q * 64 < n * (cpm + 1); q += 4) {
                 const int slot = q * 64 + lane, r = slot / (cpm + 1), c = slot - r * (cpm + 1);
-                if (r < n && c < cpm) dma16(A.msum8 + (size_t)s_list[r] * (F / 8) + c * 4, mbuf + q * 256);
+                const int sq = sel(min(r, n - 1));
+                if (r < n && c < cpm) dma16(A.msum8 + (size_t)sq * (F / 8) + c * 4, mbuf + q * 256);
             }
         }
         wait_vmem();
@@ -1241,7 +1240,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
                 A.slots[(size_t)sl * A.D + d0 + 16 * wave + j] = shared ? v : v * s_wt[idx];
             }
         }
-        __syncthreads();  // s_list, s_e, s_n, the slab and the stage are rewritten by the next item
+        __syncthreads();  // s_list, s_wt, the slab and the stage are rewritten by the next item
     }
 }
 
