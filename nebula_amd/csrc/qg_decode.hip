@@ -3,7 +3,7 @@
 // Q4_K or IQ4_NL down.  It replaces moe()/grouped_moe()/shared_direct() of
 // qwen.c:633-735 for one layer without any host round trip.
 //
-// Kernels per layer (4 for B = 1, 5 above).  No kernel waits on another block
+// Kernels per layer (3 for B = 1, 5 above).  No kernel waits on another block
 // of its own grid: on MI355X a grid-wide ticket costs ~12 ns per block of
 // serialised atomics and a device-scope fence ~17 us per 1000 waves, more than
 // a kernel boundary (~1.7-2.4 us).
@@ -12,10 +12,11 @@
 //                order, so logits, ids and weights are bit-exact.  Extra
 //                blocks write the fp16 hi/lo activation planes and per-32
 //                sums; optionally the input is RMS-normalised first.
-//   KR route   : B > 1 only; one block: a wave per token (top-10,
-//                coverage/prune, flags), then the plan: the experts in order
-//                of their first eligible selection, each cut into tiles of up
-//                to 8 selections in token order.
+//   KR route   : B > 1 only; a block per token (top-10, coverage/prune,
+//                flags), setting the token's bit in each eligible expert's
+//                token mask (cleared by the router's first plane block); the
+//                gate/up workgroups build the plan from the masks (D = 2048)
+//                or from the ids (D = 2560).
 //   K2 gate/up : B > 1 at D = 2048: one workgroup per CU, each on one
 //                expert's run of 16-row F blocks for all of the expert's
 //                tiles, so every weight row is read once (dec_gateup3).
@@ -28,7 +29,8 @@
 //                their 8-row sums.
 //   K3 down    : persistent; item = (tile, 64 output rows): weight slab and
 //                the tile's mid planes staged in shared memory, products on
-//                the matrix cores, weighted results to per-selection slots.
+//                the matrix cores, weighted results to per-selection slots
+//                (B = 1: down and combine in one kernel, dec_down1).
 //   K4 combine : router-rank sum of the 10 slots, the sigmoid-gated shared
 //                expert and the optional residual add.
 //
