@@ -440,7 +440,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     }
     const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     const int ntl = sh_tiles + (INL ? s_nent : *P.ntiles), N = ntl * RBK;
-    const int i0 = (int)((long long)N * blockIdx.x / gridDim.x), i1 = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    // N <= (3 + 170) * F / 16 items and at most 1024 workgroups: 32-bit products suffice
+    const int i0 = (int)((uint32_t)N * blockIdx.x / gridDim.x), i1 = (int)((uint32_t)N * (blockIdx.x + 1) / gridDim.x);
     const int T0 = i0 / RBK;
     if (wave == 0) {
         // the range's tiles (lane l: tile T0 + l / 8, list slot l % 8); the
