@@ -1306,28 +1306,40 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
             *(float4 *)(A.resid + o) = h;
         }
     }
-    if (A.stats && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
-        // counters in token order (deterministic, unlike the reference's
-        // atomics), summed in registers and added once
-        uint64_t tl = 0, ms = 0, ss = 0, av = 0;
-        double mass = A.stats->skipped_mass;
-        for (int u = 0; u < A.nt; u++) {
-            const int f = A.pl->flag[u], mi = A.pl->missing[u];
-            const double mu = A.pl->mass[u];
-            if (f == 3) continue;
-            tl += 1;
-            ms += (uint64_t)mi;
-            if (f == 1) {
-                ss += (uint64_t)mi;
-                av += 1;
-                mass += mu;
-            }
+    if (A.stats && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+        // counters (deterministic, unlike the reference's atomics): lane u
+        // loads token u's record, all in flight at once; counts by ballots,
+        // the skipped mass summed in token order, each added once
+        const int u = threadIdx.x;
+        int f = 3, mi = 0;
+        double mu = 0.0;
+        if (u < A.nt) {
+            f = A.pl->flag[u];
+            mi = A.pl->missing[u];
+            mu = A.pl->mass[u];
         }
-        A.stats->token_layers += tl;
-        A.stats->missing_selections += ms;
-        A.stats->skipped_selections += ss;
-        A.stats->avoided_token_handoffs += av;
-        A.stats->skipped_mass = mass;
+        const bool counted = f != 3, skipped = f == 1;
+        int ms = counted ? mi : 0, ss = skipped ? mi : 0;
+        ms = (int)qg_sum_lanes<64>((float)ms);  // small integers: exact in fp32
+        ss = (int)qg_sum_lanes<64>((float)ss);
+        const uint64_t tl = (uint64_t)__popcll(__ballot(counted)), av = (uint64_t)__popcll(__ballot(skipped));
+        // the skipped mass in token order, by every lane (the readlanes run
+        // with the whole wave active), stored by lane 0
+        const uint64_t bits = (uint64_t)__double_as_longlong(skipped ? mu : 0.0);
+        const int mhi = (int)(bits >> 32), mlo = (int)(uint32_t)bits, sk = skipped ? 1 : 0;
+        double mass = A.stats->skipped_mass;
+        for (int v = 0; v < A.nt; v++) {
+            const double m = __longlong_as_double((long long)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(mhi, v) << 32) |
+                                                              (uint32_t)__builtin_amdgcn_readlane(mlo, v)));
+            if (__builtin_amdgcn_readlane(sk, v)) mass += m;
+        }
+        if (u == 0) {
+            A.stats->token_layers += tl;
+            A.stats->missing_selections += (uint64_t)ms;
+            A.stats->skipped_selections += (uint64_t)ss;
+            A.stats->avoided_token_handoffs += av;
+            A.stats->skipped_mass = mass;
+        }
     }
 }
 
