@@ -486,6 +486,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
         if (ti != cur) {
             // the tile's activation fragments for this wave's superblocks:
             // plane row r = (token r/2, plane r%2)
+            // rows past the tile's tokens are zeros, not loaded
+            const bool real = (j >> 1) < n;
             const int r = 2 * min(j >> 1, n - 1) + (j & 1), sl0 = s_tl[ti][r >> 1];
             const int tok = e < 0 ? sl0 - MS : sl0 / QG_TOP;
             const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 512 + kq * 8;
@@ -493,8 +495,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
 #pragma unroll
             for (int sb = 0; sb < 2; sb++) {
 #pragma unroll
-                for (int m = 0; m < 8; m++) af[sb][m] = ld_frag(xr + sb * 256 + m * 32);
-                sf[sb] = kq ? qg_half8{} : ld_frag(xs + sb * 8);
+                for (int m = 0; m < 8; m++) af[sb][m] = real ? ld_frag(xr + sb * 256 + m * 32) : qg_half8{};
+                sf[sb] = (kq || !real) ? qg_half8{} : ld_frag(xs + sb * 8);
             }
             cur = ti;
         }
@@ -692,16 +694,19 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
     uint4 *ring = s_dyn + (size_t)wave * GU3_RING * GU3_SLOT;
     float2 *red0 = (float2 *)(s_dyn + GU3_RING_BYTES / 16);
     // the tiles' activation fragments for this wave's superblock: plane row
-    // r = (token r/2, plane r%2), rows past a tile's tokens repeating its last
+    // r = (token r/2, plane r%2); rows past a tile's tokens are zeros, not
+    // loaded (their products are never kept), so a one-token tile reads 2 of
+    // the 16 rows
     qg_half8 af[GU3_MAXT][8], sf[GU3_MAXT];
 #pragma unroll
     for (int m = 0; m < M; m++) {
+        const bool real = (j >> 1) < tn[m];
         const int r = 2 * min(j >> 1, tn[m] - 1) + (j & 1), tok = tt[m][r >> 1];
         const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 256 + kq * 8;
         const _Float16 *xs = A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)wave * 8;
 #pragma unroll
-        for (int f = 0; f < 8; f++) af[m][f] = ld_frag(xr + f * 32);
-        sf[m] = kq ? qg_half8{} : ld_frag(xs);
+        for (int f = 0; f < 8; f++) af[m][f] = real ? ld_frag(xr + f * 32) : qg_half8{};
+        sf[m] = (kq || !real) ? qg_half8{} : ld_frag(xs);
     }
     if (wave == 0) gu3_selections(A, e, M, tn, tt, tq, k0, lane);
     auto copy_block = [&](int rb, int s) { gu3_copy(A, gm, um, rb, ring + (size_t)s * GU3_SLOT, wave, lane); };
