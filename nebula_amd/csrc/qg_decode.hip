@@ -273,7 +273,9 @@ constexpr int GU_WROWS = 4 * GU_ROWS; // F rows per workgroup (4 waves)
 
 // Warm this XCD's L2 with the batch's activation and sum planes while the
 // plan is built (workgroups b, b + 8, ... share an XCD; each takes 4 KB); the
-// returned word is consumed once the loads are needed to have landed.
+// returned word is consumed once the loads are needed to have landed.  Used
+// by the D = 2560 kernel; at D = 2048 the warm loads measured slower (they
+// compete with the plan's own reads).
 QG_DEV uint32_t gu_warm(const GuArgs &A, int tid) {
     uint32_t warm = 0;
     const size_t pb = (size_t)A.nt * 2 * A.D * 2, tb = pb + (size_t)A.nt * 2 * (A.D / 32) * 2;
@@ -430,7 +432,6 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     __shared__ int s_nent;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int D = A.D, D32 = D / 32, RBK = A.F / GU2_ROWS;
-    const uint32_t warm = gu_warm(A, tid);
     const GuPlan P = gu_plan_at(s_dyn);
     if (INL) {
         if (wave == 0) gu_route_inline(A, lane, s_rv, s_ri, s_rank, s_rid, &s_nent);
@@ -457,7 +458,6 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
         if (!INL && blockIdx.x == 0 && lane == 0) A.pl->n_tiles = *P.ntiles;
     }
     __syncthreads();
-    asm volatile("" ::"v"(warm));  // the warming loads have landed
     if (i1 <= i0) return;  // block-uniform
     uint4 *wl = s_dyn + (size_t)wave * 2 * GU2_SL;  // this wave's two buffers
     // item -> the wave's copies into buffer b
@@ -774,7 +774,6 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tt[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int RBK = A.F / GU2_ROWS;
-    const uint32_t warm = gu_warm(A, tid);
     const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     if (wave == 0) {
         uint32_t em[QG_EXPERTS / 64];
@@ -821,7 +820,6 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
         if (lane == 0) { s_cum[0] = 0; s_nx = nx; }
     }
     __syncthreads();
-    asm volatile("" ::"v"(warm));  // the warming loads have landed
     const int nx = s_nx;
     if (nx == 0) return;  // block-uniform: nothing computed on the device
     // this workgroup's expert: the one whose cost range holds the midpoint of
