@@ -590,7 +590,7 @@ constexpr size_t GU3_RING_BYTES = (size_t)GU3_W * GU3_RING * GU3_SLOT * 16;
 constexpr size_t GU3_RED_BYTES = (size_t)GU3_W * 2 * GU3_MAXT * 64 * 8;  // wave x gate/up x tile x lane: float2
 constexpr size_t GU3_LDS = GU3_RING_BYTES + 2 * GU3_RED_BYTES;          // rings, two partial-sum buffers
 constexpr int GU3_MAXX = MAX_TILES + 1;                           // experts in the plan, the shared one included
-static_assert((size_t)(5 * GU3_MAXX + 1) * 4 <= GU3_RED_BYTES, "the expert list fits a partial-sum buffer");
+static_assert((size_t)(5 * GU3_MAXX + 1 + MS) * 4 <= GU3_RED_BYTES, "the expert list and ids fit a partial-sum buffer");
 constexpr int GU3_COST = 1;                                       // a block's copy cost in units of one tile's compute (measured best of 0..8)
 
 // The block's products for the M tiles: y[cb][m] = the wave's partial sums
@@ -652,8 +652,8 @@ QG_DEV void gu3_copy(const GuArgs &A, const uint8_t *gm, const uint8_t *um, int 
 // gave expert e, from the routing ids; shared expert: MS + t), by one wave
 // (lane l: tile l / 8, slot l % 8); with k0 >= 0 the tiles are also published
 // as routed tiles k0 .. k0 + M - 1 of the plan for the down kernel.
-QG_DEV void gu3_selections(const GuArgs &A, int e, int M, const int *tn, const int (*tt)[TILE_TOK], int (*tq)[TILE_TOK], int k0,
-                           int lane) {
+QG_DEV void gu3_selections(const GuArgs &A, const int *ids, int e, int M, const int *tn, const int (*tt)[TILE_TOK],
+                           int (*tq)[TILE_TOK], int k0, int lane) {
     const int m = lane >> 3, slot = lane & 7;
     if (m >= M) return;
     const int n = tn[m];
@@ -663,7 +663,7 @@ QG_DEV void gu3_selections(const GuArgs &A, int e, int M, const int *tn, const i
         if (e < 0) {
             q = MS + t;
         } else {
-            const int2 *row = (const int2 *)(A.ids + (size_t)t * QG_TOP);  // 8-byte aligned
+            const int2 *row = (const int2 *)(ids + t * QG_TOP);  // shared memory, 8-byte aligned
             int r = 0;
 #pragma unroll
             for (int i = 0; i < QG_TOP / 2; i++) {
@@ -685,8 +685,8 @@ QG_DEV void gu3_selections(const GuArgs &A, int e, int M, const int *tn, const i
 // counts and tokens, tq: their selections (written by wave 0 here, read after
 // the first block's barrier), all in shared memory.
 template <int M>
-QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, const int (*tt)[TILE_TOK], int (*tq)[TILE_TOK],
-                    int k0, uint4 *s_dyn, int tid) {
+QG_DEV void gu3_run(const GuArgs &A, const int *ids, int e, int rb0, int rb1, const int *tn, const int (*tt)[TILE_TOK],
+                    int (*tq)[TILE_TOK], int k0, uint4 *s_dyn, int tid) {
     const int wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int D = A.D, D32 = D / 32, nb = rb1 - rb0;
     const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
@@ -708,7 +708,7 @@ QG_DEV void gu3_run(const GuArgs &A, int e, int rb0, int rb1, const int *tn, con
         for (int f = 0; f < 8; f++) af[m][f] = real ? ld_frag(xr + f * 32) : qg_half8{};
         sf[m] = (kq || !real) ? qg_half8{} : ld_frag(xs);
     }
-    if (wave == 0) gu3_selections(A, e, M, tn, tt, tq, k0, lane);
+    if (wave == 0) gu3_selections(A, ids, e, M, tn, tt, tq, k0, lane);
     auto copy_block = [&](int rb, int s) { gu3_copy(A, gm, um, rb, ring + (size_t)s * GU3_SLOT, wave, lane); };
     const int fmt = e < 0 ? A.sh_fmt : A.fmt;
     for (int it = 0; it < nb; it++) {
@@ -770,11 +770,13 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     int *s_xe = (int *)(s_dyn + (GU3_RING_BYTES + GU3_RED_BYTES) / 16), *s_xk = s_xe + GU3_MAXX, *s_xm = s_xk + GU3_MAXX;
     int *s_cum = s_xm + GU3_MAXX;
     uint32_t *s_xt = (uint32_t *)(s_cum + GU3_MAXX + 1);
+    int *s_ids = (int *)(s_xt + GU3_MAXX);  // the routing ids, so the selections need no global reads behind the copies
     __shared__ int s_nx;
     __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tt[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int RBK = A.F / GU2_ROWS;
     const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
+    if (tid < A.nt * QG_TOP) s_ids[tid] = A.ids[tid];  // read before any copy is in flight
     if (wave == 0) {
         uint32_t em[QG_EXPERTS / 64];
 #pragma unroll
@@ -873,12 +875,12 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     }
     __syncthreads();
     if (rb1 <= rb0) {  // block-uniform: no blocks here; the first workgroup still publishes
-        if (wave == 0 && k0 >= 0) gu3_selections(A, e, M, s_tn, s_tt, s_tq, k0, lane);
+        if (wave == 0 && k0 >= 0) gu3_selections(A, s_ids, e, M, s_tn, s_tt, s_tq, k0, lane);
         return;
     }
-    if (M == 1) gu3_run<1>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
-    else if (M == 2) gu3_run<2>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
-    else gu3_run<3>(A, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
+    if (M == 1) gu3_run<1>(A, s_ids, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
+    else if (M == 2) gu3_run<2>(A, s_ids, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
+    else gu3_run<3>(A, s_ids, e, rb0, rb1, s_tn, s_tt, s_tq, k0, s_dyn, tid);
 }
 
 // Shared-memory layout of the gate/up kernel (fp16 units): 16 staged plane
