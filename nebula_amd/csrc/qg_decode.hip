@@ -1171,14 +1171,17 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     const int sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     // every wave holds the plan entry of the workgroup's next item in
     // registers (lane l: tile slot l % 8), loaded while the current item
-    // streams (routed tiles only), so no barrier precedes an item's copies
-    int p_ntl = 0, p_e = -1, p_n = 0, p_q = 0;
+    // streams (routed tiles only), so no barrier precedes an item's copies.
+    // The tile's expert and token count sit in lanes 0 and 1 of p_en: a value
+    // that differs across lanes stays in a vector register, so nothing waits
+    // for the load until the next item reads it (a wave-uniform one would be
+    // moved to a scalar register, with a wait, right after the load).
+    int p_ntl = 0, p_en = -1, p_q = 0;
     auto fetch = [&](int item) {
         const int k = item / dblocks - sh_tiles;
         if (k >= 0 && k < MAX_TILES) {
             p_ntl = A.pl->n_tiles;
-            p_e = A.pl->tile[k].e;
-            p_n = A.pl->tile[k].n;
+            p_en = (&A.pl->tile[k].e)[lane & 1];
             p_q = A.pl->tile[k].q[lane & (TILE_TOK - 1)];
         }
     };
@@ -1192,8 +1195,8 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
             n = min(TILE_TOK, A.nt - TILE_TOK * T);
             qs = MS + TILE_TOK * T + (lane & (TILE_TOK - 1));
         } else if (T - sh_tiles < MAX_TILES && T - sh_tiles < p_ntl) {
-            e = p_e;
-            n = p_n;
+            e = __builtin_amdgcn_readlane(p_en, 0);
+            n = __builtin_amdgcn_readlane(p_en, 1);
             qs = p_q;
         }
         fetch(item + gridDim.x);
