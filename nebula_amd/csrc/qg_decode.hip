@@ -111,7 +111,7 @@ struct RouterArgs {
     float *logits;                  // [nt][rows]
     int norm; float eps; float *xn; // RMS-normalise the input; normalised rows to xn
     _Float16 *xp, *xsp;             // planes [nt][2][D] (Q4_K order); planes of 32-group sums [nt][2][D/32]
-    int row_blocks;                 // blockIdx.x < row_blocks: router rows; above: planes
+    int plane_blocks;               // blockIdx.x < plane_blocks: planes; above: router rows
     const float *bias;              // F32 [512] added to the expert logits, or null
     uint32_t *emask;                // the plan's per-expert token masks, cleared by the first plane block, or null
 };
@@ -131,89 +131,125 @@ QG_DEV float exact_row_dot(const float *w, const float *x, bool norm, float sc, 
     return qg_tree32(acc);
 }
 
-// Router: grid (R x token groups of up to 5 + ceil(nt/RW) plane blocks), RW
-// waves per block (4; 1 at one token), R = 512 / (2 RW) row blocks.  Router
-// block b covers expert rows 2RW(b % R) .. +2RW-1 and the token group b / R
+// Router: grid (ceil(nt/RW) plane blocks + R x token groups of up to 5), RW
+// waves per block (4; 1 at one token), R = 512 / (2 RW) row blocks.  The
+// plane blocks come first, so they are dispatched, and their copies queued,
+// before the router blocks' 4 MB.  Router block b (counted after the plane
+// blocks) covers expert rows 2RW(b % R) .. +2RW-1 and the token group b / R
 // (TPB tokens), so the blocks sharing a row block sit on one XCD and share its
 // router rows through that L2.  Wave w owns rows 2RW(b % R) + 2w + h (32-lane
-// half h), read into registers; the group's token
-// rows are staged in shared memory by direct global->shared copies, each
-// block starting at its own offset so the CUs do not read the same L2 lines
-// at once.  Lane j accumulates columns k = j (mod 32) in ascending k with fma,
-// then the 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal the
-// reference's qc_matmul bit for bit.  Blocks above R x groups: one token per
-// wave: the shared-expert gate logit (same order), and the (optionally
-// normalised) row as fp16 hi/lo planes in the Q4_K fragment order plus hi/lo
-// planes of the sums of each 32-group.
+// half h), read into registers; the group's token rows are staged in shared
+// memory by direct global->shared copies, each block starting at its own
+// offset so the CUs do not read the same L2 lines at once.  Lane j
+// accumulates columns k = j (mod 32) in ascending k with fma, then the
+// 16/8/4/2/1 tree: the order of cpu.c:122-139, so logits equal the
+// reference's qc_matmul bit for bit.  Plane blocks: one token per wave: the
+// shared-expert gate logit (same order), and the (optionally normalised) row
+// as fp16 hi/lo planes in the Q4_K fragment order plus hi/lo planes of the
+// sums of each 32-group.
 template <int TPB, int DW, int RW>
 __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     constexpr int KS = DW / 32, RBLK = QG_EXPERTS / (2 * RW);  // row blocks of 2 RW rows
     extern __shared__ float s_rt[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
     const int nt = A.nt;
-    if (blockIdx.x >= A.row_blocks) {
-        if (A.emask && blockIdx.x == A.row_blocks)
+    constexpr int CPT = DW / 256;  // 1 KB copies per row
+    if (blockIdx.x < A.plane_blocks) {
+        if (A.emask && blockIdx.x == 0)
             for (int i = threadIdx.x; i < QG_EXPERTS; i += 64 * RW) A.emask[i] = 0u;  // the routing kernel sets them
-        const int t = (blockIdx.x - A.row_blocks) * RW + wave;
+        const int t = blockIdx.x * RW + wave;
         if (t >= nt) return;  // whole wave; the plane blocks have no block barrier
-        const float *xr = A.x + (size_t)t * DW;
-        const float sc = A.norm ? row_rms_scale(xr, DW, A.eps, lane) : 1.0f;
+        // the token row and the shared gate vector, copied into this wave's
+        // part of shared memory by 2 CPT copies (all in flight at once, where
+        // reading them with per-lane loads took three dependent rounds)
+        float *xr = s_rt + (size_t)wave * 2 * DW, *gr = xr + DW;
+        for (int c = 0; c < CPT; c++) dma16(A.x + (size_t)t * DW + c * 256 + lane * 4, xr + c * 256);
+        if (A.sh_row)
+            for (int c = 0; c < CPT; c++) dma16(A.sh_row + c * 256 + lane * 4, gr + c * 256);
+        wait_vmem();
+        const float sc = A.norm ? lds_rms_scale(xr, DW, A.eps, lane) : 1.0f;
         if (A.sh_row) {
-            const float r = exact_row_dot<KS>(A.sh_row, xr, A.norm != 0, sc, j);
+            const float r = exact_row_dot<KS>(gr, xr, A.norm != 0, sc, j);
             if (lane == 0) A.logits[(size_t)t * A.rows + QG_EXPERTS] = r;
         }
         _Float16 *hi = A.xp + (size_t)t * 2 * DW, *shi = A.xsp + (size_t)t * 2 * (DW / 32);
         token_planes(xr, DW, A.norm != 0, sc, lane, hi, hi + DW, shi, shi + DW / 32, A.xn ? A.xn + (size_t)t * DW : nullptr);
         return;
     }
-    const int rb = blockIdx.x % RBLK, t0 = (blockIdx.x / RBLK) * TPB;
+    const int b = blockIdx.x - A.plane_blocks, rb = b % RBLK, t0 = (b / RBLK) * TPB;
     const int ntg = min(TPB, nt - t0);  // tokens of this group (>= 1)
     const int row = rb * 2 * RW + 2 * wave + half;
     const float *wr = A.router + (size_t)row * DW;
     // the group's token rows, 1 KB per copy, rotated start
-    constexpr int CPT = DW / 256;
-    const int ncp = ntg * CPT, rot = (int)((blockIdx.x * 37u) % (unsigned)ncp);
+    const int ncp = ntg * CPT, rot = (int)((b * 37u) % (unsigned)ncp);
     for (int q = wave; q < ncp; q += RW) {
         int c = q + rot;
         if (c >= ncp) c -= ncp;
         dma16(A.x + (size_t)t0 * DW + c * 256 + lane * 4, s_rt + c * 256);
     }
-    // the wave's router rows, in flight with the copies
+    // the wave's router rows, in flight with the copies: a wave has at most
+    // 63 vector-memory operations outstanding (issue stalls beyond, until
+    // the oldest returns), so the first W0 go out now and the rest during
+    // the first k-steps, long before the chains reach them
+    constexpr int NCP = (TPB * CPT + RW - 1) / RW, W0 = KS < 63 - NCP ? KS : 63 - NCP;
     float wv[KS];
 #pragma unroll
-    for (int i = 0; i < KS; i++) wv[i] = wr[32 * i + j];
+    for (int i = 0; i < W0; i++) wv[i] = wr[32 * i + j];
     wait_vmem();
     __syncthreads();
+    // normalised input: wave w scales the rows of tokens w, w + RW, ... in
+    // place (the product x * scale the reference's matmul reads, rounded as
+    // there), so the chains run one fma per step
+    if (A.norm) {
+        for (int u = wave; u < ntg; u += RW) {
+            float *xr = s_rt + u * DW;
+            const float sc = lds_rms_scale(xr, DW, A.eps, lane);  // every lane's reads precede the sum it returns
+            for (int k = lane; k < DW; k += 64) xr[k] *= sc;
+        }
+        __syncthreads();
+    }
     // past the group the chains repeat its first token and are not stored
-    float sc[TPB], acc[TPB];
+    float acc[TPB];
     const float *xb[TPB];
 #pragma unroll
     for (int u = 0; u < TPB; u++) {
-        const int uu = u < ntg ? u : 0;
-        xb[u] = s_rt + uu * DW + j;
-        sc[u] = A.norm ? lds_rms_scale(s_rt + uu * DW, DW, A.eps, lane) : 1.0f;
+        xb[u] = s_rt + (u < ntg ? u : 0) * DW + j;
         acc[u] = 0.0f;
     }
-    // the TPB chains advance together, 4 k-steps per group: the compiler
-    // barriers between groups (memory, and every accumulator) keep it from
-    // running one chain ahead while the others' reads pile up in registers
-    auto chains = [&](auto scaled) {
+    // the TPB chains advance together, 4 k-steps per group, with the next
+    // group's token values read from shared memory before this group's fmas
+    // run (the empty statements pin that order and, at the end of a group,
+    // keep the compiler from running one chain ahead while the others' reads
+    // pile up in registers)
+    float xc[4][TPB], xn[4][TPB];
 #pragma unroll
-        for (int i = 0; i < KS; i++) {
+    for (int s = 0; s < 4; s++)
 #pragma unroll
-            for (int u = 0; u < TPB; u++) {
-                const float xv = xb[u][32 * i];
-                acc[u] = __builtin_fmaf(wv[i], decltype(scaled)::value ? xv * sc[u] : xv, acc[u]);
-            }
-            if ((i & 3) == 3) {
-                asm volatile("" ::: "memory");
+        for (int u = 0; u < TPB; u++) xc[s][u] = xb[u][32 * s];
 #pragma unroll
-                for (int u = 0; u < TPB; u++) asm volatile("" : "+v"(acc[u]));
-            }
+    for (int g = 0; g < KS / 4; g++) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            if (4 * g + s + W0 < KS) wv[4 * g + s + W0] = wr[32 * (4 * g + s + W0) + j];  // the deferred rows' loads
+#pragma unroll
+            for (int u = 0; u < TPB; u++)
+                if (g + 1 < KS / 4) xn[s][u] = xb[u][32 * (4 * g + 4 + s)];
         }
-    };
-    if (A.norm) chains(std::true_type{});
-    else chains(std::false_type{});
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < TPB; u++) asm volatile("" : "+v"(acc[u]));
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int u = 0; u < TPB; u++) acc[u] = __builtin_fmaf(wv[4 * g + s], xc[s][u], acc[u]);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < TPB; u++) asm volatile("" : "+v"(acc[u]));
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int u = 0; u < TPB; u++) xc[s][u] = xn[s][u];
+    }
 #pragma unroll
     for (int u = 0; u < TPB; u++) {
         const float r = qg_tree32(acc[u]);
@@ -1553,11 +1589,11 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     // waves: 6.3 -> 6.7 us at 17 tokens); one token: 256 one-wave row blocks
     // (fewer rows per CU, so more of the router's 4 MB in flight at once)
     const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr, RW = TPB == 1 ? 1 : 4;
-    const int row_blocks = QG_EXPERTS / (2 * RW) * ngr;
-    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, row_blocks,
+    const int row_blocks = QG_EXPERTS / (2 * RW) * ngr, plane_blocks = (nt + RW - 1) / RW;
+    RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, plane_blocks,
                  L->router_bias, nt > INLINE_MAX ? pl->emask : nullptr};
-    const dim3 rgrid(row_blocks + (nt + RW - 1) / RW), rblock(64 * RW);
-    const size_t rlds = (size_t)TPB * D * 4;
+    const dim3 rgrid(plane_blocks + row_blocks), rblock(64 * RW);
+    const size_t rlds = (size_t)(TPB > 2 * RW ? TPB : 2 * RW) * D * 4;  // router blocks: the group's rows; plane blocks: two rows per wave
     if (D == 2048) router_launch<2048>(TPB, rgrid, rblock, rlds, s, R);
     else router_launch<2560>(TPB, rgrid, rblock, rlds, s, R);
     int rc = hipGetLastError();
