@@ -154,6 +154,9 @@ __global__ __launch_bounds__(256) void dec_router_kernel(RouterArgs A) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
     const int nt = A.nt;
     constexpr int CPT = DW / 256;  // 1 KB copies per row
+    // every argument in the entry batch of scalar loads (see entry_grid)
+    asm volatile("" ::"s"(A.x), "s"(A.nt), "s"(A.D), "s"(A.rows), "s"(A.router), "s"(A.sh_row), "s"(A.logits), "s"(A.norm),
+                 "s"(A.eps), "s"(A.xn), "s"(A.xp), "s"(A.xsp), "s"(A.plane_blocks), "s"(A.bias), "s"(A.emask));
     if (blockIdx.x < A.plane_blocks) {
         if (A.emask && blockIdx.x == 0)
             for (int i = threadIdx.x; i < QG_EXPERTS; i += 64 * RW) A.emask[i] = 0u;  // the routing kernel sets them
@@ -306,6 +309,25 @@ constexpr int GU_ROWS = 8;           // F rows of gate and of up per wave
 constexpr int GU_WROWS = 4 * GU_ROWS; // F rows per workgroup (4 waves)
 
 // ---- pieces shared by the gate/up kernels ----
+
+// The grid size, read at kernel entry: the compiler otherwise loads this
+// hidden kernel argument where it is first used, and its round trip then sits
+// after the routing or the expert list (scalar loads return out of order, so
+// the next shared-memory wait there waits for it too).
+QG_DEV uint32_t entry_grid() {
+    const uint32_t G = gridDim.x;
+    asm volatile("" ::"s"(G));
+    return G;
+}
+// Every gate/up argument in the entry batch of scalar loads, for the same
+// reason: a field first read after the routing (the logits pointer, the plan
+// fields) would cost a round trip there.
+QG_DEV void entry_args(const GuArgs &A) {
+    asm volatile("" ::"s"(A.nt), "s"(A.D), "s"(A.F), "s"(A.inline_route), "s"(A.logits), "s"(A.ld), "s"(A.resident),
+                 "s"(A.ids), "s"(A.w), "s"(A.flags_out), "s"(A.pl));
+    asm volatile("" ::"s"(A.gate), "s"(A.up), "s"(A.sh_gate), "s"(A.sh_up), "s"(A.rb), "s"(A.xp), "s"(A.xsp), "s"(A.midp),
+                 "s"(A.msum8), "s"(A.fmt), "s"(A.sh_fmt));
+}
 
 // Warm this XCD's L2 with the batch's activation and sum planes while the
 // plan is built (workgroups b, b + 8, ... share an XCD; each takes 4 KB); the
@@ -466,6 +488,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     __shared__ __align__(16) int s_ri[QG_ROUTE_SCRATCH];
     __shared__ int s_rank[QG_TOP], s_rid[QG_TOP];
     __shared__ int s_nent;
+    const uint32_t G = entry_grid();
+    entry_args(A);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int D = A.D, D32 = D / 32, RBK = A.F / GU2_ROWS;
     const GuPlan P = gu_plan_at(s_dyn);
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     const int sh_tiles = A.sh_gate ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
     const int ntl = sh_tiles + (INL ? s_nent : *P.ntiles), N = ntl * RBK;
     // N <= (3 + 170) * F / 16 items and at most 1024 workgroups: 32-bit products suffice
-    const int i0 = (int)((uint32_t)N * blockIdx.x / gridDim.x), i1 = (int)((uint32_t)N * (blockIdx.x + 1) / gridDim.x);
+    const int i0 = (int)((uint32_t)N * blockIdx.x / G), i1 = (int)((uint32_t)N * (blockIdx.x + 1) / G);
     const int T0 = i0 / RBK;
     if (wave == 0) {
         // the range's tiles (lane l: tile T0 + l / 8, list slot l % 8); the
@@ -809,14 +833,19 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     int *s_ids = (int *)(s_xt + GU3_MAXX);  // the routing ids, so the selections need no global reads behind the copies
     __shared__ int s_nx;
     __shared__ int s_tq[GU3_MAXT][TILE_TOK], s_tt[GU3_MAXT][TILE_TOK], s_tn[GU3_MAXT];
+    const uint32_t G = entry_grid();
+    entry_args(A);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int RBK = A.F / GU2_ROWS;
     const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
-    if (tid < A.nt * QG_TOP) s_ids[tid] = A.ids[tid];  // read before any copy is in flight
-    if (wave == 0) {
-        uint32_t em[QG_EXPERTS / 64];
+    // the masks, then the routing ids (read before any copy is in flight), in
+    // one memory round trip
+    uint32_t em[QG_EXPERTS / 64];
+    if (wave == 0)
 #pragma unroll
         for (int i = 0; i < QG_EXPERTS / 64; i++) em[i] = A.pl->emask[64 * i + lane];
+    if (tid < A.nt * QG_TOP) s_ids[tid] = A.ids[tid];
+    if (wave == 0) {
         if (lane == 0 && sh) { s_xe[0] = -1; s_xk[0] = -1; s_xm[0] = sh_tiles; s_xt[0] = 0u; }
         const unsigned long long below = (1ULL << lane) - 1ULL;
         int nx = sh, ntl = 0;
@@ -863,7 +892,7 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     // this workgroup's expert: the one whose cost range holds the midpoint of
     // its share; its blocks are split evenly over the expert's workgroups
     // (C <= RBK (GU3_COST + 3) 173 and G <= 1024: 32-bit products suffice)
-    const uint32_t C = (uint32_t)s_cum[nx], G = gridDim.x, g = blockIdx.x;
+    const uint32_t C = (uint32_t)s_cum[nx], g = blockIdx.x;
     const uint32_t pos = ((2 * g + 1) * C) / (2 * G);
     int x = 0;
     for (int c0 = 0; c0 < nx; c0 += 64) {
@@ -1197,6 +1226,10 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
     __shared__ float s_wt[TILE_TOK];  // and routing weights (1 for the shared expert)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     constexpr int F = FF;  // the layer's F (512 or 640): a constant, so the staging splits need no division
+    const uint32_t G = entry_grid();
+    // every argument in the entry batch of scalar loads (see entry_grid)
+    asm volatile("" ::"s"(A.nt), "s"(A.D), "s"(A.F), "s"(A.w), "s"(A.pl), "s"(A.down), "s"(A.sh_down), "s"(A.rb), "s"(A.sh_rb),
+                 "s"(A.midp), "s"(A.msum8), "s"(A.slots));
     const int sh = A.sh_down != nullptr ? 1 : 0;
     const int dblocks = A.D / DN_ROWS;
     const int rbmax = (int)(A.rb > A.sh_rb ? A.rb : A.sh_rb);
@@ -1222,7 +1255,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
         }
     };
     fetch(blockIdx.x);
-    for (int item = blockIdx.x;; item += gridDim.x) {
+    for (int item = blockIdx.x;; item += G) {
         const int T = item / dblocks, d0 = (item - T * dblocks) * DN_ROWS;
         // this item's expert e (-1: shared), token count n (-1: past the
         // plan) and the selection qs of tile slot lane % 8, alike in every wave
@@ -1235,7 +1268,7 @@ __global__ __launch_bounds__(256, 2) void dec_down_kernel(DnArgs A) {
             n = __builtin_amdgcn_readlane(p_en, 1);
             qs = p_q;
         }
-        fetch(item + gridDim.x);
+        fetch(item + G);
         if (n < 0) break;  // block-uniform; every later item is past the plan too
         float wq = 1.0f;  // wave 0: the routing weight of tile slot `lane`, loaded behind the copies
         if (wave == 0 && lane < n) {
@@ -1307,6 +1340,9 @@ struct CombArgs {
 // rows 0.
 __global__ __launch_bounds__(256) void dec_combine_kernel(CombArgs A) {
     const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
+    // every argument in the entry batch of scalar loads (see entry_grid)
+    asm volatile("" ::"s"(A.nt), "s"(A.D), "s"(A.ids), "s"(A.pl), "s"(A.slots), "s"(A.sh_logit), "s"(A.ld), "s"(A.has_shared));
+    asm volatile("" ::"s"(A.out), "s"(A.resid), "s"(A.stats));
     if (d < A.D) {
         // every load is independent of the others (slot addresses do not depend
         // on the ids): one memory round trip; invalid selections are selected away
