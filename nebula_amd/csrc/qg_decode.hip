@@ -468,6 +468,7 @@ constexpr int GU2_ROWS = 16;                  // F rows per item (16 gate + 16 u
 constexpr int GU2_SL = 32 * 18;              // 16-byte slots per item and wave: 32 rows x 2 superblocks of 144 bytes
 constexpr int GU2_NT = 4;                     // tiles a workgroup's item range may touch
 constexpr size_t GU2_LDS = (size_t)4 * 2 * GU2_SL * 16;  // 4 waves x 2 buffers
+constexpr int GU2_CPH = (GU2_SL / 2 + 63) / 64;  // copies per wave and superblock half of an item
 
 // One token (INL) at D = 2048.
 // Persistent: the layer's items (tile, 16 F rows) in tile order, split into
@@ -520,60 +521,84 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     __syncthreads();
     if (i1 <= i0) return;  // block-uniform
     uint4 *wl = s_dyn + (size_t)wave * 2 * GU2_SL;  // this wave's two buffers
-    // item -> the wave's copies into buffer b
-    auto copy_item = [&](int item, int b) {
+    // superblock sb of an item's 32 weight rows -> the wave's copies into
+    // buffer b: 9 pieces per row (header, 8 nibble chunks), superblock 1's
+    // rows after superblock 0's, each row rotated by row / 8 pieces so the 16
+    // rows of a fragment read spread over the banks; GU2_CPH copies per half
+    auto copy_half = [&](int item, int b, int sb) {
         const int ti = item / RBK - T0, rb = item % RBK, e = s_te[ti][0];
         const uint8_t *gm = e < 0 ? A.sh_gate : A.gate + (size_t)e * A.F * A.rb;
         const uint8_t *um = e < 0 ? A.sh_up : A.up + (size_t)e * A.F * A.rb;
 #pragma unroll
-        for (int i = 0; i < GU2_SL / 64; i++) {
-            // slot sl = 18 row + position; the row's 288 bytes (its two
-            // superblocks, headers included) are one contiguous run, rotated
-            // by 2 (row / 8) positions so the 16 rows of a fragment read
-            // spread over the banks
-            const int sl = i * 64 + lane, row = sl / 18, pc = sl - 18 * row;
-            const int c = pc - 2 * (row >> 3) + (pc < 2 * (row >> 3) ? 18 : 0);
-            dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 288 + 16 * c,
-                          wl + (size_t)b * GU2_SL + i * 64);
+        for (int i = 0; i < GU2_CPH; i++) {
+            const int s = i * 64 + lane, row = s / 9, pc = s - 9 * row, rot = row >> 3;
+            const int c = pc - rot + (pc < rot ? 9 : 0);
+            if (s < GU2_SL / 2)
+                dma16_ordered((row < 16 ? gm : um) + (size_t)(rb * GU2_ROWS + (row & 15)) * A.rb + (size_t)wave * 288 +
+                                  (size_t)sb * 144 + 16 * c,
+                              wl + (size_t)b * GU2_SL + (size_t)sb * (GU2_SL / 2) + i * 64);
         }
     };
-    copy_item(i0, 0);
-    int cur = -1;
+    // the tile's activation fragments for superblock sb of this wave: plane
+    // row r = (token r/2, plane r%2).  Buffer loads: rows past the tile's
+    // tokens take an offset past the planes and read zeros without a memory
+    // access, and every load is issued by every lane (a load under a branch
+    // would keep the compiler from counting it in its waits below)
+    const __amdgpu_buffer_rsrc_t xpr = __builtin_amdgcn_make_buffer_rsrc((void *)A.xp, (short)0, A.nt * 2 * D * 2, QG_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc((void *)A.xsp, (short)0, A.nt * 2 * D32 * 2, QG_BUF_DW3);
     qg_half8 af[2][8], sf[2];
-    for (int k = 0; i0 + k < i1; k++) {
+    auto load_af = [&](int ti, int sb) {
+        const int n = s_te[ti][1], e = s_te[ti][0];
+        const bool real = (j >> 1) < n;
+        const int r = 2 * min(j >> 1, n - 1) + (j & 1), sl0 = s_tl[ti][r >> 1];
+        const int tok = e < 0 ? sl0 - MS : sl0 / QG_TOP;
+        const int xo = ((tok * 2 + (r & 1)) * D + wave * 512 + sb * 256 + kq * 8) * 2;
+        const int so = ((tok * 2 + (r & 1)) * D32 + wave * 16 + sb * 8) * 2;
+#pragma unroll
+        for (int m = 0; m < 8; m++) af[sb][m] = buf_frag(xpr, real ? xo + m * 64 : QG_BUF_OOB);
+        sf[sb] = buf_frag(xsr, (kq || !real) ? QG_BUF_OOB : so);
+    };
+    // the first item: superblock 0's fragments and copies go out before
+    // superblock 1's, so its products can start while superblock 1 streams
+    // (the compiler's own waits for the fragments then cover no copies)
+    load_af(0, 0);
+    copy_half(i0, 0, 0);
+    load_af(0, 1);
+    copy_half(i0, 0, 1);
+    // item k of the range; the first one is a separate instance, so the
+    // compiler's waits there see only the loads above (a shared loop would
+    // merge in the later items' fragment reloads)
+    int cur = 0;
+    auto item_body = [&](int k, auto first) {
+        constexpr bool FIRST = decltype(first)::value;
         const int item = i0 + k, ti = item / RBK - T0, rb = item % RBK, b = k & 1;
         const int e = s_te[ti][0], n = s_te[ti][1];
-        if (ti != cur) {
-            // the tile's activation fragments for this wave's superblocks:
-            // plane row r = (token r/2, plane r%2)
-            // rows past the tile's tokens are zeros, not loaded
-            const bool real = (j >> 1) < n;
-            const int r = 2 * min(j >> 1, n - 1) + (j & 1), sl0 = s_tl[ti][r >> 1];
-            const int tok = e < 0 ? sl0 - MS : sl0 / QG_TOP;
-            const _Float16 *xr = A.xp + ((size_t)tok * 2 + (r & 1)) * D + (size_t)wave * 512 + kq * 8;
-            const _Float16 *xs = A.xsp + ((size_t)tok * 2 + (r & 1)) * D32 + (size_t)wave * 16;
-#pragma unroll
-            for (int sb = 0; sb < 2; sb++) {
-#pragma unroll
-                for (int m = 0; m < 8; m++) af[sb][m] = real ? ld_frag(xr + sb * 256 + m * 32) : qg_half8{};
-                sf[sb] = (kq || !real) ? qg_half8{} : ld_frag(xs + sb * 8);
-            }
+        if (!FIRST && ti != cur) {
+            load_af(ti, 0);
+            load_af(ti, 1);
             cur = ti;
         }
-        wait_vmem();  // this item's copies (and fragments) have landed
-        if (i0 + k + 1 < i1) copy_item(item + 1, b ^ 1);
         const uint4 *wb = wl + (size_t)b * GU2_SL;
-        qg_f4 y[2];
+        qg_f4 y[2] = {qg_f4{0.0f, 0.0f, 0.0f, 0.0f}, qg_f4{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-            y[cb] = qg_f4{0.0f, 0.0f, 0.0f, 0.0f};
-            const int row = cb * 16 + j, rot = 2 * (row >> 3);
-            // piece c of the row (0: header 0, 1..8: nibbles 0, 9: header 1, 10..17: nibbles 1)
-            auto piece = [&](int c) { const int x = c + rot; return wb[18 * row + (x >= 18 ? x - 18 : x)]; };
+        for (int sb = 0; sb < 2; sb++) {
+            if (sb == 0) {
+                if (FIRST) wait_vmem_but<GU2_CPH>();  // all but superblock 1's copies
+                else wait_vmem();  // this item's copies (issued during the previous item) and fragments
+            } else {
+                wait_vmem();  // this item's copies and fragments
+                if (i0 + k + 1 < i1) {  // the next item streams during this superblock's products and the epilogue
+                    copy_half(item + 1, b ^ 1, 0);
+                    copy_half(item + 1, b ^ 1, 1);
+                }
+            }
 #pragma unroll
-            for (int sb = 0; sb < 2; sb++) {
-                const Q4kHeader h = q4k_header(piece(9 * sb));
-                const uint4 ch0 = piece(9 * sb + 1 + kq), ch1 = piece(9 * sb + 5 + kq);
+            for (int cb = 0; cb < 2; cb++) {
+                const int row = cb * 16 + j, rot = row >> 3;
+                // piece c of the row's superblock (0: header, 1..8: nibbles)
+                auto piece = [&](int c) { const int x = c + rot; return wb[(size_t)sb * (GU2_SL / 2) + 9 * row + (x >= 9 ? x - 9 : x)]; };
+                const Q4kHeader h = q4k_header(piece(0));
+                const uint4 ch0 = piece(1 + kq), ch1 = piece(5 + kq);
                 qg_half2 scA, ofA, scB, ofB;  // scales of groups gA, gA + 1 and gB, gB + 1
                 gq_scales(h.S[0], kq, scA, ofA);
                 gq_scales(h.S[1], kq, scB, ofB);
@@ -623,7 +648,9 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
             }
         }
         __syncthreads();  // buffer b is free for the item after next
-    }
+    };
+    item_body(0, std::true_type{});
+    for (int k = 1; i0 + k < i1; k++) item_body(k, std::false_type{});
 }
 
 // ---- K2 at D = 2048, one expert per workgroup ----

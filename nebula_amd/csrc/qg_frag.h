@@ -94,6 +94,14 @@ QG_DEV qg_half8 gq_frag(uint4 c, int f, _Float16 sc, _Float16 of) {
     return r;
 }
 QG_DEV qg_half8 ld_frag(const _Float16 *p) { return __builtin_bit_cast(qg_half8, *(const uint4 *)p); }
+// Raw buffer loads (no stride; the byte range is the descriptor's record
+// count): an offset past the range reads zeros with no memory access.
+// QG_BUF_DW3: descriptor word 3 for gfx9 raw buffers (32-bit data format).
+constexpr int QG_BUF_DW3 = 0x00020000;
+constexpr int QG_BUF_OOB = 0x7fff0000;  // an offset past any range used here
+QG_DEV qg_half8 buf_frag(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(qg_half8, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
 
 typedef __attribute__((address_space(3))) void qg_lds_void;
 
