@@ -1479,18 +1479,30 @@ template <int FMT, int SFMT>
 __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
     extern __shared__ uint4 s_dyn[];
     __shared__ float s_v[QG_TOP + 1][DN1_ROWS];
+    // every argument in the entry batch of scalar loads (see entry_grid)
+    asm volatile("" ::"s"(A.D), "s"(A.F), "s"(A.w), "s"(A.pl), "s"(A.down), "s"(A.sh_down), "s"(A.rb), "s"(A.sh_rb),
+                 "s"(A.midp), "s"(A.msum8), "s"(A.sh_logit), "s"(A.out), "s"(A.resid), "s"(A.stats));
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kq = lane >> 4;
     const int F = A.F, d0 = blockIdx.x * DN1_ROWS, sh = A.sh_down ? 1 : 0;
-    const int nent = A.pl->n_tiles, flag = A.pl->flag[0], E = nent + sh;
     uint4 *wl = s_dyn + (size_t)wave * DN1_EPW * DN1_SL;
     _Float16 *mids = (_Float16 *)(s_dyn + (size_t)DN1_W * DN1_EPW * DN1_SL);  // [E][2][F] mid planes
     float *msl = (float *)(mids + (size_t)(QG_TOP + 1) * 2 * F);          // [E][F/8] 8-row sums
+    // the wave's plan entries, read with the entry count in one round trip
+    // (entries k < DN1_W * DN1_EPW <= MAX_TILES always lie in the plan; those
+    // past the count are then dropped)
     int ee[DN1_EPW], qq[DN1_EPW];
 #pragma unroll
     for (int x = 0; x < DN1_EPW; x++) {
         const int k = wave + DN1_W * x;
-        ee[x] = k < nent ? A.pl->tile[k].e : -1;
-        qq[x] = k < nent ? A.pl->tile[k].q[0] : MS;
+        ee[x] = A.pl->tile[k].e;
+        qq[x] = A.pl->tile[k].q[0];
+    }
+    const int nent = A.pl->n_tiles, flag = A.pl->flag[0], E = nent + sh;
+#pragma unroll
+    for (int x = 0; x < DN1_EPW; x++) {
+        const int k = wave + DN1_W * x;
+        ee[x] = k < nent ? ee[x] : -1;
+        qq[x] = k < nent ? qq[x] : MS;
     }
     // every copy at once: this wave's entries' weight rows, and (spread over the
     // waves) each entry's two mid plane rows and its 8-row sums
@@ -1512,6 +1524,12 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
             if (lane < F / 32) dma16_ordered(A.msum8 + (size_t)q * (F / 8) + lane * 4, msl + (size_t)k * (F / 8));
         }
     }
+    // the entries' routing weights, read while the copies stream (read
+    // before them, the dependent load would delay their issue; read at the
+    // end, it would add a round trip after the products)
+    float wq[DN1_EPW];
+#pragma unroll
+    for (int x = 0; x < DN1_EPW; x++) wq[x] = wave + DN1_W * x < nent ? A.w[qq[x]] : 1.0f;
     wait_vmem();
     __syncthreads();
 #pragma unroll
@@ -1578,7 +1596,7 @@ __global__ __launch_bounds__(64 * DN1_W) void dec_down1_kernel(Dn1Args A) {
             }
             // lanes kq = 0 hold rows 0 (hi) and 1 (lo) of weight row j
             const float v = y[0] + y[1];
-            if (kq == 0 && j < DN1_ROWS) s_v[k][j] = shared ? v : v * A.w[q];
+            if (kq == 0 && j < DN1_ROWS) s_v[k][j] = shared ? v : v * wq[x];
         }
     }
     __syncthreads();
