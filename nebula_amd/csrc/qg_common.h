@@ -284,13 +284,33 @@ QG_DEV void qg_route_vals(const float (&v)[8], const float *s, int lane, int &id
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // rank of candidate `lane` among the total_c candidates
+    // rank of candidate `lane` among the total_c candidates, every lane
+    // reading candidates 0..15 from shared memory at once (the same
+    // addresses in every lane; entries past total_c are not counted), then
+    // any further ones one by one
     const float cv = lane < total_c ? lds_v[lane] : 0.0f;
     const int ci = lane < total_c ? lds_i[lane] : 0;
     int rank = 0;
-    for (int q = 0; q < total_c; q++) {  // candidate q from its lane's registers (wave-uniform q)
-        const float ov = rl(cv, q);
-        const int oi = __builtin_amdgcn_readlane(ci, q);
+    {
+        float4 ov[4];
+        int4 oi[4];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; c4++) {
+            ov[c4] = ((const float4 *)lds_v)[c4];
+            oi[c4] = ((const int4 *)lds_i)[c4];
+        }
+#pragma unroll
+        for (int c4 = 0; c4 < 4; c4++) {
+            const float o_v[4] = {ov[c4].x, ov[c4].y, ov[c4].z, ov[c4].w};
+            const int o_i[4] = {oi[c4].x, oi[c4].y, oi[c4].z, oi[c4].w};
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                rank += (4 * c4 + u < total_c) & ((o_v[u] > cv) | ((o_v[u] == cv) & (o_i[u] < ci)));
+        }
+    }
+    for (int q = 16; q < total_c; q++) {
+        const float ov = lds_v[q];
+        const int oi = lds_i[q];
         rank += (ov > cv) | ((ov == cv) & (oi < ci));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -302,10 +322,21 @@ QG_DEV void qg_route_vals(const float (&v)[8], const float *s, int lane, int &id
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane < QG_TOP) id_out = lds_i[lane];
     if (!weights) return;  // wave-uniform
+    // the numerators (lane k: rank k) through shared memory, summed in rank
+    // order by every lane
     const float num = lane < QG_TOP ? qg_expf(lds_v[lane] - largest) : 0.0f;
+    if (lane < QG_TOP) lds_v[lane] = num;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float nk[12];
+    *(float4 *)&nk[0] = ((const float4 *)lds_v)[0];
+    *(float4 *)&nk[4] = ((const float4 *)lds_v)[1];
+    *(float4 *)&nk[8] = ((const float4 *)lds_v)[2];
+    static_assert(QG_TOP <= 12, "the numerators fit three 16-byte reads");
     float total = 0.0f;
 #pragma unroll
-    for (int k = 0; k < QG_TOP; k++) total += rl(num, k);
+    for (int k = 0; k < QG_TOP; k++) total += nk[k];
     if (lane < QG_TOP) w_out = num / total;
 }
 QG_DEV void qg_route_fast(const float *s, int lane, int &id_out, float &w_out, float *lds_v, int *lds_i, bool weights = true) {
