@@ -632,10 +632,14 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++) {
                 const float m = qg_swiglu_fast(g[2 * t2] + g[2 * t2 + 1], u[2 * t2] + u[2 * t2 + 1]);
-                float s8 = m;  // sum over the 8 rows of this lane's group
-                s8 += __shfl_xor(s8, 1);
-                s8 += __shfl_xor(s8, 2);
-                s8 += __shfl_xor(s8, 4);
+                // the sum over the 8 rows of this lane's group: only a Q4_K down reads it
+                const bool q4k = fmt == QT_Q4_K;  // workgroup-uniform
+                float s8 = m;
+                if (q4k) {
+                    s8 += __shfl_xor(s8, 1);
+                    s8 += __shfl_xor(s8, 2);
+                    s8 += __shfl_xor(s8, 4);
+                }
                 const int idx = 2 * kq + t2;
                 if (idx < n) {
                     const int sl = s_tl[ti][idx];
@@ -643,7 +647,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
                     const _Float16 hv = (_Float16)m;
                     mp[pos] = hv;
                     mp[A.F + pos] = (_Float16)(m - (float)hv);
-                    if ((j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
+                    if (q4k && (j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
                 }
             }
         }
@@ -828,10 +832,15 @@ QG_DEV void gu3_run(const GuArgs &A, const int *ids, int e, int rb0, int rb1, co
             }
             const int rb = rb0 + it, frow = rb * GU2_ROWS + j, pos = plane_pos(fmt, frow);
             const float mv = qg_swiglu_fast(g, u);
-            float s8 = mv;  // sum over the 8 rows of this lane's group
-            s8 += __shfl_xor(s8, 1);
-            s8 += __shfl_xor(s8, 2);
-            s8 += __shfl_xor(s8, 4);
+            // the sum over the 8 rows of this lane's group, which only a Q4_K
+            // down reads (its min term); an IQ4_NL down needs none
+            const bool q4k = fmt == QT_Q4_K;  // workgroup-uniform
+            float s8 = mv;
+            if (q4k) {
+                s8 += __shfl_xor(s8, 1);
+                s8 += __shfl_xor(s8, 2);
+                s8 += __shfl_xor(s8, 4);
+            }
             const int idx = 2 * kq + t2;
             if (idx < n) {
                 const int sl = tq[m][idx];
@@ -839,7 +848,7 @@ QG_DEV void gu3_run(const GuArgs &A, const int *ids, int e, int rb0, int rb1, co
                 const _Float16 hv = (_Float16)mv;
                 mp[pos] = hv;
                 mp[A.F + pos] = (_Float16)(mv - (float)hv);
-                if ((j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
+                if (q4k && (j & 7) == 0) A.msum8[(size_t)sl * (A.F / GU_ROWS) + frow / GU_ROWS] = s8;
             }
         }
     }
