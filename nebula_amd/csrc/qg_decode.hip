@@ -303,6 +303,11 @@ struct GuArgs {
     const _Float16 *xp, *xsp;
     _Float16 *midp; float *msum8;    // mid planes [ME][2][F] in the down format's order; sums of 8 rows [ME][F/8]
     int fmt, sh_fmt;                 // down formats of the routed and shared experts
+    // one token, when the next kernel is dec_down1_kernel: the down matrices
+    // (288-byte rows), whose rows that kernel's workgroup g reads are read here
+    // once this workgroup's own copies have landed (HBM is idle while its
+    // products run), so that kernel finds them in the Infinity Cache; or null
+    const uint8_t *dn_pre, *sh_dn_pre;
 };
 
 constexpr int GU_ROWS = 8;           // F rows of gate and of up per wave
@@ -469,6 +474,7 @@ constexpr int GU2_SL = 32 * 18;              // 16-byte slots per item and wave:
 constexpr int GU2_NT = 4;                     // tiles a workgroup's item range may touch
 constexpr size_t GU2_LDS = (size_t)4 * 2 * GU2_SL * 16;  // 4 waves x 2 buffers
 constexpr int GU2_CPH = (GU2_SL / 2 + 63) / 64;  // copies per wave and superblock half of an item
+constexpr int DN1_PRE_ROWS = 8;                   // output rows per dec_down1_kernel workgroup (DN1_ROWS)
 
 // One token (INL) at D = 2048.
 // Persistent: the layer's items (tile, 16 F rows) in tile order, split into
@@ -565,6 +571,8 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     copy_half(i0, 0, 0);
     load_af(0, 1);
     copy_half(i0, 0, 1);
+    // down1's rows prefetched by workgroups g < D / DN1_PRE_ROWS with a single item
+    const bool pre = INL && A.dn_pre != nullptr && i1 - i0 == 1 && (int)blockIdx.x < D / DN1_PRE_ROWS;
     // item k of the range; the first one is a separate instance, so the
     // compiler's waits there see only the loads above (a shared loop would
     // merge in the later items' fragment reloads)
@@ -590,6 +598,20 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
                 if (i0 + k + 1 < i1) {  // the next item streams during this superblock's products and the epilogue
                     copy_half(item + 1, b ^ 1, 0);
                     copy_half(item + 1, b ^ 1, 1);
+                } else if (FIRST && INL && pre) {
+                    // down1's rows for workgroup g = blockIdx.x of every entry
+                    // (the plan's eligible ranks, then the shared expert), into
+                    // the unused second buffer, whose contents nothing reads
+                    const int E = s_nent + (A.sh_dn_pre ? 1 : 0);
+                    for (int x = wave; x < E; x += 4) {
+                        const uint8_t *W = (x < s_nent ? A.dn_pre + (size_t)s_rid[x] * D * 288 : A.sh_dn_pre) +
+                                           (size_t)blockIdx.x * DN1_PRE_ROWS * 288;
+#pragma unroll
+                        for (int c = 0; c < (DN1_PRE_ROWS * 288 / 16 + 63) / 64; c++) {
+                            const int ch = c * 64 + lane;
+                            if (ch < DN1_PRE_ROWS * 288 / 16) dma16_ordered(W + 16 * ch, wl + (size_t)(b ^ 1) * GU2_SL + c * 64);
+                        }
+                    }
                 }
             }
 #pragma unroll
@@ -655,6 +677,7 @@ __global__ __launch_bounds__(256, 2) void dec_gateup2_kernel(GuArgs A) {
     };
     item_body(0, std::true_type{});
     for (int k = 1; i0 + k < i1; k++) item_body(k, std::false_type{});
+    if (pre) wait_vmem();  // no copy may land in shared memory after the workgroup ends
 }
 
 // ---- K2 at D = 2048, one expert per workgroup ----
@@ -1470,6 +1493,7 @@ struct Dn1Args {
     qg_prune_stats *stats;
 };
 constexpr int DN1_ROWS = 8;              // output rows per workgroup (MFMA columns 8..15 repeat 0..7)
+static_assert(DN1_ROWS == DN1_PRE_ROWS, "gate/up prefetches the rows of this kernel's workgroups");
 constexpr int DN1_SL = DN1_ROWS * 288 / 16;  // 16-byte slots of the rows (288 bytes each)
 constexpr int DN1_W = 16;                // waves per workgroup
 constexpr int DN1_EPW = 1;               // entries per wave (10 routed + 1 shared, each on its own wave)
@@ -1699,7 +1723,13 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     GuArgs G2{nt, D, F, inl ? 1 : 0, logits, rows, L->resident, L->threshold, ids, weights, flags, pl,
               (const uint8_t *)L->gate, (const uint8_t *)L->up, sh ? (const uint8_t *)L->sh_gate : nullptr,
               sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D), xp, xsp, midp, msum8,
-              L->down_type, sh ? L->sh_down_type : L->down_type};
+              L->down_type, sh ? L->sh_down_type : L->down_type, nullptr, nullptr};
+    const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;
+    const bool down1 = inl && F == 512 && rb == 288 && (!sh || srb == 288) && D % DN1_ROWS == 0;
+    if (down1) {
+        G2.dn_pre = (const uint8_t *)L->down;
+        G2.sh_dn_pre = sh ? (const uint8_t *)L->sh_down : nullptr;
+    }
     // upper bound of the tiles: the shared expert's, and every selection its own tile
     const int tiles = (sh ? (nt + TILE_TOK - 1) / TILE_TOK : 0) + nt * QG_TOP;
     const int items = tiles * (F / GU_WROWS);
@@ -1722,7 +1752,6 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
         else dec_launch(2, dec_gateup_kernel<10, false>, dim3(nwg), dim3(256), gu_bytes, s, G2);
     }
     if ((rc = hipGetLastError())) return rc;
-    const size_t rb = qg_row_bytes_host(L->down_type, F), srb = sh ? qg_row_bytes_host(L->sh_down_type, F) : 0;
     float *slots = (float *)(ws + lay.slots);
     DnArgs DA{nt, D, F, weights, pl, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
               midp, msum8, slots};
@@ -1731,7 +1760,7 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     const size_t dn_lds = ((DN_ROWS * rbmax + 1023) & ~(size_t)1023) + (size_t)16 * F * 2 +
                           (((size_t)8 * (F / 8 + 4) * 4 + 1023) & ~(size_t)1023);
     const int fr = L->down_type, fs = sh ? L->sh_down_type : fr;
-    if (inl && F == 512 && rb == 288 && (!sh || srb == 288) && D % DN1_ROWS == 0) {
+    if (down1) {
         // one token: down and the combine in one kernel
         Dn1Args D1{D, F, weights, pl, (const uint8_t *)L->down, sh ? (const uint8_t *)L->sh_down : nullptr, rb, srb,
                    midp, msum8, logits + QG_EXPERTS, out, resid, (L->resident && stats) ? stats : nullptr};
