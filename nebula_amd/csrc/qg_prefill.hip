@@ -874,19 +874,23 @@ QG_DEV qg_half8 stage_frag128(const uint8_t *st, int r, int p, int c) {
     return ld_frag((const _Float16 *)(st + (r * 2 + p) * 256 + 16 * (c ^ (r & 15))));
 }
 
-// y[m][n] += d_b * (lut[q] . x) for the nb blocks of a step, weights from the
+struct NoIssue {
+    __device__ __forceinline__ void operator()(int) const {}
+};
+// y[m][n] += d_b * (lut[q] . x) for the 4 blocks of a step, weights from the
 // slot (row 16 n + j of the wave's 32: its step's bytes start at byte del[n]
-// of its slot row), activations from the stage.
-template <int M, int MY>
+// of its slot row), activations from the stage; issue(b) runs after block
+// b's products (the caller's copies for later steps go out while the matrix
+// cores work).
+template <int M, int MY, typename Issue = NoIssue>
 QG_DEV void iq_chunk_lds(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const int (&del)[NCT], const uint8_t *st, int j, int kq,
-                         int nb) {
+                         Issue issue = Issue{}) {
     static_assert(M <= MY, "row tiles");
     const uint8_t *rowp[NCT];
 #pragma unroll
     for (int n = 0; n < NCT; n++) rowp[n] = slot + (16 * n + j) * IQ_ROWB + del[n];
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b >= nb) break;  // uniform
+    for (int b = 0; b < IQ_KC / 32; b++) {  // F is a multiple of 128 (checked at launch): 4 blocks per step
         qg_half8 bf[NCT];
         float d[NCT];
 #pragma unroll
@@ -906,6 +910,7 @@ QG_DEV void iq_chunk_lds(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const int (&d
                 for (int i = 0; i < 4; i++) y[m][n][i] = __builtin_fmaf(d[n], acc[i], y[m][n][i]);
             }
         }
+        issue(b);
     }
 }
 
@@ -1039,27 +1044,32 @@ __global__ __launch_bounds__(512, 1) void pf_down_iq_kernel(DnArgs A) {
                 // the next item's rows, copied while this item streams
                 if (k + 1 < nitems) set_rows(R.at(k + 1), (k + 1) & 1);
             }
-            if (s + 1 < steps) {
-                if (kc == nkc - 1) {
-                    if (nkc == 1) {  // the rows were copied just above
-                        wait_vmem();
-                        __syncthreads();
+            // the next step's stage after block 0's products, then the weights
+            // of step s + 2 after block 1's (in this order: the wait above
+            // relies on it)
+            auto issue = [&](int b) {
+                if (b == 0 && s + 1 < steps) {
+                    if (kc == nkc - 1) {
+                        if (nkc == 1) {  // the rows were copied at the top of the step
+                            wait_vmem();
+                            __syncthreads();
+                        }
+                        set_sp(R.at(k + 1), (k + 1) & 1);
                     }
-                    set_sp(R.at(k + 1), (k + 1) & 1);
+                    stage_at(s + 1, kc + 1 < nkc ? kc + 1 : 0);
                 }
-                stage_at(s + 1, kc + 1 < nkc ? kc + 1 : 0);
-            }
-            if (s + 2 < steps) {
-                // step s + 2 is step kc + 2 of this item or of the next one(s)
-                const int kr = kc + 2 - nkc, kc2 = kr < 0 ? kc + 2 : nkc == 1 ? 0 : kr;
-                if (kc2 == 0) set_wc(R.at(k + (kr < 0 ? 0 : nkc == 1 ? 2 : 1)));  // it starts a later item
-                copy_w(qn, kc2);
-            }
+                if (b == 1 && s + 2 < steps) {
+                    // step s + 2 is step kc + 2 of this item or of the next one(s)
+                    const int kr = kc + 2 - nkc, kc2 = kr < 0 ? kc + 2 : nkc == 1 ? 0 : kr;
+                    if (kc2 == 0) set_wc(R.at(k + (kr < 0 ? 0 : nkc == 1 ? 2 : 1)));  // it starts a later item
+                    copy_w(qn, kc2);
+                }
+            };
             int del[NCT];
 #pragma unroll
             for (int n = 0; n < NCT; n++) del[n] = (int)((rlo[n] + (uint32_t)kc * 72u) & 15u);
             const uint8_t *slot = ring + qc * IQ_SLOT, *st = lds + (s & 1) * IQ_STAGE;
-            iq_chunk_lds<M>(y, slot, del, st, j, kq, nblocks(kc));
+            iq_chunk_lds<M>(y, slot, del, st, j, kq, issue);
             qc = qc == 2 ? 0 : qc + 1;
         }
         const int d0 = it.blk * DN_DB + wave * 32;
@@ -1187,9 +1197,6 @@ QG_DEV void gq_chunk_i8(qg_f4 (&y)[MY][NCT], const uint8_t *slot, const uint8_t 
     }
 }
 
-struct NoIssue {
-    __device__ __forceinline__ void operator()(int) const {}
-};
 // One half superblock for the first M row tiles: per K step f (4 of them)
 // the two weight fragments, then every row tile's products (fragment f + 1
 // is built while step f's products run); y += d * acc per half, and with the
