@@ -297,6 +297,8 @@ __global__ __launch_bounds__(64) void dec_route_kernel(RouteArgs A) {
 // ---------------- K2: gate/up + SwiGLU ----------------
 struct GuArgs {
     int nt, D, F;
+    // routing inside the kernel: 1 the one token (template INL kernels),
+    // 2 the batch (dec_gateup3_kernel), 0 none (the routing kernel ran)
     int inline_route; const float *logits; int ld; const uint8_t *resident; double thr;
     int *ids; float *w; uint8_t *flags_out; DecPlan *pl;
     const uint8_t *gate, *up, *sh_gate, *sh_up; size_t rb;
@@ -897,13 +899,54 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int RBK = A.F / GU2_ROWS;
     const int sh = A.sh_gate ? 1 : 0, sh_tiles = sh ? (A.nt + TILE_TOK - 1) / TILE_TOK : 0;
-    // the masks, then the routing ids (read before any copy is in flight), in
-    // one memory round trip
     uint32_t em[QG_EXPERTS / 64];
-    if (wave == 0)
+    if (A.inline_route == 2) {
+        // the workgroup routes the batch itself (wave w: token w; the host
+        // takes this path for up to 8 tokens), every workgroup alike;
+        // workgroup 0 publishes ids, weights and flags.  The per-expert token masks and the routing scratch sit in
+        // the rings, which nothing writes before the list's barrier below.
+        static_assert(64 * GU3_W == QG_EXPERTS, "one mask per thread");
+        static_assert((QG_EXPERTS + 2 * QG_ROUTE_SCRATCH * GU3_W) * 4 <= GU3_RING_BYTES, "masks and scratch fit the rings");
+        uint32_t *s_em = (uint32_t *)s_dyn;
+        float *s_rv = (float *)s_dyn + QG_EXPERTS + 2 * QG_ROUTE_SCRATCH * wave;
+        int *s_ri = (int *)(s_rv + QG_ROUTE_SCRATCH);
+        s_em[tid] = 0u;
+        __syncthreads();
+        const bool pub = blockIdx.x == 0;
+        for (int t = wave; t < A.nt; t += GU3_W) {
+            int id, missing;
+            float wv = 0.0f;
+            double mass;
+            // only the ids unless this workgroup publishes or the flags need the mass
+            qg_route_fast(A.logits + (size_t)t * A.ld, lane, id, wv, s_rv, s_ri, pub || A.resident != nullptr);
+            const int flag = qg_route_cover(id, wv, A.resident, A.thr, missing, mass);
+            if (lane < QG_TOP) {
+                s_ids[t * QG_TOP + lane] = id;
+                if (flag < 2 && id >= 0 && id < QG_EXPERTS) atomicOr(&s_em[id], 1u << t);
+                if (pub) {
+                    A.ids[t * QG_TOP + lane] = id;
+                    A.w[t * QG_TOP + lane] = wv;
+                }
+            }
+            if (pub && lane == 0) {
+                A.pl->flag[t] = flag;
+                A.pl->missing[t] = missing;
+                A.pl->mass[t] = mass;
+                if (A.flags_out) A.flags_out[t] = (uint8_t)flag;
+            }
+        }
+        __syncthreads();
+        if (wave == 0)
 #pragma unroll
-        for (int i = 0; i < QG_EXPERTS / 64; i++) em[i] = A.pl->emask[64 * i + lane];
-    if (tid < A.nt * QG_TOP) s_ids[tid] = A.ids[tid];
+            for (int i = 0; i < QG_EXPERTS / 64; i++) em[i] = s_em[64 * i + lane];
+    } else {
+        // the masks, then the routing ids (read before any copy is in
+        // flight), in one memory round trip
+        if (wave == 0)
+#pragma unroll
+            for (int i = 0; i < QG_EXPERTS / 64; i++) em[i] = A.pl->emask[64 * i + lane];
+        if (tid < A.nt * QG_TOP) s_ids[tid] = A.ids[tid];
+    }
     if (wave == 0) {
         if (lane == 0 && sh) { s_xe[0] = -1; s_xk[0] = -1; s_xm[0] = sh_tiles; s_xt[0] = 0u; }
         const unsigned long long below = (1ULL << lane) - 1ULL;
@@ -1704,23 +1747,28 @@ int dec_forward(float *out, float *resid, int *ids, float *weights, unsigned cha
     // (fewer rows per CU, so more of the router's 4 MB in flight at once)
     const int ngr = (nt + 4) / 5, TPB = (nt + ngr - 1) / ngr, RW = TPB == 1 ? 1 : 4;
     const int row_blocks = QG_EXPERTS / (2 * RW) * ngr, plane_blocks = (nt + RW - 1) / RW;
+    // one token: every gate/up workgroup routes it; 2..8 tokens at D = 2048:
+    // every dec_gateup3_kernel workgroup routes the batch, a token per wave
+    // (a second token per wave costs the kernel more than the routing kernel
+    // takes); otherwise the routing kernel sets the plan's token masks,
+    // cleared by the router
+    const bool inl = nt <= INLINE_MAX, gu3r = !inl && D == 2048 && nt <= GU3_W, rk = !inl && !gu3r;
     RouterArgs R{x, nt, D, rows, L->router, sh ? L->sh_gate_inp : nullptr, logits, norm, 1e-6f, xn_out, xp, xsp, plane_blocks,
-                 L->router_bias, nt > INLINE_MAX ? pl->emask : nullptr};
+                 L->router_bias, rk ? pl->emask : nullptr};
     const dim3 rgrid(plane_blocks + row_blocks), rblock(64 * RW);
     const size_t rlds = (size_t)(TPB > 2 * RW ? TPB : 2 * RW) * D * 4;  // router blocks: the group's rows; plane blocks: two rows per wave
     if (D == 2048) router_launch<2048>(TPB, rgrid, rblock, rlds, s, R);
     else router_launch<2560>(TPB, rgrid, rblock, rlds, s, R);
     int rc = hipGetLastError();
     if (rc) return rc;
-    const bool inl = nt <= INLINE_MAX;
-    if (!inl) {
+    if (rk) {
         RouteArgs RA{nt, logits, rows, L->resident, L->threshold, ids, weights, flags, pl};
         dec_launch(1, dec_route_kernel, dim3(nt), dim3(64), 0, s, RA);
         if ((rc = hipGetLastError())) return rc;
     }
     _Float16 *midp = (_Float16 *)(ws + lay.midp);
     float *msum8 = (float *)(ws + lay.msum);
-    GuArgs G2{nt, D, F, inl ? 1 : 0, logits, rows, L->resident, L->threshold, ids, weights, flags, pl,
+    GuArgs G2{nt, D, F, inl ? 1 : gu3r ? 2 : 0, logits, rows, L->resident, L->threshold, ids, weights, flags, pl,
               (const uint8_t *)L->gate, (const uint8_t *)L->up, sh ? (const uint8_t *)L->sh_gate : nullptr,
               sh ? (const uint8_t *)L->sh_up : nullptr, qg_row_bytes_host(QT_Q4_K, D), xp, xsp, midp, msum8,
               L->down_type, sh ? L->sh_down_type : L->down_type, nullptr, nullptr};
