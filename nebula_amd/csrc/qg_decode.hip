@@ -903,8 +903,9 @@ __global__ __launch_bounds__(512, 1) void dec_gateup3_kernel(GuArgs A) {
     if (A.inline_route == 2) {
         // the workgroup routes the batch itself (wave w: token w; the host
         // takes this path for up to 8 tokens), every workgroup alike;
-        // workgroup 0 publishes ids, weights and flags.  The per-expert token masks and the routing scratch sit in
-        // the rings, which nothing writes before the list's barrier below.
+        // workgroup 0 publishes ids, weights and flags.  The per-expert token
+        // masks and the routing scratch sit in the rings, which nothing
+        // writes before the list's barrier below.
         static_assert(64 * GU3_W == QG_EXPERTS, "one mask per thread");
         static_assert((QG_EXPERTS + 2 * QG_ROUTE_SCRATCH * GU3_W) * 4 <= GU3_RING_BYTES, "masks and scratch fit the rings");
         uint32_t *s_em = (uint32_t *)s_dyn;
