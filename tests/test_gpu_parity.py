@@ -432,8 +432,8 @@ def test_layer_partial_residency_flags(layer1, nt):
     from 8 correlated contexts, one of them the batch's own.  The batch then
     mixes covered (flag 0), pruned (1) and handed-off (2) tokens: flags and
     pruning exact, every unflagged row (resident experts only, pruned weights
-    0) within tolerance of the oracle; 1 token runs the inline-routing
-    kernels, 4 and 17 the routing kernel."""
+    0) within tolerance of the oracle; 1 and 4 tokens are routed inside the
+    gate/up kernels, 17 by the routing kernel."""
     L, H = layer1
     xs = synth.ranking_inputs(77, 4242)
     dx = Device(xs)
