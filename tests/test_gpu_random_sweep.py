@@ -2,10 +2,11 @@
 
 Seeded random batch sizes and inputs (independent or correlated tokens) over
 the decode path (1..17 tokens, configs 0 and 1), config-1 layers with a
-ranked resident set (coverage flags, pruning, handoff rows) and the prefill
-path (18..3000 tokens, configs 0, 1 and the Zipf-routed config 3).  Each case
-holds the bars of the fixed-case tests: routing ids, weights and flags bit
-for bit, outputs within max-abs 1e-3 and rel-L2 1e-4.
+ranked resident set (coverage flags, pruning, handoff rows), the prefill path
+(18..3000 tokens, configs 0, 1 and the Zipf-routed config 3) and the
+reference's own 2560/640 shape at both.  Each case holds the bars of the
+fixed-case tests: routing ids, weights and flags bit for bit, outputs within
+max-abs 1e-3 and rel-L2 1e-4.
 """
 import numpy as np
 import pytest
@@ -83,3 +84,28 @@ def test_prefill_random_batches(layers):
         fw = P.forward(L, x)
         P.check_routing(fw, H, x)
         P.check_outputs(fw, L, H, x, P.sample_rows(nt, min(24, nt), seed), f"prefill {name} seed={seed} B={nt} corr={corr}")
+
+
+def test_reference_shape_random_batches(qgl):
+    """The reference's own shape, D = 2560 / F = 640 (IQ4_NL down, shared
+    expert with an IQ4_NL down): random decode and prefill batch sizes."""
+    from test_gpu_dropin import REF, fetcher, host_layer
+    L, H = synth.build_layer(REF), host_layer(REF)
+    D, Fd = REF.width, REF.ff
+    rng = np.random.default_rng(SEED + 3)
+    for i in range(10):
+        nt = int(rng.integers(1, 18)) if i < 7 else int(rng.integers(18, 700))
+        corr, seed = bool(rng.integers(0, 2)), 8000 + i
+        x = synth.inputs(seed, nt, D, correlated=corr)
+        fw = synth.Forward(D, Fd, nt)
+        fw.x.set(x)
+        say(f"forward 2560/640 seed={seed} B={nt} corr={corr}")
+        fw.run(L, nt)
+        call("sync")
+        ids, w = O.route(H.logits(x))
+        np.testing.assert_array_equal(fw.ids.get()[:nt], ids, err_msg=f"routing ids seed={seed} B={nt}")
+        np.testing.assert_array_equal(fw.w.get()[:nt].view('u4'), w.view('u4'), err_msg=f"routing weights seed={seed} B={nt}")
+        rows = np.arange(nt) if nt <= 40 else P.sample_rows(nt, 24, seed)
+        out, *_ = H.forward(x[rows], fetch=fetcher(L))
+        maxabs, rel = P.assert_close(fw.out.get()[rows], out, f"2560/640 seed={seed} B={nt}")
+        say(f"  2560/640 B={nt}: max-abs {maxabs:.2e} rel-L2 {rel:.2e}")
